@@ -1,0 +1,297 @@
+"""Benchmark: W4A16 GEMV effective HBM bandwidth on one MI355X (the headline metric).
+
+Workload (benchmark configuration 2): one Llama-70B-class layer's four M=1 decode projections,
+group size 128, symmetric int4 (zp = 8), bf16 activations and outputs:
+    qkv 10240x8192, o 8192x8192, gate_up 57344x8192, down 8192x28672.
+A "step" is one pass over the four GEMVs. Weights are random int4 codes (synthetic, seeded on the
+device), packed once into the reference packet layout. Each shape has R rotated weight copies
+whose total exceeds twice the 256 MiB Infinity Cache, and consecutive steps use different copies,
+so every launch streams its weights from HBM.
+
+Timing: the launches of R steps are captured once into a HIP graph (torch.cuda.CUDAGraph) and
+replayed; HIP events on the capture stream bracket the K timed steps. value = algorithmic bytes
+per step / time per step (int4 codes + fp16 scales + activations + outputs; the packets' fp16
+beta is read but not credited).
+
+Also reported: per-shape us/call and GB/s (each shape's own graph, events over >= 200 launches),
+a roofline object for the dominant kernel (gate_up), and the CPU oracle timed on the host cores
+on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO_ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO_ROOT / "fast-kernels_amd"))
+sys.path.insert(0, str(REPO_ROOT))
+
+PEAK_HBM_GBS = 8000.0
+INFINITY_CACHE_BYTES = 256 * 1024 * 1024
+
+WORKLOADS = {
+    # name: (activation dtype, group size, [(shape name, N, K)])
+    "llama70b_layer_m1_bf16": (
+        "bf16",
+        128,
+        [("qkv", 10240, 8192), ("o", 8192, 8192), ("gate_up", 57344, 8192), ("down", 8192, 28672)],
+    ),
+    "llama7b_layer_m1_fp16": (
+        "f16",
+        128,
+        [("qkv", 12288, 4096), ("o", 4096, 4096), ("gate_up", 22016, 4096), ("down", 4096, 11008)],
+    ),
+}
+
+
+def algorithmic_bytes(batch: int, n: int, k: int, g: int) -> int:
+    return n * k // 2 + n * (k // g) * 2 + batch * k * 2 + batch * n * 2
+
+
+def parse_args() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=1000)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--workload", choices=sorted(WORKLOADS), default="llama70b_layer_m1_bf16")
+    p.add_argument("--batch", type=int, default=1)
+    p.add_argument("--split-k", type=int, default=0, help="0 = built-in plan")
+    p.add_argument("--only", default="", help="comma list of shape names to run (profiling)")
+    p.add_argument("--per-shape-launches", type=int, default=300)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--eager", action="store_true", help="launch without a HIP graph")
+    return p.parse_args()
+
+
+class ShapeBuffers:
+    def __init__(self, torch, native, name, n, k, g, batch, act, rotations, split_k):
+        from fast_kernels.ops import arc_packet_stride_bytes
+
+        self.name, self.n, self.k, self.g, self.batch = name, n, k, g, batch
+        self.stride = arc_packet_stride_bytes(g)
+        self.act_code = 1 if act == "bf16" else 0
+        dtype = torch.bfloat16 if act == "bf16" else torch.float16
+        dev = torch.device("cuda")
+        gen = torch.Generator(device=dev)
+        gen.manual_seed((batch * 1_000_003 + n * 1009 + k * 101 + g) % (2**31 - 1))
+        self.packets = []
+        ng = k // g
+        for _ in range(rotations):
+            q = torch.randint(0, 256, (n, k // 2), device=dev, dtype=torch.uint8, generator=gen)
+            alpha = (0.001 + 0.019 * torch.rand((n, ng), device=dev, generator=gen)).to(torch.float16)
+            beta = -(alpha * 8)
+            pk = torch.empty(((n // 128) * ng, self.stride), device=dev, dtype=torch.uint8)
+            native.pack_arc_w4a16_packets(
+                q.data_ptr(), alpha.data_ptr(), beta.data_ptr(), pk.data_ptr(), n, k, g,
+                self.stride, torch.cuda.current_stream().cuda_stream,
+            )
+            self.packets.append(pk)
+            del q, alpha, beta
+        self.x = torch.randn((batch, k), device=dev, generator=gen).to(dtype)
+        self.out = torch.empty((batch, n), device=dev, dtype=dtype)
+        self.plan = dict(native.arc_w4a16_plan(batch, n, k, g, self.act_code, split_k, 0))
+        self.split_k = split_k
+        self.bytes = algorithmic_bytes(batch, n, k, g)
+
+    def launch(self, native, torch, ws, r):
+        native.arc_w4a16_forward_ex(
+            self.x.data_ptr(), self.packets[r % len(self.packets)].data_ptr(), self.out.data_ptr(),
+            ws.data_ptr(), ws.numel(), self.batch, self.n, self.k, self.g, self.stride,
+            self.act_code, self.split_k, torch.cuda.current_stream().cuda_stream,
+        )
+
+
+def rotations_for(total_packet_bytes: int) -> int:
+    return max(2, math.ceil(2 * INFINITY_CACHE_BYTES / max(1, total_packet_bytes)) + 1)
+
+
+def make_runner(torch, fn, launches_per_call: int, eager: bool):
+    """Returns run(times) that issues `times` x launches_per_call launches on the current stream."""
+    if eager:
+        def run(times):
+            for _ in range(times):
+                fn()
+        return run
+    graph = torch.cuda.CUDAGraph()
+    fn()  # warm (first call may size the workspace cache; nothing allocates under capture)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        fn()
+    torch.cuda.synchronize()
+
+    def run(times):
+        for _ in range(times):
+            graph.replay()
+    return run
+
+
+def time_events(torch, run, reps: int) -> float:
+    """Milliseconds for run(reps), by HIP events on the current stream."""
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    run(reps)
+    end.record()
+    end.synchronize()
+    return float(start.elapsed_time(end))
+
+
+def cpu_baseline(workload: str, batch: int, seconds: float) -> dict:
+    """The CPU oracle (C, OpenMP) on the same shapes, host-generated inputs, timed until at least
+    `seconds` of work (whole passes over the four shapes)."""
+    import numpy as np  # noqa: F401
+
+    from fast_kernels.benchmarking.inputs import make_case
+    from oracle import oracle
+
+    act, g, shapes = WORKLOADS[workload]
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    oracle.set_threads(threads)
+    cases = [make_case(batch, n, k, g, act=act) for _, n, k in shapes]
+    total_bytes = 0
+    t0 = time.perf_counter()
+    passes = 0
+    while True:
+        for c in cases:
+            oracle.gemv(c.x, c.q_u8, c.alpha, c.beta, g, act)
+            total_bytes += algorithmic_bytes(batch, c.n, c.k, g)
+        passes += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            break
+    return {
+        "value": round(total_bytes / elapsed / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{passes} full pass(es) over the {len(shapes)} {workload} GEMVs "
+        f"({elapsed:.1f} s, oracle/w4a16_oracle.c fko_gemv, OpenMP {threads} threads, "
+        f"fp64 accumulation)",
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU only: this build has no multi-GPU path (asked for "
+            f"--gpus {args.gpus}). Run with --gpus 1.",
+            file=sys.stderr,
+        )
+        return 2
+    import torch
+
+    from fast_kernels.native import native_module
+
+    native = native_module()
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    act, g, shapes = WORKLOADS[args.workload]
+    if args.only:
+        keep = set(args.only.split(","))
+        shapes = [s for s in shapes if s[0] in keep]
+
+    bufs = []
+    for name, n, k in shapes:
+        pk_bytes = (n // 128) * (k // g) * (128 * g // 2 + 512)
+        bufs.append(
+            ShapeBuffers(torch, native, name, n, k, g, args.batch, act, rotations_for(pk_bytes), args.split_k)
+        )
+    ws_bytes = max(max(b.plan["workspace_bytes"] for b in bufs), 1)
+    ws = torch.zeros(ws_bytes + 256, device="cuda", dtype=torch.uint8)
+    torch.cuda.synchronize()
+
+    # Per-shape timing: each shape's own graph over its R rotations.
+    per_shape = {}
+    for b in bufs:
+        R = len(b.packets)
+        run = make_runner(torch, lambda b=b: [b.launch(native, torch, ws, r) for r in range(R)], R, args.eager)
+        reps = max(1, args.per_shape_launches // R)
+        time_events(torch, run, max(1, 20 // R))
+        ms = time_events(torch, run, reps)
+        us = ms * 1e3 / (reps * R)
+        per_shape[b.name] = {
+            "n": b.n,
+            "k": b.k,
+            "us_per_call": round(us, 3),
+            "gbs": round(b.bytes / (us * 1e-6) / 1e9, 1),
+            "pct_peak": round(100.0 * b.bytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 1),
+            "bytes": b.bytes,
+            "rotations": R,
+            "split_k_slices": b.plan["split_k_slices"],
+            "workgroups": b.plan["workgroups"],
+        }
+
+    # Whole step: R_max steps captured, each step = all shapes with that step's rotation.
+    R_step = max(len(b.packets) for b in bufs)
+
+    def one_cycle():
+        for r in range(R_step):
+            for b in bufs:
+                b.launch(native, torch, ws, r)
+
+    run = make_runner(torch, one_cycle, R_step * len(bufs), args.eager)
+    cycles_warm = max(1, math.ceil(args.warmup / R_step))
+    cycles = max(1, math.ceil(args.steps / R_step))
+    time_events(torch, run, cycles_warm)
+    torch.cuda.synchronize()
+    ms = time_events(torch, run, cycles)
+    torch.cuda.synchronize()
+    steps = cycles * R_step
+    ms_per_step = ms / steps
+    step_bytes = sum(b.bytes for b in bufs)
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    dominant = max(bufs, key=lambda b: b.bytes)
+    dom = per_shape[dominant.name]
+    achieved = dom["gbs"]
+    result = {
+        "metric": "W4A16 GEMV effective HBM GB/s (% of MI355X peak) + us/call, M=1",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": cycles_warm * R_step,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": act if act == "bf16" else "fp16",
+        "data": "synthetic (seeded random int4 codes, fp16 scales U[0.001,0.02], zp=8, x~N(0,1))",
+        "config": {
+            "workload": args.workload,
+            "batch": args.batch,
+            "group_size": g,
+            "shapes": {b.name: [b.n, b.k] for b in bufs},
+            "step": "one pass over the listed GEMVs, launched from a HIP graph",
+            "cache_busting": "rotated weight copies > 2 x 256 MiB per shape",
+        },
+        "pct_peak": round(100.0 * value / PEAK_HBM_GBS, 1),
+        "per_shape": per_shape,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"w4a16_gemv_kernel ({dominant.name} {dominant.n}x{dominant.k})",
+            "achieved": achieved,
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(args.workload, args.batch, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

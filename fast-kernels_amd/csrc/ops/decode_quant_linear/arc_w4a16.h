@@ -1,0 +1,94 @@
+// C++ op API of the W4A16 decode linear ("ARC") family.
+//
+// The first eleven declarations keep the names, argument order and meaning of the reference op
+// header (csrc/ops/decode_quant_linear/arc_w4a16.h:8-52): device buffers as std::uintptr_t,
+// dimensions as int, the HIP stream last. Errors are thrown as std::invalid_argument (bad
+// arguments, checked before any device call) or std::runtime_error (HIP / hipBLASLt failures),
+// as in the reference (arc_w4a16.cu:23-85). The three vendor-baseline functions keep the
+// reference's cublaslt_* names for drop-in callers and are served by hipBLASLt.
+//
+// The declarations after them are additions for MI355X callers: bf16 activations, an explicit
+// caller-owned workspace and split-K choice, and a workspace-size query.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+namespace fast_kernels::decode_quant_linear {
+
+void pack_arc_w4a16_packets(std::uintptr_t q_ptr, std::uintptr_t alpha_ptr, std::uintptr_t beta_ptr,
+                            std::uintptr_t packets_ptr, int n, int k, int group_size,
+                            int packet_stride_bytes, std::uintptr_t stream_ptr);
+
+void compute_arc_w4a16_group_sums(std::uintptr_t activations_ptr, std::uintptr_t sums_ptr,
+                                  int batch, int k, int group_size, std::uintptr_t stream_ptr);
+
+void arc_w4a16_forward(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
+                       std::uintptr_t group_sums_ptr, std::uintptr_t output_ptr, int batch, int n,
+                       int k, int group_size, int packet_stride_bytes, std::uintptr_t stream_ptr);
+
+void arc_w4a16_forward_split_k(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
+                               std::uintptr_t group_sums_ptr, std::uintptr_t partials_ptr,
+                               int batch, int n, int k, int group_size, int packet_stride_bytes,
+                               int split_k_slices, std::uintptr_t stream_ptr);
+
+void reduce_arc_w4a16_split_k_partials(std::uintptr_t partials_ptr, std::uintptr_t output_ptr,
+                                       int batch, int n, int split_k_slices,
+                                       std::uintptr_t stream_ptr);
+
+void dequant_w4a16_to_fp16(std::uintptr_t q_ptr, std::uintptr_t alpha_ptr, std::uintptr_t beta_ptr,
+                           std::uintptr_t output_ptr, int n, int k, int group_size,
+                           std::uintptr_t stream_ptr);
+
+void dequant_arc_w4a16_packets_to_fp16(std::uintptr_t packets_ptr, std::uintptr_t output_ptr, int n,
+                                       int k, int group_size, int packet_stride_bytes,
+                                       std::uintptr_t stream_ptr);
+
+void cublaslt_fp16_with_weight(std::uintptr_t activations_ptr, std::uintptr_t weight_ptr,
+                               std::uintptr_t output_ptr, std::uintptr_t workspace_ptr,
+                               std::size_t workspace_bytes, int batch, int n, int k,
+                               std::uintptr_t stream_ptr);
+
+void cublaslt_fp16_after_packet_dequant(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
+                                        std::uintptr_t output_ptr, std::uintptr_t weight_ptr,
+                                        std::uintptr_t workspace_ptr, std::size_t workspace_bytes,
+                                        int batch, int n, int k, int group_size,
+                                        int packet_stride_bytes, std::uintptr_t stream_ptr);
+
+void cublaslt_fp16_after_dequant(std::uintptr_t activations_ptr, std::uintptr_t q_ptr,
+                                 std::uintptr_t alpha_ptr, std::uintptr_t beta_ptr,
+                                 std::uintptr_t output_ptr, std::uintptr_t weight_ptr,
+                                 std::uintptr_t workspace_ptr, std::size_t workspace_bytes,
+                                 int batch, int n, int k, int group_size,
+                                 std::uintptr_t stream_ptr);
+
+// ---- additions (no reference counterpart) -------------------------------------------------
+
+enum ActivationDtype : int { kActivationF16 = 0, kActivationBF16 = 1 };
+
+struct ArcW4A16Plan {
+  int m_tile;
+  int split_k_slices;   // 1 = one workgroup covers all of K
+  int groups_per_slice;
+  int workgroups;
+  std::size_t workspace_bytes;  // caller workspace needed by arc_w4a16_forward_ex
+};
+
+// The launch the GEMV will use for this shape on the current device. split_k_slices = 0 picks
+// the built-in policy.
+ArcW4A16Plan plan_arc_w4a16(int batch, int n, int k, int group_size, int activation_dtype,
+                            int split_k_slices);
+// The same policy for a given CU count, with no device query (host-only, testable without a GPU).
+ArcW4A16Plan plan_arc_w4a16_for_cu_count(int batch, int n, int k, int group_size,
+                                         int activation_dtype, int split_k_slices, int cu_count);
+
+// Packet GEMV with fp16 or bf16 activations (output in the same dtype), one launch, no group-sum
+// prepass. workspace must be at least plan.workspace_bytes and zero-filled before its first use;
+// every call leaves it zero-filled again. Calls that share a workspace must be stream-ordered.
+void arc_w4a16_forward_ex(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
+                          std::uintptr_t output_ptr, std::uintptr_t workspace_ptr,
+                          std::size_t workspace_bytes, int batch, int n, int k, int group_size,
+                          int packet_stride_bytes, int activation_dtype, int split_k_slices,
+                          std::uintptr_t stream_ptr);
+
+}  // namespace fast_kernels::decode_quant_linear

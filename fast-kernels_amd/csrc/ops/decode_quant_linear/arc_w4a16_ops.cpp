@@ -1,0 +1,524 @@
+// Validation, launch policy and vendor baseline behind the ARC W4A16 op API (arc_w4a16.h).
+//
+// Validation rules and error classes follow the reference (arc_w4a16.cu:23-85, 649-828):
+// group_size in {64,128}; batch, k > 0; k % group_size == 0; n > 0 and n % 128 == 0;
+// packet_stride_bytes == 128*G/2 + 512; 1 < split_k_slices <= K/G for the split-K entry point.
+// Every check runs before any device call. HIP errors are checked after every launch.
+#include "ops/decode_quant_linear/arc_w4a16.h"
+
+#include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
+
+#include <algorithm>
+#include <array>
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+#include <sstream>
+#include <stdexcept>
+#include <string>
+
+#include "kernels/decode_quant_linear/w4a16_aux.h"
+#include "kernels/decode_quant_linear/w4a16_gemv.h"
+
+namespace fast_kernels::decode_quant_linear {
+namespace {
+
+constexpr int kTileCols = fk::kTileCols;
+constexpr int kMaxDevices = 64;
+constexpr std::size_t kCounterRegionAlign = 256;
+// Split-K workspace layout: a fixed counter region (one uint32 per (tile, m-tile)) followed by
+// the fp32 partials. Fixing the region's size keeps every shape's counters clear of any other
+// shape's partials, so one zero-filled workspace serves calls of different shapes.
+constexpr std::size_t kMaxFixupCounters = 16384;
+constexpr std::size_t kCounterRegionBytes = kMaxFixupCounters * sizeof(std::uint32_t);
+
+[[noreturn]] void throw_invalid(const std::string& message) { throw std::invalid_argument(message); }
+
+void check_hip(hipError_t status, const char* what) {
+  if (status != hipSuccess) {
+    std::ostringstream oss;
+    oss << what << " failed: " << hipGetErrorString(status);
+    throw std::runtime_error(oss.str());
+  }
+}
+
+void validate_group_size_and_k(int batch, int k, int group_size) {
+  if (batch <= 0 || k <= 0) {
+    throw_invalid("batch and k must be positive");
+  }
+  if (group_size != 64 && group_size != 128) {
+    throw_invalid("group_size must be 64 or 128");
+  }
+  if (k % group_size != 0) {
+    throw_invalid("k must be divisible by group_size");
+  }
+}
+
+void validate_dimensions(int batch, int n, int k, int group_size) {
+  validate_group_size_and_k(batch, k, group_size);
+  if (n <= 0) {
+    throw_invalid("n must be positive");
+  }
+  if (n % kTileCols != 0) {
+    throw_invalid("n must be a multiple of 128");
+  }
+}
+
+void validate_packet_stride(int group_size, int packet_stride_bytes) {
+  const int expected = fk::packet_stride_bytes(group_size);
+  if (packet_stride_bytes != expected) {
+    std::ostringstream oss;
+    oss << "packet_stride_bytes=" << packet_stride_bytes << " does not match expected " << expected;
+    throw_invalid(oss.str());
+  }
+}
+
+void validate_pointer(std::uintptr_t ptr, std::size_t alignment, const char* name) {
+  if (ptr == 0) {
+    throw_invalid(std::string(name) + " must not be null");
+  }
+  if (ptr % alignment != 0) {
+    std::ostringstream oss;
+    oss << name << " must be " << alignment << "-byte aligned";
+    throw_invalid(oss.str());
+  }
+}
+
+void validate_activation_dtype(int activation_dtype) {
+  if (activation_dtype != kActivationF16 && activation_dtype != kActivationBF16) {
+    throw_invalid("activation_dtype must be 0 (fp16) or 1 (bf16)");
+  }
+}
+
+// CU count per device, read once (the reference queries device properties on every call,
+// arc_w4a16.cu:512-518).
+int device_cu_count() {
+  static std::array<int, kMaxDevices> cache{};
+  static std::mutex mutex;
+  int device = 0;
+  check_hip(hipGetDevice(&device), "hipGetDevice");
+  if (device < 0 || device >= kMaxDevices) {
+    throw std::runtime_error("device index out of range");
+  }
+  std::lock_guard<std::mutex> lock(mutex);
+  if (cache[device] == 0) {
+    int count = 0;
+    check_hip(hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device),
+              "hipDeviceGetAttribute(multiProcessorCount)");
+    cache[device] = std::max(count, 1);
+  }
+  return cache[device];
+}
+
+
+std::size_t fixup_workspace_bytes(int batch, int n, int m_tile, int splits) {
+  if (splits <= 1) {
+    return 0;
+  }
+  const std::size_t partials = fk::gemv_fixup_partial_floats(n, batch, m_tile, splits) * sizeof(float);
+  return kCounterRegionBytes + partials;
+}
+
+}  // namespace
+
+ArcW4A16Plan plan_arc_w4a16_for_cu_count(int batch, int n, int k, int group_size,
+                                         int activation_dtype, int split_k_slices, int cu_count) {
+  validate_dimensions(batch, n, k, group_size);
+  validate_activation_dtype(activation_dtype);
+  if (split_k_slices < 0) {
+    throw_invalid("split_k_slices must be >= 0 (0 = automatic)");
+  }
+  if (cu_count <= 0) {
+    throw_invalid("cu_count must be positive");
+  }
+  ArcW4A16Plan plan{};
+  plan.m_tile = fk::gemv_m_tile_for_batch(batch);
+  if (activation_dtype == kActivationBF16) {
+    plan.m_tile = std::min(plan.m_tile, 4);  // the bf16 unpack needs more registers per row
+  }
+  const int num_groups = k / group_size;
+  const int tiles = n / kTileCols;
+  const int mtiles = (batch + plan.m_tile - 1) / plan.m_tile;
+  const int base = tiles * mtiles;
+  int splits = 1;
+  if (split_k_slices > 0) {
+    splits = std::min(split_k_slices, num_groups);
+  } else {
+    // Aim for about four 4-wave workgroups per CU, with at least one group per wave; round the
+    // groups per workgroup to a multiple of the wave count so no wave idles inside a slice.
+    const int target = 4 * cu_count;
+    splits = (target + base - 1) / base;
+    splits = std::max(1, std::min(splits, std::max(1, num_groups / 4)));
+  }
+  int gps = (num_groups + splits - 1) / splits;
+  if (split_k_slices <= 0 && num_groups >= 4) {
+    gps = std::min(num_groups, (gps + 3) / 4 * 4);
+  }
+  splits = (num_groups + gps - 1) / gps;
+  if (splits > 1 && fk::gemv_fixup_counters(n, batch, plan.m_tile) > kMaxFixupCounters) {
+    throw_invalid("n * ceil(batch / m_tile) / 128 exceeds the split-K counter capacity (16384)");
+  }
+  plan.split_k_slices = splits;
+  plan.groups_per_slice = gps;
+  plan.workgroups = base * splits;
+  plan.workspace_bytes = fixup_workspace_bytes(batch, n, plan.m_tile, splits);
+  return plan;
+}
+
+namespace {
+
+// Library-owned fix-up workspace per device for the reference-signature forward, which has no
+// workspace argument. Grown on demand (so the first call for a larger shape allocates and must not
+// run under stream capture); the counter region is zeroed once, stream-ordered, at allocation and
+// the kernel leaves it zeroed. Calls on one device that run concurrently on different streams share
+// it and must not overlap (the reference's cached group_sums buffer has the same restriction,
+// decode_quant_linear.py:150-168).
+struct DeviceWorkspace {
+  void* ptr = nullptr;
+  std::size_t bytes = 0;
+};
+
+void* library_workspace(std::size_t bytes, hipStream_t stream) {
+  static std::array<DeviceWorkspace, kMaxDevices> spaces{};
+  static std::mutex mutex;
+  int device = 0;
+  check_hip(hipGetDevice(&device), "hipGetDevice");
+  std::lock_guard<std::mutex> lock(mutex);
+  DeviceWorkspace& ws = spaces[device];
+  if (ws.bytes < bytes) {
+    if (ws.ptr != nullptr) {
+      check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+      check_hip(hipFree(ws.ptr), "hipFree");
+      ws.ptr = nullptr;
+      ws.bytes = 0;
+    }
+    const std::size_t grown = std::max<std::size_t>(bytes, 1u << 20);
+    check_hip(hipMalloc(&ws.ptr, grown), "hipMalloc(workspace)");
+    check_hip(hipMemsetAsync(ws.ptr, 0, grown, stream), "hipMemsetAsync(workspace)");
+    ws.bytes = grown;
+  }
+  return ws.ptr;
+}
+
+void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::uintptr_t output_ptr,
+              void* workspace, const ArcW4A16Plan& plan, int batch, int n, int k, int group_size,
+              int activation_dtype, hipStream_t stream) {
+  fk::GemvLaunch l;
+  l.x = reinterpret_cast<const void*>(activations_ptr);
+  l.packets = reinterpret_cast<const void*>(packets_ptr);
+  l.out = reinterpret_cast<void*>(output_ptr);
+  l.M = batch;
+  l.N = n;
+  l.K = k;
+  l.group_size = group_size;
+  l.act = activation_dtype == kActivationBF16 ? fk::Act::kBF16 : fk::Act::kF16;
+  l.m_tile = plan.m_tile;
+  l.splits = plan.split_k_slices;
+  l.gps = plan.groups_per_slice;
+  if (plan.split_k_slices > 1) {
+    l.mode = fk::GemvMode::kFixup;
+    l.counters = workspace;
+    l.partials = static_cast<char*>(workspace) + kCounterRegionBytes;
+  } else {
+    l.mode = fk::GemvMode::kDirect;
+  }
+  check_hip(fk::launch_w4a16_gemv(l, stream), "w4a16_gemv launch");
+}
+
+void validate_forward_buffers(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
+                              std::uintptr_t output_ptr) {
+  validate_pointer(activations_ptr, 16, "activations");
+  validate_pointer(packets_ptr, 16, "packets");
+  validate_pointer(output_ptr, 2, "output");
+}
+
+// ---- vendor baseline: dequantised fp16 weight x hipBLASLt --------------------------------
+
+void check_blas(hipblasStatus_t status, const char* what) {
+  if (status != HIPBLAS_STATUS_SUCCESS) {
+    std::ostringstream oss;
+    oss << what << " failed with hipblasStatus " << static_cast<int>(status);
+    throw std::runtime_error(oss.str());
+  }
+}
+
+hipblasLtHandle_t blaslt_handle() {
+  static std::array<hipblasLtHandle_t, kMaxDevices> handles{};
+  static std::mutex mutex;
+  int device = 0;
+  check_hip(hipGetDevice(&device), "hipGetDevice");
+  std::lock_guard<std::mutex> lock(mutex);
+  if (handles[device] == nullptr) {
+    check_blas(hipblasLtCreate(&handles[device]), "hipblasLtCreate");
+  }
+  return handles[device];
+}
+
+// Y[M,N] = X[M,K] W[N,K]^T, row-major fp16, fp32 compute. hipBLASLt is column-major, so this is
+// issued as Y^T[N,M] = W^T(op T on the [K,N] column-major view of W) x X^T.
+void run_blaslt_matmul(const void* activations, const void* weight, void* output, void* workspace,
+                       std::size_t workspace_bytes, int batch, int n, int k, hipStream_t stream) {
+  hipblasLtHandle_t handle = blaslt_handle();
+  hipblasLtMatmulDesc_t op = nullptr;
+  hipblasLtMatrixLayout_t a_desc = nullptr, b_desc = nullptr, c_desc = nullptr;
+  hipblasLtMatmulPreference_t pref = nullptr;
+  struct Cleanup {
+    hipblasLtMatmulDesc_t& op;
+    hipblasLtMatrixLayout_t& a;
+    hipblasLtMatrixLayout_t& b;
+    hipblasLtMatrixLayout_t& c;
+    hipblasLtMatmulPreference_t& p;
+    ~Cleanup() {
+      if (p) hipblasLtMatmulPreferenceDestroy(p);
+      if (c) hipblasLtMatrixLayoutDestroy(c);
+      if (b) hipblasLtMatrixLayoutDestroy(b);
+      if (a) hipblasLtMatrixLayoutDestroy(a);
+      if (op) hipblasLtMatmulDescDestroy(op);
+    }
+  } cleanup{op, a_desc, b_desc, c_desc, pref};
+
+  const hipblasOperation_t trans_a = HIPBLAS_OP_T;
+  const hipblasOperation_t trans_b = HIPBLAS_OP_N;
+  check_blas(hipblasLtMatmulDescCreate(&op, HIPBLAS_COMPUTE_32F, HIP_R_32F), "hipblasLtMatmulDescCreate");
+  check_blas(hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSA, &trans_a, sizeof(trans_a)),
+             "set TRANSA");
+  check_blas(hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSB, &trans_b, sizeof(trans_b)),
+             "set TRANSB");
+  check_blas(hipblasLtMatrixLayoutCreate(&a_desc, HIP_R_16F, k, n, k), "layout A");
+  check_blas(hipblasLtMatrixLayoutCreate(&b_desc, HIP_R_16F, k, batch, k), "layout B");
+  check_blas(hipblasLtMatrixLayoutCreate(&c_desc, HIP_R_16F, n, batch, n), "layout C");
+  check_blas(hipblasLtMatmulPreferenceCreate(&pref), "hipblasLtMatmulPreferenceCreate");
+  std::uint64_t ws_bytes = workspace == nullptr ? 0 : workspace_bytes;
+  check_blas(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
+                                                   &ws_bytes, sizeof(ws_bytes)),
+             "set max workspace");
+  hipblasLtMatmulHeuristicResult_t heuristic{};
+  int returned = 0;
+  check_blas(hipblasLtMatmulAlgoGetHeuristic(handle, op, a_desc, b_desc, c_desc, c_desc, pref, 1,
+                                             &heuristic, &returned),
+             "hipblasLtMatmulAlgoGetHeuristic");
+  if (returned == 0 && ws_bytes != 0) {
+    ws_bytes = 0;
+    workspace = nullptr;
+    check_blas(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
+                                                     &ws_bytes, sizeof(ws_bytes)),
+               "set max workspace");
+    check_blas(hipblasLtMatmulAlgoGetHeuristic(handle, op, a_desc, b_desc, c_desc, c_desc, pref, 1,
+                                               &heuristic, &returned),
+               "hipblasLtMatmulAlgoGetHeuristic");
+  }
+  if (returned == 0) {
+    throw std::runtime_error("hipblasLtMatmulAlgoGetHeuristic returned no usable algorithm");
+  }
+  const float alpha = 1.0f;
+  const float beta = 0.0f;
+  check_blas(hipblasLtMatmul(handle, op, &alpha, weight, a_desc, activations, b_desc, &beta, output,
+                             c_desc, output, c_desc, &heuristic.algo, workspace,
+                             static_cast<std::size_t>(ws_bytes), stream),
+             "hipblasLtMatmul");
+}
+
+}  // namespace
+
+void pack_arc_w4a16_packets(std::uintptr_t q_ptr, std::uintptr_t alpha_ptr, std::uintptr_t beta_ptr,
+                            std::uintptr_t packets_ptr, int n, int k, int group_size,
+                            int packet_stride_bytes, std::uintptr_t stream_ptr) {
+  validate_dimensions(1, n, k, group_size);
+  validate_packet_stride(group_size, packet_stride_bytes);
+  validate_pointer(q_ptr, 16, "q");
+  validate_pointer(alpha_ptr, 2, "alpha");
+  validate_pointer(beta_ptr, 2, "beta");
+  validate_pointer(packets_ptr, 16, "packets");
+  check_hip(fk::launch_pack_packets(reinterpret_cast<const void*>(q_ptr),
+                                    reinterpret_cast<const void*>(alpha_ptr),
+                                    reinterpret_cast<const void*>(beta_ptr),
+                                    reinterpret_cast<void*>(packets_ptr), n, k, group_size,
+                                    reinterpret_cast<hipStream_t>(stream_ptr)),
+            "pack_packets launch");
+}
+
+void compute_arc_w4a16_group_sums(std::uintptr_t activations_ptr, std::uintptr_t sums_ptr,
+                                  int batch, int k, int group_size, std::uintptr_t stream_ptr) {
+  validate_group_size_and_k(batch, k, group_size);
+  validate_pointer(activations_ptr, 4, "activations");
+  validate_pointer(sums_ptr, 4, "sums");
+  check_hip(fk::launch_group_sums(reinterpret_cast<const void*>(activations_ptr),
+                                  reinterpret_cast<void*>(sums_ptr), batch, k, group_size,
+                                  reinterpret_cast<hipStream_t>(stream_ptr)),
+            "group_sums launch");
+}
+
+// group_sums_ptr is accepted for signature compatibility and not read: the kernel derives the
+// per-group activation sums it needs from the activations themselves, in the same launch.
+void arc_w4a16_forward(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
+                       std::uintptr_t group_sums_ptr, std::uintptr_t output_ptr, int batch, int n,
+                       int k, int group_size, int packet_stride_bytes, std::uintptr_t stream_ptr) {
+  (void)group_sums_ptr;
+  validate_dimensions(batch, n, k, group_size);
+  validate_packet_stride(group_size, packet_stride_bytes);
+  validate_forward_buffers(activations_ptr, packets_ptr, output_ptr);
+  const auto stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  const ArcW4A16Plan plan =
+      plan_arc_w4a16_for_cu_count(batch, n, k, group_size, kActivationF16, 0, device_cu_count());
+  void* workspace = plan.workspace_bytes > 0 ? library_workspace(plan.workspace_bytes, stream) : nullptr;
+  run_gemv(activations_ptr, packets_ptr, output_ptr, workspace, plan, batch, n, k, group_size,
+           kActivationF16, stream);
+}
+
+void arc_w4a16_forward_split_k(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
+                               std::uintptr_t group_sums_ptr, std::uintptr_t partials_ptr,
+                               int batch, int n, int k, int group_size, int packet_stride_bytes,
+                               int split_k_slices, std::uintptr_t stream_ptr) {
+  (void)group_sums_ptr;
+  validate_dimensions(batch, n, k, group_size);
+  validate_packet_stride(group_size, packet_stride_bytes);
+  if (split_k_slices <= 1) {
+    throw_invalid("split_k_slices must be greater than 1");
+  }
+  const int num_groups = k / group_size;
+  if (split_k_slices > num_groups) {
+    throw_invalid("split_k_slices must not exceed the number of groups");
+  }
+  validate_pointer(activations_ptr, 16, "activations");
+  validate_pointer(packets_ptr, 16, "packets");
+  validate_pointer(partials_ptr, 4, "partials");
+  // Slice z covers groups [z*gps, (z+1)*gps) with gps = ceil(NG / S), as in the reference
+  // (arc_w4a16.cu:341-386, 463). A slice past the end writes zeros instead of leaving its
+  // partials unwritten.
+  fk::GemvLaunch l;
+  l.x = reinterpret_cast<const void*>(activations_ptr);
+  l.packets = reinterpret_cast<const void*>(packets_ptr);
+  l.partials = reinterpret_cast<void*>(partials_ptr);
+  l.M = batch;
+  l.N = n;
+  l.K = k;
+  l.group_size = group_size;
+  l.act = fk::Act::kF16;
+  l.mode = fk::GemvMode::kPartials;
+  l.m_tile = fk::gemv_m_tile_for_batch(batch);
+  l.splits = split_k_slices;
+  l.gps = (num_groups + split_k_slices - 1) / split_k_slices;
+  check_hip(fk::launch_w4a16_gemv(l, reinterpret_cast<hipStream_t>(stream_ptr)),
+            "w4a16_gemv split-K launch");
+}
+
+void reduce_arc_w4a16_split_k_partials(std::uintptr_t partials_ptr, std::uintptr_t output_ptr,
+                                       int batch, int n, int split_k_slices,
+                                       std::uintptr_t stream_ptr) {
+  if (batch <= 0 || n <= 0 || split_k_slices <= 1) {
+    throw_invalid("batch, n, and split_k_slices must be positive with split_k_slices > 1");
+  }
+  validate_pointer(partials_ptr, 4, "partials");
+  validate_pointer(output_ptr, 2, "output");
+  check_hip(fk::launch_reduce_partials(reinterpret_cast<const void*>(partials_ptr),
+                                       reinterpret_cast<void*>(output_ptr), batch, n,
+                                       split_k_slices, reinterpret_cast<hipStream_t>(stream_ptr)),
+            "reduce_partials launch");
+}
+
+void dequant_w4a16_to_fp16(std::uintptr_t q_ptr, std::uintptr_t alpha_ptr, std::uintptr_t beta_ptr,
+                           std::uintptr_t output_ptr, int n, int k, int group_size,
+                           std::uintptr_t stream_ptr) {
+  validate_dimensions(1, n, k, group_size);
+  validate_pointer(q_ptr, 4, "q");
+  validate_pointer(alpha_ptr, 2, "alpha");
+  validate_pointer(beta_ptr, 2, "beta");
+  validate_pointer(output_ptr, 16, "output");
+  check_hip(fk::launch_dequant(reinterpret_cast<const void*>(q_ptr),
+                               reinterpret_cast<const void*>(alpha_ptr),
+                               reinterpret_cast<const void*>(beta_ptr),
+                               reinterpret_cast<void*>(output_ptr), n, k, group_size,
+                               reinterpret_cast<hipStream_t>(stream_ptr)),
+            "dequant launch");
+}
+
+void dequant_arc_w4a16_packets_to_fp16(std::uintptr_t packets_ptr, std::uintptr_t output_ptr, int n,
+                                       int k, int group_size, int packet_stride_bytes,
+                                       std::uintptr_t stream_ptr) {
+  validate_dimensions(1, n, k, group_size);
+  validate_packet_stride(group_size, packet_stride_bytes);
+  validate_pointer(packets_ptr, 16, "packets");
+  validate_pointer(output_ptr, 16, "output");
+  check_hip(fk::launch_dequant_packets(reinterpret_cast<const void*>(packets_ptr),
+                                       reinterpret_cast<void*>(output_ptr), n, k, group_size,
+                                       reinterpret_cast<hipStream_t>(stream_ptr)),
+            "dequant_packets launch");
+}
+
+void cublaslt_fp16_with_weight(std::uintptr_t activations_ptr, std::uintptr_t weight_ptr,
+                               std::uintptr_t output_ptr, std::uintptr_t workspace_ptr,
+                               std::size_t workspace_bytes, int batch, int n, int k,
+                               std::uintptr_t stream_ptr) {
+  if (batch <= 0 || n <= 0 || k <= 0) {
+    throw_invalid("batch, n, and k must be positive");
+  }
+  validate_pointer(activations_ptr, 2, "activations");
+  validate_pointer(weight_ptr, 2, "weight");
+  validate_pointer(output_ptr, 2, "output");
+  run_blaslt_matmul(reinterpret_cast<const void*>(activations_ptr),
+                    reinterpret_cast<const void*>(weight_ptr), reinterpret_cast<void*>(output_ptr),
+                    reinterpret_cast<void*>(workspace_ptr), workspace_bytes, batch, n, k,
+                    reinterpret_cast<hipStream_t>(stream_ptr));
+}
+
+void cublaslt_fp16_after_packet_dequant(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
+                                        std::uintptr_t output_ptr, std::uintptr_t weight_ptr,
+                                        std::uintptr_t workspace_ptr, std::size_t workspace_bytes,
+                                        int batch, int n, int k, int group_size,
+                                        int packet_stride_bytes, std::uintptr_t stream_ptr) {
+  validate_dimensions(batch, n, k, group_size);
+  validate_packet_stride(group_size, packet_stride_bytes);
+  dequant_arc_w4a16_packets_to_fp16(packets_ptr, weight_ptr, n, k, group_size, packet_stride_bytes,
+                                    stream_ptr);
+  cublaslt_fp16_with_weight(activations_ptr, weight_ptr, output_ptr, workspace_ptr, workspace_bytes,
+                            batch, n, k, stream_ptr);
+}
+
+void cublaslt_fp16_after_dequant(std::uintptr_t activations_ptr, std::uintptr_t q_ptr,
+                                 std::uintptr_t alpha_ptr, std::uintptr_t beta_ptr,
+                                 std::uintptr_t output_ptr, std::uintptr_t weight_ptr,
+                                 std::uintptr_t workspace_ptr, std::size_t workspace_bytes,
+                                 int batch, int n, int k, int group_size,
+                                 std::uintptr_t stream_ptr) {
+  validate_dimensions(batch, n, k, group_size);
+  dequant_w4a16_to_fp16(q_ptr, alpha_ptr, beta_ptr, weight_ptr, n, k, group_size, stream_ptr);
+  cublaslt_fp16_with_weight(activations_ptr, weight_ptr, output_ptr, workspace_ptr, workspace_bytes,
+                            batch, n, k, stream_ptr);
+}
+
+ArcW4A16Plan plan_arc_w4a16(int batch, int n, int k, int group_size, int activation_dtype,
+                            int split_k_slices) {
+  validate_dimensions(batch, n, k, group_size);
+  return plan_arc_w4a16_for_cu_count(batch, n, k, group_size, activation_dtype, split_k_slices,
+                                     device_cu_count());
+}
+
+void arc_w4a16_forward_ex(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
+                          std::uintptr_t output_ptr, std::uintptr_t workspace_ptr,
+                          std::size_t workspace_bytes, int batch, int n, int k, int group_size,
+                          int packet_stride_bytes, int activation_dtype, int split_k_slices,
+                          std::uintptr_t stream_ptr) {
+  validate_dimensions(batch, n, k, group_size);
+  validate_packet_stride(group_size, packet_stride_bytes);
+  validate_activation_dtype(activation_dtype);
+  validate_forward_buffers(activations_ptr, packets_ptr, output_ptr);
+  if (split_k_slices < 0) {
+    throw_invalid("split_k_slices must be >= 0 (0 = automatic)");
+  }
+  const ArcW4A16Plan plan = plan_arc_w4a16_for_cu_count(batch, n, k, group_size, activation_dtype,
+                                                        split_k_slices, device_cu_count());
+  if (plan.workspace_bytes > 0) {
+    validate_pointer(workspace_ptr, kCounterRegionAlign, "workspace");
+    if (workspace_bytes < plan.workspace_bytes) {
+      std::ostringstream oss;
+      oss << "workspace_bytes=" << workspace_bytes << " is smaller than the " << plan.workspace_bytes
+          << " bytes this launch needs";
+      throw_invalid(oss.str());
+    }
+  }
+  run_gemv(activations_ptr, packets_ptr, output_ptr, reinterpret_cast<void*>(workspace_ptr), plan,
+           batch, n, k, group_size, activation_dtype, reinterpret_cast<hipStream_t>(stream_ptr));
+}
+
+}  // namespace fast_kernels::decode_quant_linear

@@ -1,0 +1,129 @@
+/*
+ * fk_w4a16.h - C ABI of the MI355X (gfx950) W4A16 decode-linear library, libfk_w4a16.so.
+ *
+ * Drop-in boundary for the reference's ARC W4A16 path. Each fk_* function below replaces the
+ * reference C++ op of the same name (minus the fk_ prefix) declared in
+ * csrc/ops/decode_quant_linear/arc_w4a16.h:8-52 and implemented in
+ * csrc/kernels/decode_quant_linear/arc_w4a16.cu:649-828; the pybind11 module
+ * csrc/bindings/python_module.cpp:119-240 binds them under the same names. Argument order and
+ * meaning are unchanged. Differences at the ABI level only:
+ *   - device buffers are plain pointers (the reference passes std::uintptr_t), the HIP stream is a
+ *     hipStream_t passed as void* (0/NULL = the null stream);
+ *   - C++ exceptions become return codes: FK_OK, FK_ERR_INVALID_ARGUMENT (reference:
+ *     std::invalid_argument, raised before any device work) or FK_ERR_RUNTIME (reference:
+ *     std::runtime_error from CUDA / cuBLASLt); fk_last_error() returns the message of the last
+ *     failure on the calling thread.
+ *
+ * Layouts (all row-major, little-endian):
+ *   q_u8     uint8 [N, K/2]   byte b of row n holds code k=2b in bits 0-3, k=2b+1 in bits 4-7
+ *   alpha    fp16  [N, K/G]   per-group scale;  beta fp16 [N, K/G] per-group offset
+ *            weight value W[n,k] = alpha[n,k/G] * q[n,k] + beta[n,k/G]
+ *   packets  uint8 [(N/128)*(K/G), 128*G/2 + 512]; packet (tile t, group g) is row t*(K/G)+g:
+ *            code word w (codes 8w..8w+7 of the group) of column c at byte (w*128 + c)*4, then
+ *            alpha[128], then beta[128] (fp16)
+ *   activations [M, K] fp16 (bf16 where stated), output [M, N] in the activation dtype
+ * All launches are asynchronous on the given stream; nothing synchronises the host.
+ */
+#ifndef FK_W4A16_H_
+#define FK_W4A16_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FK_OK 0
+#define FK_ERR_INVALID_ARGUMENT 1
+#define FK_ERR_RUNTIME 2
+
+#define FK_ACT_F16 0
+#define FK_ACT_BF16 1
+
+/* Message of the last failed call on this thread ("" if none). Valid until the next fk_* call. */
+const char* fk_last_error(void);
+
+/* Library version and target, e.g. "0.1.0 gfx950". */
+const char* fk_build_info(void);
+
+/* Reference: pack_arc_w4a16_packets, arc_w4a16.h:8-10 / arc_w4a16.cu:649-669. */
+int fk_pack_arc_w4a16_packets(const void* q, const void* alpha, const void* beta, void* packets,
+                              int n, int k, int group_size, int packet_stride_bytes, void* stream);
+
+/* Reference: compute_arc_w4a16_group_sums, arc_w4a16.h:12-13 / arc_w4a16.cu:671-685.
+ * sums[b, g] = sum over the group of x[b, k], fp32. */
+int fk_compute_arc_w4a16_group_sums(const void* activations, void* sums, int batch, int k,
+                                    int group_size, void* stream);
+
+/* Reference: arc_w4a16_forward, arc_w4a16.h:15-17 / arc_w4a16.cu:687-707.
+ * group_sums is accepted for signature compatibility and not read (may be NULL): the kernel forms
+ * the activation sums it needs itself, in the same launch. Uses a library-owned per-device
+ * split-K workspace; calls on one device must be stream-ordered with respect to each other. */
+int fk_arc_w4a16_forward(const void* activations, const void* packets, const void* group_sums,
+                         void* output, int batch, int n, int k, int group_size,
+                         int packet_stride_bytes, void* stream);
+
+/* Reference: arc_w4a16_forward_split_k, arc_w4a16.h:19-22 / arc_w4a16.cu:709-737.
+ * Writes fp32 partials[S, batch, n]; slice z covers groups [z*ceil(NG/S), (z+1)*ceil(NG/S)).
+ * group_sums is not read (may be NULL). */
+int fk_arc_w4a16_forward_split_k(const void* activations, const void* packets,
+                                 const void* group_sums, void* partials, int batch, int n, int k,
+                                 int group_size, int packet_stride_bytes, int split_k_slices,
+                                 void* stream);
+
+/* Reference: reduce_arc_w4a16_split_k_partials, arc_w4a16.h:24-26 / arc_w4a16.cu:739-751. */
+int fk_reduce_arc_w4a16_split_k_partials(const void* partials, void* output, int batch, int n,
+                                         int split_k_slices, void* stream);
+
+/* Reference: dequant_w4a16_to_fp16, arc_w4a16.h:28-30 / arc_w4a16.cu:753-770. */
+int fk_dequant_w4a16_to_fp16(const void* q, const void* alpha, const void* beta, void* output,
+                             int n, int k, int group_size, void* stream);
+
+/* Reference: dequant_arc_w4a16_packets_to_fp16, arc_w4a16.h:32-34 / arc_w4a16.cu:772-789. */
+int fk_dequant_arc_w4a16_packets_to_fp16(const void* packets, void* output, int n, int k,
+                                         int group_size, int packet_stride_bytes, void* stream);
+
+/* Vendor baseline. Reference: cublaslt_fp16_with_weight / _after_packet_dequant / _after_dequant,
+ * arc_w4a16.h:36-52 / arc_w4a16.cu:791-828; served by hipBLASLt (fp16 in, fp32 compute). */
+int fk_hipblaslt_fp16_with_weight(const void* activations, const void* weight, void* output,
+                                  void* workspace, size_t workspace_bytes, int batch, int n, int k,
+                                  void* stream);
+int fk_hipblaslt_fp16_after_packet_dequant(const void* activations, const void* packets,
+                                           void* output, void* weight, void* workspace,
+                                           size_t workspace_bytes, int batch, int n, int k,
+                                           int group_size, int packet_stride_bytes, void* stream);
+int fk_hipblaslt_fp16_after_dequant(const void* activations, const void* q, const void* alpha,
+                                    const void* beta, void* output, void* weight, void* workspace,
+                                    size_t workspace_bytes, int batch, int n, int k,
+                                    int group_size, void* stream);
+
+/* ---- additions with no reference counterpart (BASELINE extensions of the same path) ------ */
+
+typedef struct fk_arc_w4a16_plan {
+  int m_tile;             /* activation rows per workgroup */
+  int split_k_slices;     /* workgroups per 128-column tile along K (1 = no split) */
+  int groups_per_slice;
+  int workgroups;         /* grid size */
+  size_t workspace_bytes; /* workspace fk_arc_w4a16_forward_ex needs */
+} fk_arc_w4a16_plan;
+
+/* Launch plan for a shape. split_k_slices = 0 selects the built-in policy. cu_count = 0 queries
+ * the current device; a positive cu_count plans without touching the GPU. */
+int fk_arc_w4a16_plan_for(int batch, int n, int k, int group_size, int activation_dtype,
+                          int split_k_slices, int cu_count, fk_arc_w4a16_plan* plan);
+
+/* Packet GEMV in one launch with fp16 or bf16 activations (FK_ACT_*), output in the same dtype,
+ * and a caller-owned workspace: at least plan.workspace_bytes, 256-byte aligned, zero-filled
+ * before its first use (every call leaves it zero-filled). Calls sharing a workspace must be
+ * stream-ordered. Capturable into a HIP graph (no allocation, no memset). */
+int fk_arc_w4a16_forward_ex(const void* activations, const void* packets, void* output,
+                            void* workspace, size_t workspace_bytes, int batch, int n, int k,
+                            int group_size, int packet_stride_bytes, int activation_dtype,
+                            int split_k_slices, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FK_W4A16_H_ */

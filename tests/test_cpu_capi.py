@@ -1,0 +1,142 @@
+"""The C-ABI library loads and exports every symbol include/fk_w4a16.h declares; host-only
+entry points (plan, argument validation) behave without a GPU."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parent.parent
+HEADER = REPO / "include" / "fk_w4a16.h"
+LIB = REPO / "fast-kernels_amd" / "fast_kernels" / "libfk_w4a16.so"
+
+
+def _declared() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(fk_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib() -> ctypes.CDLL:
+    if not LIB.exists():
+        pytest.fail(f"{LIB} is missing: run python __graft_entry__.py")
+    return ctypes.CDLL(str(LIB))
+
+
+def test_header_declares_expected_entry_points() -> None:
+    names = _declared()
+    for ref in [
+        "pack_arc_w4a16_packets",
+        "compute_arc_w4a16_group_sums",
+        "arc_w4a16_forward",
+        "arc_w4a16_forward_split_k",
+        "reduce_arc_w4a16_split_k_partials",
+        "dequant_w4a16_to_fp16",
+        "dequant_arc_w4a16_packets_to_fp16",
+    ]:
+        assert f"fk_{ref}" in names
+    assert len(names) >= 14
+
+
+def test_library_exports_every_declared_symbol(lib: ctypes.CDLL) -> None:
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+class Plan(ctypes.Structure):
+    _fields_ = [
+        ("m_tile", ctypes.c_int),
+        ("split_k_slices", ctypes.c_int),
+        ("groups_per_slice", ctypes.c_int),
+        ("workgroups", ctypes.c_int),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+def _plan(lib, batch, n, k, g, act=0, split=0, cu=256):
+    p = Plan()
+    rc = lib.fk_arc_w4a16_plan_for(batch, n, k, g, act, split, cu, ctypes.byref(p))
+    return rc, p
+
+
+def test_plan_policy_without_gpu(lib: ctypes.CDLL) -> None:
+    rc, p = _plan(lib, 1, 57344, 8192, 128)
+    assert rc == 0
+    assert p.m_tile == 1 and p.split_k_slices >= 1
+    assert p.split_k_slices * p.groups_per_slice >= 64
+    assert (p.split_k_slices - 1) * p.groups_per_slice < 64  # no empty slice
+    assert p.workgroups == (57344 // 128) * p.split_k_slices
+    rc, p = _plan(lib, 16, 14336, 4096, 64)
+    assert rc == 0 and p.m_tile == 8
+    rc, p = _plan(lib, 16, 14336, 4096, 64, act=1)
+    assert rc == 0 and p.m_tile == 4  # bf16 caps the rows per workgroup
+    rc, p = _plan(lib, 1, 1024, 8192, 128, split=7)
+    assert rc == 0 and p.split_k_slices == 7 and p.groups_per_slice == 10
+    assert p.workspace_bytes >= 7 * 8 * 128 * 4
+
+
+@pytest.mark.parametrize(
+    "args",
+    [
+        (1, 100, 4096, 128),   # n not a multiple of 128
+        (1, 128, 4000, 128),   # k not a multiple of G
+        (1, 128, 4096, 96),    # unsupported group size
+        (0, 128, 4096, 128),   # batch 0
+    ],
+)
+def test_plan_rejects_bad_shapes(lib: ctypes.CDLL, args) -> None:
+    rc, _ = _plan(lib, *args)
+    assert rc == 1
+    lib.fk_last_error.restype = ctypes.c_char_p
+    assert lib.fk_last_error()
+
+
+def test_validation_runs_before_any_device_call(lib: ctypes.CDLL) -> None:
+    # Bad arguments are rejected (FK_ERR_INVALID_ARGUMENT) without touching the GPU, so this
+    # works on a machine with no GPU at all.
+    lib.fk_last_error.restype = ctypes.c_char_p
+    fwd = lib.fk_arc_w4a16_forward
+    rc = fwd(None, None, None, None, 1, 128, 256, 128, 999, None)
+    assert rc == 1 and b"packet_stride_bytes" in lib.fk_last_error()
+    rc = fwd(None, None, None, None, 1, 128, 256, 128, 128 * 64 + 512, None)
+    assert rc == 1 and b"must not be null" in lib.fk_last_error()
+    rc = lib.fk_arc_w4a16_forward_split_k(None, None, None, None, 1, 128, 256, 128, 8704, 1, None)
+    assert rc == 1 and b"greater than 1" in lib.fk_last_error()
+    rc = lib.fk_arc_w4a16_forward_split_k(None, None, None, None, 1, 128, 256, 128, 8704, 3, None)
+    assert rc == 1 and b"exceed" in lib.fk_last_error()
+    rc = lib.fk_reduce_arc_w4a16_split_k_partials(None, None, 1, 128, 1, None)
+    assert rc == 1
+    rc = lib.fk_arc_w4a16_forward_ex(None, None, None, None, 0, 1, 128, 256, 128, 8704, 5, 0, None)
+    assert rc == 1 and b"activation_dtype" in lib.fk_last_error()
+
+
+def test_pybind_module_mirrors_reference_names() -> None:
+    from fast_kernels.native import native_build_info, native_module
+
+    m = native_module()
+    for name in [
+        "build_info",
+        "compute_arc_w4a16_group_sums",
+        "pack_arc_w4a16_packets",
+        "arc_w4a16_forward",
+        "arc_w4a16_forward_split_k",
+        "reduce_arc_w4a16_split_k_partials",
+        "dequant_w4a16_to_fp16",
+        "dequant_arc_w4a16_packets_to_fp16",
+        "cublaslt_fp16_with_weight",
+        "cublaslt_fp16_after_packet_dequant",
+        "cublaslt_fp16_after_dequant",
+        "arc_w4a16_forward_ex",
+        "arc_w4a16_plan",
+    ]:
+        assert hasattr(m, name), name
+    info = native_build_info()
+    assert info["available"] and info["compiled_with_hip"]
+    with pytest.raises(ValueError):
+        m.arc_w4a16_forward(
+            activations_ptr=0, packets_ptr=0, group_sums_ptr=0, output_ptr=0, batch=1, n=128,
+            k=256, group_size=64, packet_stride_bytes=1, stream_ptr=0,
+        )
