@@ -227,7 +227,7 @@ def main() -> int:
             "pct_peak": round(100.0 * b.bytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 1),
             "bytes": b.bytes,
             "rotations": R,
-            "split_k_slices": b.plan["split_k_slices"],
+            "groups_per_workgroup": b.plan["groups_per_workgroup"],
             "workgroups": b.plan["workgroups"],
         }
 

@@ -209,9 +209,9 @@ PYBIND11_MODULE(_native, m) {
                                     cu_count, &plan));
         py::dict d;
         d["m_tile"] = plan.m_tile;
-        d["split_k_slices"] = plan.split_k_slices;
-        d["groups_per_slice"] = plan.groups_per_slice;
         d["workgroups"] = plan.workgroups;
+        d["groups_per_workgroup"] = plan.groups_per_workgroup;
+        d["max_tile_contributors"] = plan.max_tile_contributors;
         d["workspace_bytes"] = plan.workspace_bytes;
         return d;
       },

@@ -147,9 +147,9 @@ int fk_arc_w4a16_plan_for(int batch, int n, int k, int group_size, int activatio
                      : ops::plan_arc_w4a16(batch, n, k, group_size, activation_dtype,
                                            split_k_slices);
     plan->m_tile = p.m_tile;
-    plan->split_k_slices = p.split_k_slices;
-    plan->groups_per_slice = p.groups_per_slice;
     plan->workgroups = p.workgroups;
+    plan->groups_per_workgroup = p.groups_per_workgroup;
+    plan->max_tile_contributors = p.max_tile_contributors;
     plan->workspace_bytes = p.workspace_bytes;
   });
 }

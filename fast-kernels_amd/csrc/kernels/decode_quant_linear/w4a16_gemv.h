@@ -8,36 +8,36 @@
 namespace fk {
 
 enum class GemvMode : int {
-  kDirect = 0,    // one workgroup per (tile, m-tile) covers all of K, writes the output
-  kFixup = 1,     // split-K, last-arriving workgroup of a tile reduces partials in-kernel
-  kPartials = 2,  // split-K, writes fp32 partials [S_k, M, N] (reference layout, no reduce)
+  kStreamK = 0,   // equal runs of (tile, group) units per workgroup, in-kernel fix-up
+  kPartials = 1,  // fixed split-K, writes fp32 partials [S_k, M, N] (reference layout)
 };
 
 struct GemvLaunch {
   const void* x = nullptr;
   const void* packets = nullptr;
   void* out = nullptr;
-  void* partials = nullptr;   // kFixup: scratch, kPartials: [S_k, M, N] fp32
-  void* counters = nullptr;   // kFixup only: zero-initialised uint32 per (tile, m-tile)
+  void* partials = nullptr;   // kStreamK: scratch, kPartials: [S_k, M, N] fp32
+  void* counters = nullptr;   // kStreamK: zero-initialised uint32 per (tile, m-tile)
   int M = 0, N = 0, K = 0;
   int group_size = 128;
   Act act = Act::kF16;
-  GemvMode mode = GemvMode::kDirect;
+  GemvMode mode = GemvMode::kStreamK;
   int m_tile = 1;
-  int splits = 1;
-  int gps = 0;  // groups per split
+  int splits = 1;               // kPartials
+  int gps = 0;                  // kPartials: groups per split
+  int units_per_workgroup = 0;  // kStreamK: group units per workgroup
+  int max_contributors = 0;     // kStreamK: partial slots per tile in the scratch
 };
 
 int gemv_m_tile_for_batch(int batch);
 
-// fp32 scratch floats and counters the kFixup mode needs for a launch.
-inline size_t gemv_fixup_partial_floats(int n, int batch, int m_tile, int splits) {
-  const size_t tiles = static_cast<size_t>(n / kTileCols);
-  const size_t mtiles = static_cast<size_t>((batch + m_tile - 1) / m_tile);
-  return tiles * mtiles * static_cast<size_t>(splits) * m_tile * kTileCols;
-}
-inline size_t gemv_fixup_counters(int n, int batch, int m_tile) {
+// Tiles (128 columns x m_tile rows) of a launch; the stream-K scratch holds one counter and
+// max_contributors fp32 partial slots of m_tile x 128 floats per tile.
+inline size_t gemv_tiles(int n, int batch, int m_tile) {
   return static_cast<size_t>(n / kTileCols) * static_cast<size_t>((batch + m_tile - 1) / m_tile);
+}
+inline size_t gemv_streamk_partial_floats(int n, int batch, int m_tile, int max_contributors) {
+  return gemv_tiles(n, batch, m_tile) * static_cast<size_t>(max_contributors) * m_tile * kTileCols;
 }
 
 hipError_t launch_w4a16_gemv(const GemvLaunch& launch, hipStream_t stream);

@@ -7,19 +7,25 @@
 //  * 128-bit loads. A packet (arc_w4a16.cu:87-122) stores word w of column c at byte
 //    (w*128 + c)*4, so one 64-lane dwordx4 load covers two word rows x 128 columns: lane l holds
 //    word row 2i + (l>>5) for the four columns 4*(l&31) .. +3. A wave streams one whole group
-//    (G/16 loads) and keeps the next group's loads in flight while it computes.
-//  * Register dequant with no per-element conversion: nibbles are OR-ed into fp16 / bf16
-//    mantissas (see w4a16_device.h) and multiplied by v_dot2 against activations that were
-//    re-paired once per workgroup in LDS. The constant bias that trick adds (1024 for fp16, 128
-//    for bf16, times 1 or 16 depending on nibble position) is removed once per group and column
-//    with per-group activation sums: sum((B + s*q) x) = B*sum(x) + s*sum(q x).
-//  * Split-K across workgroups with an in-kernel fix-up: each workgroup reduces its 4 waves
-//    through LDS (lanes l and l^32 first, with a cross-lane swap), writes an fp32 partial, and the
-//    last workgroup of a tile to arrive (device-scope atomic counter) sums the partials in
-//    split order, so the result does not depend on arrival order. The counter is reset by that
-//    workgroup, so no memset is needed between calls (graph-capture friendly).
-//  * Logical tile order is remapped so that consecutive logical workgroups (the splits of one
-//    tile) run on the same XCD: the hardware dispatches workgroup b to XCD b % 8.
+//    (G/16 loads) while the next group's loads are in flight.
+//  * Register dequant with no per-element conversion: nibbles are OR-ed into fp16 mantissas
+//    (see w4a16_device.h) and multiplied by v_dot2_f32_f16 (fp32 accumulation) against
+//    activations re-paired once per workgroup in LDS. The constant bias the trick adds (1024 for
+//    low nibbles, 1024 + 16x scale for high nibbles) is removed once per group and column with
+//    per-group activation sums: sum((1024 + s*q) x) = 1024*sum(x) + s*sum(q x).
+//  * bf16 activations are converted to fp16 when staged, after scaling each (row, group) by a
+//    power of two that keeps its largest magnitude inside fp16's range; the scale is re-applied
+//    to the group's fp32 partial. Every bf16 value whose scaled magnitude is >= 2^-17 converts
+//    exactly (bf16 has 8 significant bits, fp16 normals 11), so bf16 runs the same fp16 inner
+//    loop.
+//  * Stream-K work split: the grid is sized to be resident on the chip at once and each
+//    workgroup takes an equal run of (tile, group) units, crossing tile boundaries; tiles shared
+//    by several workgroups are finished in-kernel by their last contributor (see the kernel).
+//    Equal runs avoid both the load imbalance of whole-tile workgroups (448 tiles on 256 CUs)
+//    and a second round of short workgroups.
+//  * Logical workgroup order is remapped so that consecutive logical workgroups (the
+//    contributors of one tile) run on the same XCD: the hardware dispatches workgroup b to
+//    XCD b % 8.
 #include "w4a16_gemv.h"
 
 #include <hip/hip_runtime.h>
@@ -34,33 +40,47 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kChunkGroups = 16;  // groups whose activations are staged in LDS at once
+// Groups whose activations are staged in LDS at once: a whole split of K in the common M=1
+// plans, so a workgroup passes one barrier before streaming.
+#ifndef FK_GEMV_M1_CHUNK
+#define FK_GEMV_M1_CHUNK 32
+#endif
+template <int MT>
+constexpr int chunk_groups() {
+  return MT == 1 ? FK_GEMV_M1_CHUNK : 16;
+}
 // s_waitcnt immediate for gfx9: vmcnt = 0 (bits 3:0 and 15:14), expcnt and lgkmcnt left at max.
 constexpr int kWaitVmcnt0 = 0x0F70;
+// Largest bf16 biased exponent whose values all fit in fp16 (2^15 * (2 - 2^-7) < 65504).
+constexpr int kMaxFp16SafeBf16Exp = 142;
 
 template <int G, int MT>
 struct Smem {
+  static constexpr int kChunk = chunk_groups<MT>();
   static constexpr int kWordRows = G / 8;
-  uint4 xs[MT][kChunkGroups][kWordRows];  // re-paired activations, 16 B per word row
-  float4 sums[MT][kChunkGroups];          // {even p0, odd p0, even p1, odd p1}
-  float red[kWaves][MT][kTileCols];       // cross-wave reduction
-  int last;                               // this workgroup finishes the tile
+  uint4 xs[MT][kChunk][kWordRows];  // re-paired fp16 activations, 16 B per word row
+  float4 sums[MT][kChunk];          // {even p0, odd p0, even p1, odd p1} of the staged values
+  float scale[MT][kChunk];          // power of two undoing the bf16 staging scale (1 for fp16)
+  float red[kWaves][MT][kTileCols]; // cross-wave reduction
+  int last;                         // this workgroup finishes the tile
 };
 
 struct GemvParams {
-  const uint16_t* x;      // [M, K] activations (fp16 or bf16 bits)
-  const uint8_t* packets; // [(N/128) * NG, S]
-  uint16_t* out;          // [M, N] (unused in partials mode)
-  float* partials;        // fix-up scratch or reference split-K partials [S_k, M, N]
-  uint32_t* counters;     // fix-up arrival counters, one per (tile, m-tile)
+  const uint16_t* x;       // [M, K] activations (fp16 or bf16 bits)
+  const uint8_t* packets;  // [(N/128) * NG, S]
+  uint16_t* out;           // [M, N] (unused in partials mode)
+  float* partials;         // fix-up scratch or reference split-K partials [S_k, M, N]
+  uint32_t* counters;      // fix-up arrival counters, one per (tile, m-tile)
   int M, N, K, NG;
-  int tiles, mtiles, splits, gps;
+  int tiles, mtiles, splits, gps;  // kPartials: fixed split of every tile
+  int per;                          // stream-K: group units per workgroup
+  int max_contrib;                  // stream-K: partial slots per tile in the scratch
   int xcd_remap;
 };
 
 template <int G, int MT>
 struct StageRegs {
-  static constexpr int kUnits = MT * kChunkGroups * (G / 8);
+  static constexpr int kUnits = MT * chunk_groups<MT>() * (G / 8);
   static constexpr int kPerThread = (kUnits + kThreads - 1) / kThreads;
   uint4 raw[kPerThread];
 };
@@ -70,13 +90,14 @@ template <int G, int MT>
 __device__ __forceinline__ void stage_load(StageRegs<G, MT>& st, const GemvParams& p, int row0,
                                            int g0, int n_chunk) {
   constexpr int WR = G / 8;
+  constexpr int kChunk = chunk_groups<MT>();
   const int tid = static_cast<int>(threadIdx.x);
 #pragma unroll
   for (int it = 0; it < StageRegs<G, MT>::kPerThread; ++it) {
     const int u = it * kThreads + tid;
     const int w = u % WR;
-    const int gl = (u / WR) % kChunkGroups;
-    const int m = u / (WR * kChunkGroups);
+    const int gl = (u / WR) % kChunk;
+    const int m = u / (WR * kChunk);
     st.raw[it] = make_uint4(0u, 0u, 0u, 0u);
     if (u < StageRegs<G, MT>::kUnits && gl < n_chunk && row0 + m < p.M) {
       const size_t off = static_cast<size_t>(row0 + m) * p.K +
@@ -86,30 +107,55 @@ __device__ __forceinline__ void stage_load(StageRegs<G, MT>& st, const GemvParam
   }
 }
 
-// Re-pair the staged activations into LDS and reduce the per-(row, group, parity) sums.
+__device__ __forceinline__ uint32_t bf16_exp(uint32_t pair_word) {
+  return max((pair_word >> 7) & 0xffu, (pair_word >> 23) & 0xffu);
+}
+
+__device__ __forceinline__ uint32_t bf16_pair_to_half_pair(uint32_t w, float s) {
+  const uint32_t lo = float_to_half_bits(bf16_bits_to_float(static_cast<uint16_t>(w)) * s);
+  const uint32_t hi = float_to_half_bits(bf16_bits_to_float(static_cast<uint16_t>(w >> 16)) * s);
+  return lo | (hi << 16);
+}
+
+// Convert (bf16) and re-pair the staged activations into LDS and reduce the per-(row, group,
+// parity) sums. Rows of one (m, group) are WR consecutive, WR-aligned lanes, so xor-shuffles
+// over 1..WR/2 stay inside the group.
 template <int G, Act A, int MT>
-__device__ __forceinline__ void stage_store(Smem<G, MT>& sm, const StageRegs<G, MT>& st,
-                                            int n_chunk) {
+__device__ __forceinline__ void stage_store(Smem<G, MT>& sm, StageRegs<G, MT>& st, int n_chunk) {
   constexpr int WR = G / 8;
+  constexpr int kChunk = chunk_groups<MT>();
   const int tid = static_cast<int>(threadIdx.x);
 #pragma unroll
   for (int it = 0; it < StageRegs<G, MT>::kPerThread; ++it) {
     const int u = it * kThreads + tid;
     const int w = u % WR;
-    const int gl = (u / WR) % kChunkGroups;
-    const int m = u / (WR * kChunkGroups);
-    const uint4 r = st.raw[it];
+    const int gl = (u / WR) % kChunk;
+    const int m = u / (WR * kChunk);
+    uint4 r = st.raw[it];
+    float undo = 1.0f;
+    if constexpr (A == Act::kBF16) {
+      uint32_t e = max(max(bf16_exp(r.x), bf16_exp(r.y)), max(bf16_exp(r.z), bf16_exp(r.w)));
+#pragma unroll
+      for (int off = 1; off < WR; off <<= 1) {
+        e = max(e, static_cast<uint32_t>(__shfl_xor(static_cast<int>(e), off)));
+      }
+      const int shift = max(0, static_cast<int>(e) - kMaxFp16SafeBf16Exp);
+      const float s = __builtin_bit_cast(float, static_cast<uint32_t>(127 - shift) << 23);
+      undo = __builtin_bit_cast(float, static_cast<uint32_t>(127 + shift) << 23);
+      r.x = bf16_pair_to_half_pair(r.x, s);
+      r.y = bf16_pair_to_half_pair(r.y, s);
+      r.z = bf16_pair_to_half_pair(r.z, s);
+      r.w = bf16_pair_to_half_pair(r.w, s);
+    }
     // even k: x0 x2 x4 x6 (low halves), odd k: x1 x3 x5 x7 (high halves)
-    float se = act_bits_to_float<A>(static_cast<uint16_t>(r.x)) +
-               act_bits_to_float<A>(static_cast<uint16_t>(r.y)) +
-               act_bits_to_float<A>(static_cast<uint16_t>(r.z)) +
-               act_bits_to_float<A>(static_cast<uint16_t>(r.w));
-    float so = act_bits_to_float<A>(static_cast<uint16_t>(r.x >> 16)) +
-               act_bits_to_float<A>(static_cast<uint16_t>(r.y >> 16)) +
-               act_bits_to_float<A>(static_cast<uint16_t>(r.z >> 16)) +
-               act_bits_to_float<A>(static_cast<uint16_t>(r.w >> 16));
-    // Sum the word rows of one (m, group) that share a parity: they sit in WR consecutive,
-    // WR-aligned lanes, so xor-shuffles over 2..WR/2 stay inside the group.
+    float se = half_bits_to_float(static_cast<uint16_t>(r.x)) +
+               half_bits_to_float(static_cast<uint16_t>(r.y)) +
+               half_bits_to_float(static_cast<uint16_t>(r.z)) +
+               half_bits_to_float(static_cast<uint16_t>(r.w));
+    float so = half_bits_to_float(static_cast<uint16_t>(r.x >> 16)) +
+               half_bits_to_float(static_cast<uint16_t>(r.y >> 16)) +
+               half_bits_to_float(static_cast<uint16_t>(r.z >> 16)) +
+               half_bits_to_float(static_cast<uint16_t>(r.w >> 16));
 #pragma unroll
     for (int off = 2; off < WR; off <<= 1) {
       se += __shfl_xor(se, off);
@@ -121,6 +167,9 @@ __device__ __forceinline__ void stage_store(Smem<G, MT>& sm, const StageRegs<G, 
         float* s = reinterpret_cast<float*>(&sm.sums[m][gl]);
         s[2 * w + 0] = se;
         s[2 * w + 1] = so;
+      }
+      if (w == 0) {
+        sm.scale[m][gl] = undo;
       }
     }
   }
@@ -160,11 +209,15 @@ __device__ __forceinline__ void load_group(GroupLoad<G>& gl, const uint8_t* pack
   }
 }
 
+// One group: multiply-accumulate its codes against the staged activations, then apply the
+// group's scales and remove the unpack bias:
+// y += alpha * (acc_e - 1024 S_e) + alpha/16 * (acc_o - 1024 S_o) + beta * (S_e + S_o).
 template <int G, Act A, int MT>
 __device__ __forceinline__ void compute_group(const Smem<G, MT>& sm, const GroupLoad<G>& ld,
                                               int gl, int parity, uint32_t mask_lo,
                                               uint32_t mask_hi, float (&y)[MT][4]) {
   constexpr int NL = G / 16;
+  constexpr uint32_t kBias = 0x64006400u;  // fp16 1024.0 pair
   float acc_e[MT][4];
   float acc_o[MT][4];
 #pragma unroll
@@ -188,33 +241,17 @@ __device__ __forceinline__ void compute_group(const Smem<G, MT>& sm, const Group
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t wv = words[j];
-      if constexpr (A == Act::kF16) {
-        constexpr uint32_t kBias = 0x64006400u;
-        const uint32_t e0 = (wv & mask_lo) | kBias;  // 1024+q for k0,k4
-        const uint32_t o0 = (wv & mask_hi) | kBias;  // 1024+16q for k1,k5
-        const uint32_t w8 = wv >> 8;
-        const uint32_t e1 = (w8 & mask_lo) | kBias;  // k2,k6
-        const uint32_t o1 = (w8 & mask_hi) | kBias;  // k3,k7
+      const uint32_t e0 = (wv & mask_lo) | kBias;  // 1024+q for k0,k4
+      const uint32_t o0 = (wv & mask_hi) | kBias;  // 1024+16q for k1,k5
+      const uint32_t w8 = wv >> 8;
+      const uint32_t e1 = (w8 & mask_lo) | kBias;  // k2,k6
+      const uint32_t o1 = (w8 & mask_hi) | kBias;  // k3,k7
 #pragma unroll
-        for (int m = 0; m < MT; ++m) {
-          acc_e[m][j] = dot2<A>(e0, xp[m].x, acc_e[m][j]);
-          acc_o[m][j] = dot2<A>(o0, xp[m].y, acc_o[m][j]);
-          acc_e[m][j] = dot2<A>(e1, xp[m].z, acc_e[m][j]);
-          acc_o[m][j] = dot2<A>(o1, xp[m].w, acc_o[m][j]);
-        }
-      } else {
-        constexpr uint32_t kBias = 0x43004300u;  // bf16 128.0 pair
-        const uint32_t t0 = (wv & mask_lo) | kBias;
-        const uint32_t t1 = ((wv >> 4) & mask_lo) | kBias;
-        const uint32_t t2 = ((wv >> 8) & mask_lo) | kBias;
-        const uint32_t t3 = ((wv >> 12) & mask_lo) | kBias;
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-          acc_e[m][j] = dot2<A>(t0, xp[m].x, acc_e[m][j]);
-          acc_o[m][j] = dot2<A>(t1, xp[m].y, acc_o[m][j]);
-          acc_e[m][j] = dot2<A>(t2, xp[m].z, acc_e[m][j]);
-          acc_o[m][j] = dot2<A>(t3, xp[m].w, acc_o[m][j]);
-        }
+      for (int m = 0; m < MT; ++m) {
+        acc_e[m][j] = dot2<Act::kF16>(e0, xp[m].x, acc_e[m][j]);
+        acc_o[m][j] = dot2<Act::kF16>(o0, xp[m].y, acc_o[m][j]);
+        acc_e[m][j] = dot2<Act::kF16>(e1, xp[m].z, acc_e[m][j]);
+        acc_o[m][j] = dot2<Act::kF16>(o1, xp[m].w, acc_o[m][j]);
       }
     }
   }
@@ -227,107 +264,99 @@ __device__ __forceinline__ void compute_group(const Smem<G, MT>& sm, const Group
   for (int j = 0; j < 4; ++j) {
     const float a = half_bits_to_float(a_bits[j]);
     const float b = half_bits_to_float(b_bits[j]);
-    if constexpr (A == Act::kF16) {
-      const float a16 = a * 0.0625f;
-      const float ce = fmaf(-1024.0f, a, b);  // beta - 1024 alpha
-      const float co = fmaf(-64.0f, a, b);    // beta - 64 alpha
+    const float a16 = a * 0.0625f;
+    const float ce = fmaf(-1024.0f, a, b);  // beta - 1024 alpha
+    const float co = fmaf(-64.0f, a, b);    // beta - 64 alpha
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        const float4 s = sm.sums[m][gl];
-        const float se = parity ? s.z : s.x;
-        const float so = parity ? s.w : s.y;
-        float t = fmaf(a, acc_e[m][j], ce * se);
-        t = fmaf(a16, acc_o[m][j], t);
-        t = fmaf(co, so, t);
-        y[m][j] += t;
+    for (int m = 0; m < MT; ++m) {
+      const float4 s = sm.sums[m][gl];
+      const float se = parity ? s.z : s.x;
+      const float so = parity ? s.w : s.y;
+      float t = fmaf(a, acc_e[m][j], ce * se);
+      t = fmaf(a16, acc_o[m][j], t);
+      t = fmaf(co, so, t);
+      if constexpr (A == Act::kBF16) {
+        t *= sm.scale[m][gl];
       }
-    } else {
-      const float c = fmaf(-128.0f, a, b);  // beta - 128 alpha
-#pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        const float4 s = sm.sums[m][gl];
-        const float sp = parity ? (s.z + s.w) : (s.x + s.y);
-        const float t = fmaf(a, acc_e[m][j] + acc_o[m][j], c * sp);
-        y[m][j] += t;
+      y[m][j] += t;
+    }
+  }
+}
+
+// Waves per SIMD the M=1 kernel must fit (caps its VGPRs at 512 / waves). Two is the measured
+// optimum: the double-buffered loop needs ~170 VGPRs, and capping lower spills registers.
+#ifndef FK_GEMV_M1_MIN_WAVES_PER_EU
+#define FK_GEMV_M1_MIN_WAVES_PER_EU 2
+#endif
+template <int MT>
+constexpr int min_waves_per_eu() {
+  return MT == 1 ? FK_GEMV_M1_MIN_WAVES_PER_EU : 1;
+}
+
+// Accumulate groups [g_lo, g_hi) of one 128-column tile into y: stage the activations of up to
+// kChunk groups in LDS, then each wave streams groups g_lo + wave, g_lo + wave + 4, ...
+template <int G, Act A, int MT>
+__device__ __forceinline__ void stream_groups(Smem<G, MT>& sm, const GemvParams& p,
+                                              const uint8_t* tile_packets, int row0, int g_lo,
+                                              int g_hi, int lane, int wave, int parity,
+                                              uint32_t mask_lo, uint32_t mask_hi,
+                                              float (&y)[MT][4]) {
+  constexpr int kChunk = chunk_groups<MT>();
+  const size_t stride = static_cast<size_t>(packet_stride_bytes(G));
+  for (int g0 = g_lo; g0 < g_hi; g0 += kChunk) {
+    const int n_chunk = min(kChunk, g_hi - g0);
+    if (g0 != g_lo) {
+      lds_barrier();  // previous chunk's readers are done with xs / sums
+    }
+    // Activation loads first, then this wave's first weight groups, so the LDS writes below only
+    // wait for the activations while the weights stay in flight across the barrier.
+    StageRegs<G, MT> st;
+    stage_load<G, MT>(st, p, row0, g0, n_chunk);
+    // This wave's groups in the chunk: gl = wave, wave + 4, ... (n_w of them). Two register
+    // buffers alternate and each is refilled right after it is consumed, so one group's loads
+    // are always in flight behind the group being computed. The steady-state loop has no
+    // conditional loads, so the compiler keeps both buffers in place (no register copies that
+    // would force an early wait on loads still in flight).
+    const int n_w = n_chunk > wave ? (n_chunk - wave + kWaves - 1) / kWaves : 0;
+    const uint8_t* gp = tile_packets + static_cast<size_t>(g0 + wave) * stride;
+    const size_t step = static_cast<size_t>(kWaves) * stride;
+    GroupLoad<G> buf_a;
+    GroupLoad<G> buf_b;
+    if (n_w > 0) {
+      load_group<G>(buf_a, gp, lane);
+    }
+    stage_store<G, A, MT>(sm, st, n_chunk);
+    if (n_w > 1) {
+      load_group<G>(buf_b, gp + step, lane);
+    }
+    lds_barrier();
+    int t = 0;
+    for (; t + 3 < n_w; t += 2) {
+      compute_group<G, A, MT>(sm, buf_a, wave + t * kWaves, parity, mask_lo, mask_hi, y);
+      load_group<G>(buf_a, gp + static_cast<size_t>(t + 2) * step, lane);
+      compute_group<G, A, MT>(sm, buf_b, wave + (t + 1) * kWaves, parity, mask_lo, mask_hi, y);
+      load_group<G>(buf_b, gp + static_cast<size_t>(t + 3) * step, lane);
+    }
+    // 0..3 groups remain: t and t+1 are loaded, t+2 is not.
+    if (t < n_w) {
+      compute_group<G, A, MT>(sm, buf_a, wave + t * kWaves, parity, mask_lo, mask_hi, y);
+      if (t + 2 < n_w) {
+        load_group<G>(buf_a, gp + static_cast<size_t>(t + 2) * step, lane);
+      }
+      if (t + 1 < n_w) {
+        compute_group<G, A, MT>(sm, buf_b, wave + (t + 1) * kWaves, parity, mask_lo, mask_hi, y);
+      }
+      if (t + 2 < n_w) {
+        compute_group<G, A, MT>(sm, buf_a, wave + (t + 2) * kWaves, parity, mask_lo, mask_hi, y);
       }
     }
   }
 }
 
-template <int G, Act A, int MT, GemvMode MODE>
-__global__ void __launch_bounds__(kThreads)
-w4a16_gemv_kernel(GemvParams p) {
-  __shared__ Smem<G, MT> sm;
-  const int tid = static_cast<int>(threadIdx.x);
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int parity = lane >> 5;
-
-  // Logical workgroup id: keep consecutive ids (the splits of one tile) on one XCD.
-  const int total = p.tiles * p.mtiles * p.splits;
-  int L = static_cast<int>(blockIdx.x);
-  if (p.xcd_remap) {
-    L = (L & 7) * (total >> 3) + (L >> 3);
-  }
-  const int split = L % p.splits;
-  const int rest = L / p.splits;
-  const int tile = rest % p.tiles;
-  const int mtile = rest / p.tiles;
-  const int row0 = mtile * MT;
-
-  const int g_begin = split * p.gps;
-  const int g_end = min(p.NG, g_begin + p.gps);
-  const size_t stride = static_cast<size_t>(packet_stride_bytes(G));
-  const uint8_t* tile_packets = p.packets + static_cast<size_t>(tile) * p.NG * stride;
-
-  float y[MT][4];
-#pragma unroll
-  for (int m = 0; m < MT; ++m) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      y[m][j] = 0.0f;
-    }
-  }
-
-  const uint32_t mask_lo = vgpr_constant(0x000f000fu);
-  const uint32_t mask_hi = vgpr_constant(0x00f000f0u);
-  for (int g0 = g_begin; g0 < g_end; g0 += kChunkGroups) {
-    const int n_chunk = min(kChunkGroups, g_end - g0);
-    if (g0 != g_begin) {
-      lds_barrier();  // previous chunk's readers are done with xs / sums
-    }
-    // Activation loads first, then this wave's first weight group, so the LDS writes below only
-    // wait for the activations while the weights stay in flight across the barrier.
-    StageRegs<G, MT> st;
-    stage_load<G, MT>(st, p, row0, g0, n_chunk);
-    GroupLoad<G> buf_a;
-    GroupLoad<G> buf_b;
-    int gl = wave;
-    if (gl < n_chunk) {
-      load_group<G>(buf_a, tile_packets + static_cast<size_t>(g0 + gl) * stride, lane);
-    }
-    stage_store<G, A, MT>(sm, st, n_chunk);
-    lds_barrier();
-    // Ping-pong between two register buffers: the next group's loads are issued before the
-    // current group is computed.
-    while (gl < n_chunk) {
-      if (gl + kWaves < n_chunk) {
-        load_group<G>(buf_b, tile_packets + static_cast<size_t>(g0 + gl + kWaves) * stride, lane);
-      }
-      compute_group<G, A, MT>(sm, buf_a, gl, parity, mask_lo, mask_hi, y);
-      gl += kWaves;
-      if (gl >= n_chunk) {
-        break;
-      }
-      if (gl + kWaves < n_chunk) {
-        load_group<G>(buf_a, tile_packets + static_cast<size_t>(g0 + gl + kWaves) * stride, lane);
-      }
-      compute_group<G, A, MT>(sm, buf_b, gl, parity, mask_lo, mask_hi, y);
-      gl += kWaves;
-    }
-  }
-
-  // Lanes l and l^32 hold the two word-row parities of the same four columns.
+// Sum y over the lanes l / l^32 (the two word-row parities) and the 4 waves into sm.red.
+template <int G, int MT>
+__device__ __forceinline__ void reduce_to_lds(Smem<G, MT>& sm, float (&y)[MT][4], int lane,
+                                              int wave, int parity) {
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
 #pragma unroll
@@ -343,68 +372,138 @@ w4a16_gemv_kernel(GemvParams p) {
     }
   }
   __syncthreads();
+}
 
-  const int col_base = tile * kTileCols;
+template <int G, int MT>
+__device__ __forceinline__ float red_sum(const Smem<G, MT>& sm, int m, int c) {
+  return sm.red[0][m][c] + sm.red[1][m][c] + sm.red[2][m][c] + sm.red[3][m][c];
+}
+
+// Work decomposition. The (tile, m-tile) pairs laid end to end form a line of T*NG group units
+// (T = tiles * mtiles). Workgroup b owns units [b*per, (b+1)*per): "stream-K", every workgroup
+// gets the same number of groups whatever the shape, and the grid is sized to fit on the chip
+// at once, so no workgroup waits for a second round. A tile whose units all belong to one
+// workgroup is written directly. A tile split between workgroups is finished by the last of its
+// contributors to arrive (device-scope counter), which adds the fp32 partials in workgroup
+// order, so results do not depend on arrival order; it also resets the counter, so no memset is
+// needed between calls (graph-capture friendly).
+//
+// kPartials (the reference split-K protocol) instead writes each workgroup's fp32 partial to
+// partials[split, m, n] with split = b % splits over a fixed per-tile split.
+template <int G, Act A, int MT, GemvMode MODE>
+__global__ void __launch_bounds__(kThreads, min_waves_per_eu<MT>())
+w4a16_gemv_kernel(GemvParams p) {
   constexpr int kOut = MT * kTileCols;
+  __shared__ Smem<G, MT> sm;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int parity = lane >> 5;
+  const uint32_t mask_lo = vgpr_constant(0x000f000fu);
+  const uint32_t mask_hi = vgpr_constant(0x00f000f0u);
+  const size_t stride = static_cast<size_t>(packet_stride_bytes(G));
 
-  if constexpr (MODE == GemvMode::kDirect) {
+  // Logical workgroup id: keep consecutive ids (the contributors of one tile) on one XCD.
+  const int grid = static_cast<int>(gridDim.x);
+  int b = static_cast<int>(blockIdx.x);
+  if (p.xcd_remap) {
+    b = (b & 7) * (grid >> 3) + (b >> 3);
+  }
+
+  if constexpr (MODE == GemvMode::kPartials) {
+    const int split = b % p.splits;
+    const int T = b / p.splits;
+    const int tile = T % p.tiles;
+    const int row0 = (T / p.tiles) * MT;
+    const int g_lo = split * p.gps;
+    const int g_hi = min(p.NG, g_lo + p.gps);
+    float y[MT][4] = {};
+    const uint8_t* tile_packets = p.packets + static_cast<size_t>(tile) * p.NG * stride;
+    stream_groups<G, A, MT>(sm, p, tile_packets, row0, g_lo, g_hi, lane, wave, parity, mask_lo,
+                            mask_hi, y);
+    reduce_to_lds<G, MT>(sm, y, lane, wave, parity);
     for (int idx = tid; idx < kOut; idx += kThreads) {
       const int m = idx / kTileCols;
       const int c = idx % kTileCols;
       if (row0 + m < p.M) {
-        const float v = sm.red[0][m][c] + sm.red[1][m][c] + sm.red[2][m][c] + sm.red[3][m][c];
-        p.out[static_cast<size_t>(row0 + m) * p.N + col_base + c] = float_to_act_bits<A>(v);
+        p.partials[(static_cast<size_t>(split) * p.M + row0 + m) * p.N + tile * kTileCols + c] =
+            red_sum(sm, m, c);
       }
     }
-  } else if constexpr (MODE == GemvMode::kPartials) {
-    for (int idx = tid; idx < kOut; idx += kThreads) {
-      const int m = idx / kTileCols;
-      const int c = idx % kTileCols;
-      if (row0 + m < p.M) {
-        const float v = sm.red[0][m][c] + sm.red[1][m][c] + sm.red[2][m][c] + sm.red[3][m][c];
-        p.partials[(static_cast<size_t>(split) * p.M + row0 + m) * p.N + col_base + c] = v;
-      }
-    }
+    return;
   } else {
-    // Cross-workgroup hand-off without cache-wide maintenance: the partials and the counter are
-    // accessed only through agent-scope relaxed atomics, which the gfx950 memory model serves
-    // coherently across XCDs (their L2s are not coherent with each other) without the
-    // whole-L2 write-back / invalidate an agent-scope fence costs. Ordering between the partial
-    // stores and the counter increment comes from waiting for the stores to complete (vmcnt(0))
-    // before the workgroup barrier that precedes the increment.
-    const int tm = mtile * p.tiles + tile;
-    float* ws = p.partials + static_cast<size_t>(tm) * p.splits * kOut;
-    for (int idx = tid; idx < kOut; idx += kThreads) {
-      const int m = idx / kTileCols;
-      const int c = idx % kTileCols;
-      const float v = sm.red[0][m][c] + sm.red[1][m][c] + sm.red[2][m][c] + sm.red[3][m][c];
-      __hip_atomic_store(&ws[static_cast<size_t>(split) * kOut + idx], v, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-    __syncthreads();
-    if (tid == 0) {
-      const uint32_t prev =
-          __hip_atomic_fetch_add(&p.counters[tm], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      sm.last = (prev == static_cast<uint32_t>(p.splits - 1)) ? 1 : 0;
-    }
-    __syncthreads();
-    if (sm.last) {
-      for (int idx = tid; idx < kOut; idx += kThreads) {
-        const int m = idx / kTileCols;
-        const int c = idx % kTileCols;
-        if (row0 + m < p.M) {
-          float v = 0.0f;
-          for (int s = 0; s < p.splits; ++s) {
-            v += __hip_atomic_load(&ws[static_cast<size_t>(s) * kOut + idx], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+    const long long total_units = static_cast<long long>(p.tiles) * p.mtiles * p.NG;
+    const long long u_begin = static_cast<long long>(b) * p.per;
+    const long long u_end = min(total_units, u_begin + p.per);
+    long long u = u_begin;
+    while (u < u_end) {
+      const int T = static_cast<int>(u / p.NG);
+      const int g_lo = static_cast<int>(u - static_cast<long long>(T) * p.NG);
+      const int g_hi = static_cast<int>(min(static_cast<long long>(p.NG), g_lo + (u_end - u)));
+      const int tile = T % p.tiles;
+      const int row0 = (T / p.tiles) * MT;
+      const int col_base = tile * kTileCols;
+      float y[MT][4] = {};
+      const uint8_t* tile_packets = p.packets + static_cast<size_t>(tile) * p.NG * stride;
+      stream_groups<G, A, MT>(sm, p, tile_packets, row0, g_lo, g_hi, lane, wave, parity,
+                              mask_lo, mask_hi, y);
+      reduce_to_lds<G, MT>(sm, y, lane, wave, parity);
+
+      const long long tile_u0 = static_cast<long long>(T) * p.NG;
+      const int first = static_cast<int>(tile_u0 / p.per);
+      const int last = static_cast<int>((tile_u0 + p.NG - 1) / p.per);
+      if (first == last) {
+        for (int idx = tid; idx < kOut; idx += kThreads) {
+          const int m = idx / kTileCols;
+          const int c = idx % kTileCols;
+          if (row0 + m < p.M) {
+            p.out[static_cast<size_t>(row0 + m) * p.N + col_base + c] =
+                float_to_act_bits<A>(red_sum(sm, m, c));
           }
-          p.out[static_cast<size_t>(row0 + m) * p.N + col_base + c] = float_to_act_bits<A>(v);
+        }
+      } else {
+        // Cross-workgroup hand-off without cache-wide maintenance: the partials and the counter
+        // are accessed only through agent-scope relaxed atomics, which the gfx950 memory model
+        // serves coherently across XCDs (their L2s are not coherent with each other) without
+        // the whole-L2 write-back / invalidate an agent-scope fence costs. Ordering between the
+        // partial stores and the counter increment comes from waiting for the stores to
+        // complete (vmcnt(0)) before the workgroup barrier that precedes the increment.
+        const int contributors = last - first + 1;
+        float* ws = p.partials + static_cast<size_t>(T) * p.max_contrib * kOut;
+        for (int idx = tid; idx < kOut; idx += kThreads) {
+          const int m = idx / kTileCols;
+          const int c = idx % kTileCols;
+          __hip_atomic_store(&ws[static_cast<size_t>(b - first) * kOut + idx], red_sum(sm, m, c),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __syncthreads();
+        if (tid == 0) {
+          const uint32_t prev = __hip_atomic_fetch_add(&p.counters[T], 1u, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT);
+          sm.last = (prev == static_cast<uint32_t>(contributors - 1)) ? 1 : 0;
+        }
+        __syncthreads();
+        if (sm.last) {
+          for (int idx = tid; idx < kOut; idx += kThreads) {
+            const int m = idx / kTileCols;
+            const int c = idx % kTileCols;
+            if (row0 + m < p.M) {
+              float v = 0.0f;
+              for (int s = 0; s < contributors; ++s) {
+                v += __hip_atomic_load(&ws[static_cast<size_t>(s) * kOut + idx], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+              }
+              p.out[static_cast<size_t>(row0 + m) * p.N + col_base + c] = float_to_act_bits<A>(v);
+            }
+          }
+          if (tid == 0) {
+            __hip_atomic_store(&p.counters[T], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
         }
       }
-      if (tid == 0) {
-        __hip_atomic_store(&p.counters[tm], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+      __syncthreads();  // sm.red / sm.last are reused by the next segment
+      u += g_hi - g_lo;
     }
   }
 }
@@ -425,9 +524,17 @@ hipError_t launch_t(const GemvLaunch& l, hipStream_t stream) {
   p.mtiles = (l.M + MT - 1) / MT;
   p.splits = l.splits;
   p.gps = l.gps;
-  const int total = p.tiles * p.mtiles * p.splits;
-  p.xcd_remap = (total % 8 == 0) ? 1 : 0;
-  hipLaunchKernelGGL((w4a16_gemv_kernel<G, A, MT, MODE>), dim3(total), dim3(kThreads), 0, stream, p);
+  p.per = l.units_per_workgroup;
+  p.max_contrib = l.max_contributors;
+  int grid = 0;
+  if (MODE == GemvMode::kPartials) {
+    grid = p.tiles * p.mtiles * p.splits;
+  } else {
+    const long long total = static_cast<long long>(p.tiles) * p.mtiles * p.NG;
+    grid = static_cast<int>((total + p.per - 1) / p.per);
+  }
+  p.xcd_remap = (grid % 8 == 0) ? 1 : 0;
+  hipLaunchKernelGGL((w4a16_gemv_kernel<G, A, MT, MODE>), dim3(grid), dim3(kThreads), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -444,9 +551,8 @@ hipError_t dispatch_mt(const GemvLaunch& l, hipStream_t stream) {
 template <int G, Act A>
 hipError_t dispatch_mode(const GemvLaunch& l, hipStream_t stream) {
   switch (l.mode) {
-    case GemvMode::kDirect: return dispatch_mt<G, A, GemvMode::kDirect>(l, stream);
-    case GemvMode::kPartials: return dispatch_mt<G, A, GemvMode::kPartials>(l, stream);
-    default: return dispatch_mt<G, A, GemvMode::kFixup>(l, stream);
+    case GemvMode::kStreamK: return dispatch_mt<G, A, GemvMode::kStreamK>(l, stream);
+    default: return dispatch_mt<G, A, GemvMode::kPartials>(l, stream);
   }
 }
 

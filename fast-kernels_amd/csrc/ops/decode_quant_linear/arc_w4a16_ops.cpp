@@ -112,13 +112,9 @@ int device_cu_count() {
 }
 
 
-std::size_t fixup_workspace_bytes(int batch, int n, int m_tile, int splits) {
-  if (splits <= 1) {
-    return 0;
-  }
-  const std::size_t partials = fk::gemv_fixup_partial_floats(n, batch, m_tile, splits) * sizeof(float);
-  return kCounterRegionBytes + partials;
-}
+// Smallest run per workgroup: two groups per wave, so every wave has a buffered group behind
+// the one it computes.
+constexpr int kMinGroupsPerWorkgroup = 8;
 
 }  // namespace
 
@@ -134,35 +130,44 @@ ArcW4A16Plan plan_arc_w4a16_for_cu_count(int batch, int n, int k, int group_size
   }
   ArcW4A16Plan plan{};
   plan.m_tile = fk::gemv_m_tile_for_batch(batch);
-  if (activation_dtype == kActivationBF16) {
-    plan.m_tile = std::min(plan.m_tile, 4);  // the bf16 unpack needs more registers per row
-  }
   const int num_groups = k / group_size;
-  const int tiles = n / kTileCols;
-  const int mtiles = (batch + plan.m_tile - 1) / plan.m_tile;
-  const int base = tiles * mtiles;
-  int splits = 1;
+  const long long tiles = static_cast<long long>(fk::gemv_tiles(n, batch, plan.m_tile));
+  const long long units = tiles * num_groups;
+  long long per = 0;
   if (split_k_slices > 0) {
-    splits = std::min(split_k_slices, num_groups);
+    const int s_req = std::min(split_k_slices, num_groups);
+    per = (num_groups + s_req - 1) / s_req;
   } else {
-    // Aim for about four 4-wave workgroups per CU, with at least one group per wave; round the
-    // groups per workgroup to a multiple of the wave count so no wave idles inside a slice.
-    const int target = 4 * cu_count;
-    splits = (target + base - 1) / base;
-    splits = std::max(1, std::min(splits, std::max(1, num_groups / 4)));
+    // Split each tile into the largest power-of-two number of runs that still leaves at most one
+    // workgroup per CU and at least kMinGroupsPerWorkgroup groups per run. Measured on MI355X
+    // (Llama-7B/8B/70B decode shapes): one workgroup per CU streams at ~18-25 GB/s, a second
+    // one per CU adds little, and every extra run costs a fix-up round trip, so fewer, longer
+    // runs win once the CUs are covered; shapes with more tiles than CUs are not split.
+    long long s_split = 1;
+    while (tiles * s_split * 2 <= cu_count && num_groups / (s_split * 2) >= kMinGroupsPerWorkgroup) {
+      s_split *= 2;
+    }
+    per = (num_groups + s_split - 1) / s_split;
   }
-  int gps = (num_groups + splits - 1) / splits;
-  if (split_k_slices <= 0 && num_groups >= 4) {
-    gps = std::min(num_groups, (gps + 3) / 4 * 4);
+  const long long workgroups = (units + per - 1) / per;
+  if (workgroups > 0x7fffffffLL || per > 0x7fffffffLL) {
+    throw_invalid("shape too large for one launch");
   }
-  splits = (num_groups + gps - 1) / gps;
-  if (splits > 1 && fk::gemv_fixup_counters(n, batch, plan.m_tile) > kMaxFixupCounters) {
-    throw_invalid("n * ceil(batch / m_tile) / 128 exceeds the split-K counter capacity (16384)");
+  plan.workgroups = static_cast<int>(workgroups);
+  plan.groups_per_workgroup = static_cast<int>(per);
+  const bool aligned = per % num_groups == 0;  // every tile lies inside one run
+  plan.max_tile_contributors = aligned ? 1 : static_cast<int>((num_groups + per - 1) / per + 1);
+  if (aligned) {
+    plan.workspace_bytes = 0;
+  } else {
+    if (static_cast<std::size_t>(tiles) > kMaxFixupCounters) {
+      throw_invalid("n * ceil(batch / m_tile) / 128 exceeds the split tile capacity (16384)");
+    }
+    plan.workspace_bytes =
+        kCounterRegionBytes + fk::gemv_streamk_partial_floats(n, batch, plan.m_tile,
+                                                              plan.max_tile_contributors) *
+                                  sizeof(float);
   }
-  plan.split_k_slices = splits;
-  plan.groups_per_slice = gps;
-  plan.workgroups = base * splits;
-  plan.workspace_bytes = fixup_workspace_bytes(batch, n, plan.m_tile, splits);
   return plan;
 }
 
@@ -214,14 +219,12 @@ void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::u
   l.group_size = group_size;
   l.act = activation_dtype == kActivationBF16 ? fk::Act::kBF16 : fk::Act::kF16;
   l.m_tile = plan.m_tile;
-  l.splits = plan.split_k_slices;
-  l.gps = plan.groups_per_slice;
-  if (plan.split_k_slices > 1) {
-    l.mode = fk::GemvMode::kFixup;
+  l.mode = fk::GemvMode::kStreamK;
+  l.units_per_workgroup = plan.groups_per_workgroup;
+  l.max_contributors = plan.max_tile_contributors;
+  if (plan.workspace_bytes > 0) {
     l.counters = workspace;
     l.partials = static_cast<char*>(workspace) + kCounterRegionBytes;
-  } else {
-    l.mode = fk::GemvMode::kDirect;
   }
   check_hip(fk::launch_w4a16_gemv(l, stream), "w4a16_gemv launch");
 }

@@ -101,15 +101,16 @@ int fk_hipblaslt_fp16_after_dequant(const void* activations, const void* q, cons
 /* ---- additions with no reference counterpart (BASELINE extensions of the same path) ------ */
 
 typedef struct fk_arc_w4a16_plan {
-  int m_tile;             /* activation rows per workgroup */
-  int split_k_slices;     /* workgroups per 128-column tile along K (1 = no split) */
-  int groups_per_slice;
-  int workgroups;         /* grid size */
-  size_t workspace_bytes; /* workspace fk_arc_w4a16_forward_ex needs */
+  int m_tile;                /* activation rows per 128-column tile */
+  int workgroups;            /* grid size */
+  int groups_per_workgroup;  /* run of (tile, group) units each workgroup streams */
+  int max_tile_contributors; /* workgroups that can share one tile (1 = none shared) */
+  size_t workspace_bytes;    /* workspace fk_arc_w4a16_forward_ex needs */
 } fk_arc_w4a16_plan;
 
-/* Launch plan for a shape. split_k_slices = 0 selects the built-in policy. cu_count = 0 queries
- * the current device; a positive cu_count plans without touching the GPU. */
+/* Launch plan for a shape. split_k_slices = 0 selects the built-in policy (one resident round of
+ * equal runs); S > 0 gives every workgroup ceil(K/G/S) groups. cu_count = 0 queries the current
+ * device; a positive cu_count plans without touching the GPU. */
 int fk_arc_w4a16_plan_for(int batch, int n, int k, int group_size, int activation_dtype,
                           int split_k_slices, int cu_count, fk_arc_w4a16_plan* plan);
 

@@ -49,9 +49,9 @@ def test_library_exports_every_declared_symbol(lib: ctypes.CDLL) -> None:
 class Plan(ctypes.Structure):
     _fields_ = [
         ("m_tile", ctypes.c_int),
-        ("split_k_slices", ctypes.c_int),
-        ("groups_per_slice", ctypes.c_int),
         ("workgroups", ctypes.c_int),
+        ("groups_per_workgroup", ctypes.c_int),
+        ("max_tile_contributors", ctypes.c_int),
         ("workspace_bytes", ctypes.c_size_t),
     ]
 
@@ -62,20 +62,43 @@ def _plan(lib, batch, n, k, g, act=0, split=0, cu=256):
     return rc, p
 
 
-def test_plan_policy_without_gpu(lib: ctypes.CDLL) -> None:
-    rc, p = _plan(lib, 1, 57344, 8192, 128)
+@pytest.mark.parametrize(
+    "shape,want_runs_per_tile",
+    [
+        ((1, 57344, 8192, 128), 1),  # 448 tiles >= 256 CUs: whole tiles, no fix-up
+        ((1, 10240, 8192, 128), 2),  # 80 tiles -> 160 workgroups
+        ((1, 8192, 8192, 128), 4),   # 64 tiles -> 256 workgroups
+        ((1, 8192, 28672, 128), 4),  # 64 tiles -> 256 workgroups of 56 groups
+        ((1, 4096, 4096, 128), 4),   # 32 groups per tile: runs stay >= 8 groups
+        ((1, 4096, 14336, 128), 8),
+    ],
+)
+def test_plan_policy_without_gpu(lib: ctypes.CDLL, shape, want_runs_per_tile) -> None:
+    batch, n, k, g = shape
+    rc, p = _plan(lib, batch, n, k, g)
     assert rc == 0
-    assert p.m_tile == 1 and p.split_k_slices >= 1
-    assert p.split_k_slices * p.groups_per_slice >= 64
-    assert (p.split_k_slices - 1) * p.groups_per_slice < 64  # no empty slice
-    assert p.workgroups == (57344 // 128) * p.split_k_slices
+    ng = k // g
+    tiles = n // 128
+    assert p.m_tile == 1
+    assert p.groups_per_workgroup == -(-ng // want_runs_per_tile)
+    assert p.workgroups == -(-(tiles * ng) // p.groups_per_workgroup)
+    assert p.workgroups <= 256 or want_runs_per_tile == 1
+    if want_runs_per_tile == 1:
+        assert p.max_tile_contributors == 1 and p.workspace_bytes == 0
+    else:
+        assert p.workspace_bytes >= 65536 + tiles * 128 * 4 * p.max_tile_contributors
+
+
+def test_plan_batch_tiles_and_forced_split(lib: ctypes.CDLL) -> None:
     rc, p = _plan(lib, 16, 14336, 4096, 64)
     assert rc == 0 and p.m_tile == 8
-    rc, p = _plan(lib, 16, 14336, 4096, 64, act=1)
-    assert rc == 0 and p.m_tile == 4  # bf16 caps the rows per workgroup
+    rc, p = _plan(lib, 3, 14336, 4096, 64, act=1)
+    assert rc == 0 and p.m_tile == 4
+    # S = 7 slices of a 64-group tile: runs of ceil(64/7) = 10 groups straddle tile boundaries
     rc, p = _plan(lib, 1, 1024, 8192, 128, split=7)
-    assert rc == 0 and p.split_k_slices == 7 and p.groups_per_slice == 10
-    assert p.workspace_bytes >= 7 * 8 * 128 * 4
+    assert rc == 0 and p.groups_per_workgroup == 10
+    assert p.workgroups == -(-(8 * 64) // 10)
+    assert p.max_tile_contributors == 8
 
 
 @pytest.mark.parametrize(
