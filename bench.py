@@ -67,7 +67,27 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--eager", action="store_true", help="launch without a HIP graph")
+    p.add_argument(
+        "--copy-calibration",
+        action="store_true",
+        help="only run a plain 256 MiB device-to-device copy 10 times (scales rocprofv3 "
+        "FETCH_SIZE / WRITE_SIZE to bytes)",
+    )
     return p.parse_args()
+
+
+COPY_CALIBRATION_BYTES = 256 * 1024 * 1024
+
+
+def copy_calibration(torch) -> int:
+    src = torch.empty(COPY_CALIBRATION_BYTES, device="cuda", dtype=torch.uint8).random_(0, 255)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": COPY_CALIBRATION_BYTES, "launches": 10}))
+    return 0
 
 
 class ShapeBuffers:
@@ -144,6 +164,21 @@ def time_events(torch, run, reps: int) -> float:
     return float(start.elapsed_time(end))
 
 
+def measured_traffic(workload: str, shape: str):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 PMC summary
+    (profiles/w4a16_gemv_traffic.json, FETCH_SIZE + WRITE_SIZE scaled by a plain copy of known
+    size), or None when no measurement for this workload and shape is committed."""
+    path = REPO_ROOT / "profiles" / "w4a16_gemv_traffic.json"
+    if not path.exists():
+        return None
+    try:
+        data = json.loads(path.read_text())
+        entry = data[workload][shape]
+        return int(entry["hbm_bytes_per_launch"])
+    except (KeyError, ValueError, TypeError):
+        return None
+
+
 def cpu_baseline(workload: str, batch: int, seconds: float) -> dict:
     """The CPU oracle (C, OpenMP) on the same shapes, host-generated inputs, timed until at least
     `seconds` of work (whole passes over the four shapes)."""
@@ -195,6 +230,8 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
+    if args.copy_calibration:
+        return copy_calibration(torch)
     act, g, shapes = WORKLOADS[args.workload]
     if args.only:
         keep = set(args.only.split(","))
@@ -284,7 +321,7 @@ def main() -> int:
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(args.workload, dominant.name),
         },
     }
     if not args.no_cpu_baseline:
