@@ -213,6 +213,7 @@ PYBIND11_MODULE(_native, m) {
         d["groups_per_workgroup"] = plan.groups_per_workgroup;
         d["max_tile_contributors"] = plan.max_tile_contributors;
         d["workspace_bytes"] = plan.workspace_bytes;
+        d["slice_cols"] = plan.slice_cols;
         return d;
       },
       py::arg("batch"), py::arg("n"), py::arg("k"), py::arg("group_size"),

@@ -151,6 +151,7 @@ int fk_arc_w4a16_plan_for(int batch, int n, int k, int group_size, int activatio
     plan->groups_per_workgroup = p.groups_per_workgroup;
     plan->max_tile_contributors = p.max_tile_contributors;
     plan->workspace_bytes = p.workspace_bytes;
+    plan->slice_cols = p.slice_cols;
   });
 }
 

@@ -26,13 +26,15 @@ struct GemvLaunch {
   int splits = 1;               // kPartials
   int gps = 0;                  // kPartials: groups per split
   int units_per_workgroup = 0;  // kStreamK: group units per workgroup
-  int max_contributors = 0;     // kStreamK: partial slots per tile in the scratch
+  int max_contributors = 0;     // kStreamK: partial slots per slice in the scratch
+  int slice_cols = kTileCols;   // kStreamK: columns per workgroup slice (128, 64 or 32)
 };
 
 int gemv_m_tile_for_batch(int batch);
 
-// Tiles (128 columns x m_tile rows) of a launch; the stream-K scratch holds one counter and
-// max_contributors fp32 partial slots of m_tile x 128 floats per tile.
+// Tiles (128 columns x m_tile rows) of a launch; the stream-K scratch holds one counter per slice
+// (tiles x 128 / slice_cols) and max_contributors fp32 partial slots of m_tile x 128 floats per
+// tile (the slices of a tile share its slots' size).
 inline size_t gemv_tiles(int n, int batch, int m_tile) {
   return static_cast<size_t>(n / kTileCols) * static_cast<size_t>((batch + m_tile - 1) / m_tile);
 }

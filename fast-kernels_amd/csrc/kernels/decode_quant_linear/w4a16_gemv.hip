@@ -4,10 +4,15 @@
 // accumulation, output in the activation dtype (fp16 or bf16). Follows the math of the reference
 // hot loop (arc_w4a16.cu:222-297, accumulate_arc_group_range) but not its structure:
 //
-//  * 128-bit loads. A packet (arc_w4a16.cu:87-122) stores word w of column c at byte
-//    (w*128 + c)*4, so one 64-lane dwordx4 load covers two word rows x 128 columns: lane l holds
-//    word row 2i + (l>>5) for the four columns 4*(l&31) .. +3. A wave streams one whole group
-//    (G/16 loads) while the next group's loads are in flight.
+//  * 128-bit loads over column slices. A packet (arc_w4a16.cu:87-122) stores word w of column c
+//    at byte (w*128 + c)*4, so a word row is 512 contiguous bytes. A workgroup owns a slice of
+//    CW in {128, 64, 32} columns of a 128-column tile; one 64-lane dwordx4 load covers 256/CW word
+//    rows of the slice (CW*4 contiguous bytes each, whole 128-byte lines), and lane l holds the
+//    four columns 4*(l % (CW/4)) .. +3 of word row l / (CW/4). Narrow slices give small-N shapes
+//    enough workgroups to fill the chip without splitting K across workgroups.
+//  * A wave streams its own groups of the slice through D register buffers of one group each
+//    (D*G*CW/2048 = 16 dwordx4 loads in flight whatever CW), refilling each buffer as soon as
+//    it is consumed.
 //  * Register dequant with no per-element conversion: nibbles are OR-ed into fp16 mantissas
 //    (see w4a16_device.h) and multiplied by v_dot2_f32_f16 (fp32 accumulation) against
 //    activations re-paired once per workgroup in LDS. The constant bias the trick adds (1024 for
@@ -19,12 +24,11 @@
 //    exactly (bf16 has 8 significant bits, fp16 normals 11), so bf16 runs the same fp16 inner
 //    loop.
 //  * Stream-K work split: the grid is sized to be resident on the chip at once and each
-//    workgroup takes an equal run of (tile, group) units, crossing tile boundaries; tiles shared
-//    by several workgroups are finished in-kernel by their last contributor (see the kernel).
-//    Equal runs avoid both the load imbalance of whole-tile workgroups (448 tiles on 256 CUs)
-//    and a second round of short workgroups.
+//    workgroup takes an equal run of (slice, group) units, crossing slice boundaries; slices
+//    shared by several workgroups are finished in-kernel by their last contributor (see the
+//    kernel).
 //  * Logical workgroup order is remapped so that consecutive logical workgroups (the
-//    contributors of one tile) run on the same XCD: the hardware dispatches workgroup b to
+//    contributors of one slice) run on the same XCD: the hardware dispatches workgroup b to
 //    XCD b % 8.
 #include "w4a16_gemv.h"
 
@@ -40,29 +44,47 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-// Groups whose activations are staged in LDS at once: a whole split of K in the common M=1
-// plans, so a workgroup passes one barrier before streaming.
-#ifndef FK_GEMV_M1_CHUNK
-#define FK_GEMV_M1_CHUNK 32
-#endif
-template <int MT>
-constexpr int chunk_groups() {
-  return MT == 1 ? FK_GEMV_M1_CHUNK : 16;
+constexpr int kWordRowBytes = kTileCols * 4;
+
+// s_waitcnt immediate for gfx9 waiting until at most n vector-memory operations are outstanding:
+// vmcnt in bits 3:0 and 15:14, expcnt (6:4) and lgkmcnt (11:8) left at their maximum (no wait).
+constexpr int wait_vmcnt(int n) {
+  return (n & 0xF) | (((n >> 4) & 0x3) << 14) | 0x0F70;
 }
-// s_waitcnt immediate for gfx9: vmcnt = 0 (bits 3:0 and 15:14), expcnt and lgkmcnt left at max.
-constexpr int kWaitVmcnt0 = 0x0F70;
+constexpr int kWaitVmcnt0 = wait_vmcnt(0);
 // Largest bf16 biased exponent whose values all fit in fp16 (2^15 * (2 - 2^-7) < 65504).
 constexpr int kMaxFp16SafeBf16Exp = 142;
 
-template <int G, int MT>
+// Geometry of a CW-column slice of a G-group packet.
+template <int G, int CW>
+struct Slice {
+  static constexpr int kLanesPerRow = CW / 4;             // lanes covering one word row
+  static constexpr int kRowsPerLoad = 64 / kLanesPerRow;  // word rows per wave-wide load
+  static constexpr int kWordRows = G / 8;                 // word rows per group
+  static constexpr int kLoads = kWordRows / kRowsPerLoad;  // dwordx4 loads per group and lane
+  static constexpr int kDepth = 16 / kLoads;              // register buffers (groups in flight)
+  static constexpr int kSlices = kTileCols / CW;
+  static_assert(kLoads >= 1 && kWordRows % kRowsPerLoad == 0, "unsupported slice");
+};
+
+// Groups whose activations are staged in LDS at once. Wide slices run two workgroups per CU, so
+// their staging area stays small; narrow slices are used when there are fewer slices than CUs
+// (one workgroup per CU) and stage more of K per barrier.
+template <int MT, int CW>
+constexpr int chunk_groups() {
+  return MT > 1 ? 16 : (CW == kTileCols ? 32 : 64);
+}
+
+template <int G, int MT, int CW>
 struct Smem {
-  static constexpr int kChunk = chunk_groups<MT>();
+  static constexpr int kChunk = chunk_groups<MT, CW>();
   static constexpr int kWordRows = G / 8;
-  uint4 xs[MT][kChunk][kWordRows];  // re-paired fp16 activations, 16 B per word row
-  float4 sums[MT][kChunk];          // {even p0, odd p0, even p1, odd p1} of the staged values
-  float scale[MT][kChunk];          // power of two undoing the bf16 staging scale (1 for fp16)
-  float red[kWaves][MT][kTileCols]; // cross-wave reduction
-  int last;                         // this workgroup finishes the tile
+  static constexpr int kRowsPerLoad = Slice<G, CW>::kRowsPerLoad;
+  uint4 xs[MT][kChunk][kWordRows];        // re-paired fp16 activations, 16 B per word row
+  float2 sums[MT][kChunk][kRowsPerLoad];  // {even, odd} sums over word rows r mod kRowsPerLoad
+  float scale[MT][kChunk];                // power of two undoing the bf16 staging scale
+  float red[kWaves][MT][CW];              // cross-wave reduction
+  int last;                               // this workgroup finishes the slice
 };
 
 struct GemvParams {
@@ -70,36 +92,36 @@ struct GemvParams {
   const uint8_t* packets;  // [(N/128) * NG, S]
   uint16_t* out;           // [M, N] (unused in partials mode)
   float* partials;         // fix-up scratch or reference split-K partials [S_k, M, N]
-  uint32_t* counters;      // fix-up arrival counters, one per (tile, m-tile)
+  uint32_t* counters;      // fix-up arrival counters, one per (slice, m-tile)
   int M, N, K, NG;
   int tiles, mtiles, splits, gps;  // kPartials: fixed split of every tile
   int per;                          // stream-K: group units per workgroup
-  int max_contrib;                  // stream-K: partial slots per tile in the scratch
+  int max_contrib;                  // stream-K: partial slots per slice in the scratch
   int xcd_remap;
 };
 
-template <int G, int MT>
+template <int G, int MT, int CW>
 struct StageRegs {
-  static constexpr int kUnits = MT * chunk_groups<MT>() * (G / 8);
+  static constexpr int kUnits = MT * chunk_groups<MT, CW>() * (G / 8);
   static constexpr int kPerThread = (kUnits + kThreads - 1) / kThreads;
   uint4 raw[kPerThread];
 };
 
 // Issue the global loads of one chunk's activations (16 B = one word row per unit).
-template <int G, int MT>
-__device__ __forceinline__ void stage_load(StageRegs<G, MT>& st, const GemvParams& p, int row0,
+template <int G, int MT, int CW>
+__device__ __forceinline__ void stage_load(StageRegs<G, MT, CW>& st, const GemvParams& p, int row0,
                                            int g0, int n_chunk) {
   constexpr int WR = G / 8;
-  constexpr int kChunk = chunk_groups<MT>();
+  constexpr int kChunk = chunk_groups<MT, CW>();
   const int tid = static_cast<int>(threadIdx.x);
 #pragma unroll
-  for (int it = 0; it < StageRegs<G, MT>::kPerThread; ++it) {
+  for (int it = 0; it < StageRegs<G, MT, CW>::kPerThread; ++it) {
     const int u = it * kThreads + tid;
     const int w = u % WR;
     const int gl = (u / WR) % kChunk;
     const int m = u / (WR * kChunk);
     st.raw[it] = make_uint4(0u, 0u, 0u, 0u);
-    if (u < StageRegs<G, MT>::kUnits && gl < n_chunk && row0 + m < p.M) {
+    if (u < StageRegs<G, MT, CW>::kUnits && gl < n_chunk && row0 + m < p.M) {
       const size_t off = static_cast<size_t>(row0 + m) * p.K +
                          static_cast<size_t>(g0 + gl) * G + static_cast<size_t>(w) * 8;
       st.raw[it] = *reinterpret_cast<const uint4*>(p.x + off);
@@ -118,15 +140,17 @@ __device__ __forceinline__ uint32_t bf16_pair_to_half_pair(uint32_t w, float s) 
 }
 
 // Convert (bf16) and re-pair the staged activations into LDS and reduce the per-(row, group,
-// parity) sums. Rows of one (m, group) are WR consecutive, WR-aligned lanes, so xor-shuffles
-// over 1..WR/2 stay inside the group.
-template <int G, Act A, int MT>
-__device__ __forceinline__ void stage_store(Smem<G, MT>& sm, StageRegs<G, MT>& st, int n_chunk) {
+// word row mod R) sums, R = word rows per load. Word rows of one (m, group) are WR consecutive,
+// WR-aligned lanes, so xor-shuffles over R..WR/2 stay inside the group.
+template <int G, Act A, int MT, int CW>
+__device__ __forceinline__ void stage_store(Smem<G, MT, CW>& sm, StageRegs<G, MT, CW>& st,
+                                            int n_chunk) {
   constexpr int WR = G / 8;
-  constexpr int kChunk = chunk_groups<MT>();
+  constexpr int R = Slice<G, CW>::kRowsPerLoad;
+  constexpr int kChunk = chunk_groups<MT, CW>();
   const int tid = static_cast<int>(threadIdx.x);
 #pragma unroll
-  for (int it = 0; it < StageRegs<G, MT>::kPerThread; ++it) {
+  for (int it = 0; it < StageRegs<G, MT, CW>::kPerThread; ++it) {
     const int u = it * kThreads + tid;
     const int w = u % WR;
     const int gl = (u / WR) % kChunk;
@@ -157,16 +181,14 @@ __device__ __forceinline__ void stage_store(Smem<G, MT>& sm, StageRegs<G, MT>& s
                half_bits_to_float(static_cast<uint16_t>(r.z >> 16)) +
                half_bits_to_float(static_cast<uint16_t>(r.w >> 16));
 #pragma unroll
-    for (int off = 2; off < WR; off <<= 1) {
+    for (int off = R; off < WR; off <<= 1) {
       se += __shfl_xor(se, off);
       so += __shfl_xor(so, off);
     }
-    if (u < StageRegs<G, MT>::kUnits && gl < n_chunk) {
+    if (u < StageRegs<G, MT, CW>::kUnits && gl < n_chunk) {
       sm.xs[m][gl][w] = pair_activations(r);
-      if (w < 2) {
-        float* s = reinterpret_cast<float*>(&sm.sums[m][gl]);
-        s[2 * w + 0] = se;
-        s[2 * w + 1] = so;
+      if (w < R) {
+        sm.sums[m][gl][w] = make_float2(se, so);
       }
       if (w == 0) {
         sm.scale[m][gl] = undo;
@@ -188,35 +210,51 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <int G>
+template <int G, int CW>
 struct GroupLoad {
-  static constexpr int NL = G / 16;
+  static constexpr int NL = Slice<G, CW>::kLoads;
   uint4 w[NL];
   uint2 alpha;
   uint2 beta;
 };
 
-template <int G>
-__device__ __forceinline__ void load_group(GroupLoad<G>& gl, const uint8_t* packet, int lane) {
-  constexpr int QB = kTileCols * G / 2;
-  const int c0 = (lane & 31) * 4;
-  gl.alpha = *reinterpret_cast<const uint2*>(packet + QB + c0 * 2);
-  gl.beta = *reinterpret_cast<const uint2*>(packet + QB + kTileCols * 2 + c0 * 2);
-  const uint4* q = reinterpret_cast<const uint4*>(packet) + lane;
+// Per-lane constant parts of a group's addresses inside its packet.
+struct LaneAddr {
+  int code;   // byte offset of the lane's first 16 B of codes
+  int scale;  // byte offset of the lane's 4 alphas (the betas follow 256 bytes later)
+};
+
+template <int G, int CW>
+__device__ __forceinline__ LaneAddr lane_addr(int lane, int slice) {
+  constexpr int LPR = Slice<G, CW>::kLanesPerRow;
+  const int col = slice * CW + 4 * (lane % LPR);
+  LaneAddr a;
+  a.code = (lane / LPR) * kWordRowBytes + col * 4;
+  a.scale = kTileCols * G / 2 + col * 2;
+  return a;
+}
+
+template <int G, int CW>
+__device__ __forceinline__ void load_group(GroupLoad<G, CW>& gl, const uint8_t* packet,
+                                           LaneAddr la) {
+  constexpr int R = Slice<G, CW>::kRowsPerLoad;
+  gl.alpha = *reinterpret_cast<const uint2*>(packet + la.scale);
+  gl.beta = *reinterpret_cast<const uint2*>(packet + la.scale + kTileCols * 2);
 #pragma unroll
-  for (int i = 0; i < GroupLoad<G>::NL; ++i) {
-    gl.w[i] = q[i * 64];
+  for (int i = 0; i < GroupLoad<G, CW>::NL; ++i) {
+    gl.w[i] = *reinterpret_cast<const uint4*>(packet + la.code + i * R * kWordRowBytes);
   }
 }
 
 // One group: multiply-accumulate its codes against the staged activations, then apply the
 // group's scales and remove the unpack bias:
 // y += alpha * (acc_e - 1024 S_e) + alpha/16 * (acc_o - 1024 S_o) + beta * (S_e + S_o).
-template <int G, Act A, int MT>
-__device__ __forceinline__ void compute_group(const Smem<G, MT>& sm, const GroupLoad<G>& ld,
-                                              int gl, int parity, uint32_t mask_lo,
-                                              uint32_t mask_hi, float (&y)[MT][4]) {
-  constexpr int NL = G / 16;
+template <int G, Act A, int MT, int CW>
+__device__ __forceinline__ void compute_group(const Smem<G, MT, CW>& sm, const GroupLoad<G, CW>& ld,
+                                              int gl, int sub, uint32_t mask_lo, uint32_t mask_hi,
+                                              float (&y)[MT][4]) {
+  constexpr int NL = GroupLoad<G, CW>::NL;
+  constexpr int R = Slice<G, CW>::kRowsPerLoad;
   constexpr uint32_t kBias = 0x64006400u;  // fp16 1024.0 pair
   float acc_e[MT][4];
   float acc_o[MT][4];
@@ -231,7 +269,7 @@ __device__ __forceinline__ void compute_group(const Smem<G, MT>& sm, const Group
 
 #pragma unroll
   for (int i = 0; i < NL; ++i) {
-    const int wrow = 2 * i + parity;
+    const int wrow = i * R + sub;
     uint4 xp[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -269,12 +307,10 @@ __device__ __forceinline__ void compute_group(const Smem<G, MT>& sm, const Group
     const float co = fmaf(-64.0f, a, b);    // beta - 64 alpha
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-      const float4 s = sm.sums[m][gl];
-      const float se = parity ? s.z : s.x;
-      const float so = parity ? s.w : s.y;
-      float t = fmaf(a, acc_e[m][j], ce * se);
+      const float2 s = sm.sums[m][gl][sub];
+      float t = fmaf(a, acc_e[m][j], ce * s.x);
       t = fmaf(a16, acc_o[m][j], t);
-      t = fmaf(co, so, t);
+      t = fmaf(co, s.y, t);
       if constexpr (A == Act::kBF16) {
         t *= sm.scale[m][gl];
       }
@@ -284,87 +320,85 @@ __device__ __forceinline__ void compute_group(const Smem<G, MT>& sm, const Group
 }
 
 // Waves per SIMD the M=1 kernel must fit (caps its VGPRs at 512 / waves). Two is the measured
-// optimum: the double-buffered loop needs ~170 VGPRs, and capping lower spills registers.
-#ifndef FK_GEMV_M1_MIN_WAVES_PER_EU
-#define FK_GEMV_M1_MIN_WAVES_PER_EU 2
-#endif
+// optimum: the pipelined loop needs ~170-190 VGPRs, and capping lower spills registers.
 template <int MT>
 constexpr int min_waves_per_eu() {
-  return MT == 1 ? FK_GEMV_M1_MIN_WAVES_PER_EU : 1;
+  return MT == 1 ? 2 : 1;
 }
 
-// Accumulate groups [g_lo, g_hi) of one 128-column tile into y: stage the activations of up to
-// kChunk groups in LDS, then each wave streams groups g_lo + wave, g_lo + wave + 4, ...
-template <int G, Act A, int MT>
-__device__ __forceinline__ void stream_groups(Smem<G, MT>& sm, const GemvParams& p,
-                                              const uint8_t* tile_packets, int row0, int g_lo,
-                                              int g_hi, int lane, int wave, int parity,
+// Accumulate groups [g_lo, g_hi) of one slice into y: stage the activations of up to kChunk
+// groups in LDS, then each wave streams groups g_lo + wave, g_lo + wave + 4, ... through D
+// register buffers.
+template <int G, Act A, int MT, int CW>
+__device__ __forceinline__ void stream_groups(Smem<G, MT, CW>& sm, const GemvParams& p,
+                                              const uint8_t* tile_packets, LaneAddr la, int row0,
+                                              int g_lo, int g_hi, int wave, int sub,
                                               uint32_t mask_lo, uint32_t mask_hi,
                                               float (&y)[MT][4]) {
-  constexpr int kChunk = chunk_groups<MT>();
+  constexpr int kChunk = chunk_groups<MT, CW>();
+  constexpr int D = Slice<G, CW>::kDepth;
   const size_t stride = static_cast<size_t>(packet_stride_bytes(G));
   for (int g0 = g_lo; g0 < g_hi; g0 += kChunk) {
     const int n_chunk = min(kChunk, g_hi - g0);
     if (g0 != g_lo) {
       lds_barrier();  // previous chunk's readers are done with xs / sums
     }
-    // Activation loads first, then this wave's first weight groups, so the LDS writes below only
-    // wait for the activations while the weights stay in flight across the barrier.
-    StageRegs<G, MT> st;
-    stage_load<G, MT>(st, p, row0, g0, n_chunk);
-    // This wave's groups in the chunk: gl = wave, wave + 4, ... (n_w of them). Two register
-    // buffers alternate and each is refilled right after it is consumed, so one group's loads
-    // are always in flight behind the group being computed. The steady-state loop has no
-    // conditional loads, so the compiler keeps both buffers in place (no register copies that
-    // would force an early wait on loads still in flight).
+    // Activation loads first, then the first D weight groups of this wave, so the LDS writes
+    // below only wait for the activations while the weights stay in flight across the barrier.
+    StageRegs<G, MT, CW> st;
+    stage_load<G, MT, CW>(st, p, row0, g0, n_chunk);
+    // This wave's groups in the chunk: gl = wave + 4t, t < n_w; buffer d holds t = d mod D.
+    // Loads are unconditional (past its last group a wave re-reads that group, an L2 hit it
+    // does not compute), so the compiler can count the loads behind any buffer and wait for that
+    // buffer alone.
     const int n_w = n_chunk > wave ? (n_chunk - wave + kWaves - 1) / kWaves : 0;
-    const uint8_t* gp = tile_packets + static_cast<size_t>(g0 + wave) * stride;
+    const int t_last = max(n_w - 1, 0);
+    const int gl_base = n_w > 0 ? wave : n_chunk - 1;
+    const uint8_t* gp = tile_packets + static_cast<size_t>(g0 + gl_base) * stride;
     const size_t step = static_cast<size_t>(kWaves) * stride;
-    GroupLoad<G> buf_a;
-    GroupLoad<G> buf_b;
-    if (n_w > 0) {
-      load_group<G>(buf_a, gp, lane);
+    GroupLoad<G, CW> buf[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      load_group<G, CW>(buf[d], gp + static_cast<size_t>(min(d, t_last)) * step, la);
     }
-    stage_store<G, A, MT>(sm, st, n_chunk);
-    if (n_w > 1) {
-      load_group<G>(buf_b, gp + step, lane);
-    }
+    __builtin_amdgcn_sched_barrier(0);  // keep every load above the first use of the activations
+    stage_store<G, A, MT, CW>(sm, st, n_chunk);
     lds_barrier();
-    int t = 0;
-    for (; t + 3 < n_w; t += 2) {
-      compute_group<G, A, MT>(sm, buf_a, wave + t * kWaves, parity, mask_lo, mask_hi, y);
-      load_group<G>(buf_a, gp + static_cast<size_t>(t + 2) * step, lane);
-      compute_group<G, A, MT>(sm, buf_b, wave + (t + 1) * kWaves, parity, mask_lo, mask_hi, y);
-      load_group<G>(buf_b, gp + static_cast<size_t>(t + 3) * step, lane);
+    // Blocks of D groups; every block but the last refills each buffer right after computing it.
+    const int n_blocks = (n_w + D - 1) / D;
+    int t0 = 0;
+    for (int blk = 0; blk + 1 < n_blocks; ++blk, t0 += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        compute_group<G, A, MT, CW>(sm, buf[d], wave + (t0 + d) * kWaves, sub, mask_lo, mask_hi, y);
+        load_group<G, CW>(buf[d], gp + static_cast<size_t>(min(t0 + D + d, t_last)) * step, la);
+      }
     }
-    // 0..3 groups remain: t and t+1 are loaded, t+2 is not.
-    if (t < n_w) {
-      compute_group<G, A, MT>(sm, buf_a, wave + t * kWaves, parity, mask_lo, mask_hi, y);
-      if (t + 2 < n_w) {
-        load_group<G>(buf_a, gp + static_cast<size_t>(t + 2) * step, lane);
-      }
-      if (t + 1 < n_w) {
-        compute_group<G, A, MT>(sm, buf_b, wave + (t + 1) * kWaves, parity, mask_lo, mask_hi, y);
-      }
-      if (t + 2 < n_w) {
-        compute_group<G, A, MT>(sm, buf_a, wave + (t + 2) * kWaves, parity, mask_lo, mask_hi, y);
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      if (t0 + d < n_w) {
+        compute_group<G, A, MT, CW>(sm, buf[d], wave + (t0 + d) * kWaves, sub, mask_lo, mask_hi, y);
       }
     }
   }
 }
 
-// Sum y over the lanes l / l^32 (the two word-row parities) and the 4 waves into sm.red.
-template <int G, int MT>
-__device__ __forceinline__ void reduce_to_lds(Smem<G, MT>& sm, float (&y)[MT][4], int lane,
-                                              int wave, int parity) {
+// Sum y over the lanes that share columns (different word rows) and over the waves into sm.red.
+template <int G, int MT, int CW>
+__device__ __forceinline__ void reduce_to_lds(Smem<G, MT, CW>& sm, float (&y)[MT][4], int lane,
+                                              int wave) {
+  constexpr int LPR = Slice<G, CW>::kLanesPerRow;
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      y[m][j] += __shfl_xor(y[m][j], 32);
+#pragma unroll
+      for (int off = LPR; off < 64; off <<= 1) {
+        y[m][j] += __shfl_xor(y[m][j], off);
+      }
     }
   }
-  if (parity == 0) {
+  if (lane < LPR) {
     const int c0 = lane * 4;
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -374,36 +408,43 @@ __device__ __forceinline__ void reduce_to_lds(Smem<G, MT>& sm, float (&y)[MT][4]
   __syncthreads();
 }
 
-template <int G, int MT>
-__device__ __forceinline__ float red_sum(const Smem<G, MT>& sm, int m, int c) {
-  return sm.red[0][m][c] + sm.red[1][m][c] + sm.red[2][m][c] + sm.red[3][m][c];
+template <int G, int MT, int CW>
+__device__ __forceinline__ float red_sum(const Smem<G, MT, CW>& sm, int m, int c) {
+  float v = sm.red[0][m][c];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) {
+    v += sm.red[w][m][c];
+  }
+  return v;
 }
 
-// Work decomposition. The (tile, m-tile) pairs laid end to end form a line of T*NG group units
-// (T = tiles * mtiles). Workgroup b owns units [b*per, (b+1)*per): "stream-K", every workgroup
-// gets the same number of groups whatever the shape, and the grid is sized to fit on the chip
-// at once, so no workgroup waits for a second round. A tile whose units all belong to one
-// workgroup is written directly. A tile split between workgroups is finished by the last of its
-// contributors to arrive (device-scope counter), which adds the fp32 partials in workgroup
-// order, so results do not depend on arrival order; it also resets the counter, so no memset is
-// needed between calls (graph-capture friendly).
+// Work decomposition. A "slice" is CW columns of a 128-column tile for one m-tile of rows; the
+// slices laid end to end (slices of a tile, then tiles, then m-tiles) form a line of T*NG group
+// units. Workgroup b owns units [b*per, (b+1)*per): "stream-K", every workgroup gets the same
+// number of groups whatever the shape, and the grid is sized to fit on the chip at once, so no
+// workgroup waits for a second round. A slice whose units all belong to one workgroup is written
+// directly. A slice split between workgroups is finished by the last of its contributors to
+// arrive (device-scope counter), which adds the fp32 partials in workgroup order, so results do
+// not depend on arrival order; it also resets the counter, so no memset is needed between calls
+// (graph-capture friendly).
 //
-// kPartials (the reference split-K protocol) instead writes each workgroup's fp32 partial to
-// partials[split, m, n] with split = b % splits over a fixed per-tile split.
-template <int G, Act A, int MT, GemvMode MODE>
+// kPartials (the reference split-K protocol, whole tiles) instead writes each workgroup's fp32
+// partial to partials[split, m, n] with split = b % splits over a fixed per-tile split.
+template <int G, Act A, int MT, GemvMode MODE, int CW>
 __global__ void __launch_bounds__(kThreads, min_waves_per_eu<MT>())
 w4a16_gemv_kernel(GemvParams p) {
-  constexpr int kOut = MT * kTileCols;
-  __shared__ Smem<G, MT> sm;
+  constexpr int kOut = MT * CW;
+  constexpr int kSlices = Slice<G, CW>::kSlices;
+  __shared__ Smem<G, MT, CW> sm;
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int parity = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
+  const int sub = lane / Slice<G, CW>::kLanesPerRow;         // word row within a load
   const uint32_t mask_lo = vgpr_constant(0x000f000fu);
   const uint32_t mask_hi = vgpr_constant(0x00f000f0u);
   const size_t stride = static_cast<size_t>(packet_stride_bytes(G));
 
-  // Logical workgroup id: keep consecutive ids (the contributors of one tile) on one XCD.
+  // Logical workgroup id: keep consecutive ids (the contributors of one slice) on one XCD.
   const int grid = static_cast<int>(gridDim.x);
   int b = static_cast<int>(blockIdx.x);
   if (p.xcd_remap) {
@@ -411,6 +452,7 @@ w4a16_gemv_kernel(GemvParams p) {
   }
 
   if constexpr (MODE == GemvMode::kPartials) {
+    static_assert(CW == kTileCols, "the partials protocol runs on whole tiles");
     const int split = b % p.splits;
     const int T = b / p.splits;
     const int tile = T % p.tiles;
@@ -419,12 +461,12 @@ w4a16_gemv_kernel(GemvParams p) {
     const int g_hi = min(p.NG, g_lo + p.gps);
     float y[MT][4] = {};
     const uint8_t* tile_packets = p.packets + static_cast<size_t>(tile) * p.NG * stride;
-    stream_groups<G, A, MT>(sm, p, tile_packets, row0, g_lo, g_hi, lane, wave, parity, mask_lo,
-                            mask_hi, y);
-    reduce_to_lds<G, MT>(sm, y, lane, wave, parity);
+    stream_groups<G, A, MT, CW>(sm, p, tile_packets, lane_addr<G, CW>(lane, 0), row0, g_lo, g_hi,
+                                wave, sub, mask_lo, mask_hi, y);
+    reduce_to_lds<G, MT, CW>(sm, y, lane, wave);
     for (int idx = tid; idx < kOut; idx += kThreads) {
-      const int m = idx / kTileCols;
-      const int c = idx % kTileCols;
+      const int m = idx / CW;
+      const int c = idx % CW;
       if (row0 + m < p.M) {
         p.partials[(static_cast<size_t>(split) * p.M + row0 + m) * p.N + tile * kTileCols + c] =
             red_sum(sm, m, c);
@@ -432,7 +474,7 @@ w4a16_gemv_kernel(GemvParams p) {
     }
     return;
   } else {
-    const long long total_units = static_cast<long long>(p.tiles) * p.mtiles * p.NG;
+    const long long total_units = static_cast<long long>(p.tiles) * kSlices * p.mtiles * p.NG;
     const long long u_begin = static_cast<long long>(b) * p.per;
     const long long u_end = min(total_units, u_begin + p.per);
     long long u = u_begin;
@@ -440,22 +482,23 @@ w4a16_gemv_kernel(GemvParams p) {
       const int T = static_cast<int>(u / p.NG);
       const int g_lo = static_cast<int>(u - static_cast<long long>(T) * p.NG);
       const int g_hi = static_cast<int>(min(static_cast<long long>(p.NG), g_lo + (u_end - u)));
-      const int tile = T % p.tiles;
-      const int row0 = (T / p.tiles) * MT;
-      const int col_base = tile * kTileCols;
+      const int slice = T % kSlices;
+      const int tile = (T / kSlices) % p.tiles;
+      const int row0 = (T / (kSlices * p.tiles)) * MT;
+      const int col_base = tile * kTileCols + slice * CW;
       float y[MT][4] = {};
       const uint8_t* tile_packets = p.packets + static_cast<size_t>(tile) * p.NG * stride;
-      stream_groups<G, A, MT>(sm, p, tile_packets, row0, g_lo, g_hi, lane, wave, parity,
-                              mask_lo, mask_hi, y);
-      reduce_to_lds<G, MT>(sm, y, lane, wave, parity);
+      stream_groups<G, A, MT, CW>(sm, p, tile_packets, lane_addr<G, CW>(lane, slice), row0, g_lo,
+                                  g_hi, wave, sub, mask_lo, mask_hi, y);
+      reduce_to_lds<G, MT, CW>(sm, y, lane, wave);
 
-      const long long tile_u0 = static_cast<long long>(T) * p.NG;
-      const int first = static_cast<int>(tile_u0 / p.per);
-      const int last = static_cast<int>((tile_u0 + p.NG - 1) / p.per);
+      const long long slice_u0 = static_cast<long long>(T) * p.NG;
+      const int first = static_cast<int>(slice_u0 / p.per);
+      const int last = static_cast<int>((slice_u0 + p.NG - 1) / p.per);
       if (first == last) {
         for (int idx = tid; idx < kOut; idx += kThreads) {
-          const int m = idx / kTileCols;
-          const int c = idx % kTileCols;
+          const int m = idx / CW;
+          const int c = idx % CW;
           if (row0 + m < p.M) {
             p.out[static_cast<size_t>(row0 + m) * p.N + col_base + c] =
                 float_to_act_bits<A>(red_sum(sm, m, c));
@@ -471,8 +514,8 @@ w4a16_gemv_kernel(GemvParams p) {
         const int contributors = last - first + 1;
         float* ws = p.partials + static_cast<size_t>(T) * p.max_contrib * kOut;
         for (int idx = tid; idx < kOut; idx += kThreads) {
-          const int m = idx / kTileCols;
-          const int c = idx % kTileCols;
+          const int m = idx / CW;
+          const int c = idx % CW;
           __hip_atomic_store(&ws[static_cast<size_t>(b - first) * kOut + idx], red_sum(sm, m, c),
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -486,8 +529,8 @@ w4a16_gemv_kernel(GemvParams p) {
         __syncthreads();
         if (sm.last) {
           for (int idx = tid; idx < kOut; idx += kThreads) {
-            const int m = idx / kTileCols;
-            const int c = idx % kTileCols;
+            const int m = idx / CW;
+            const int c = idx % CW;
             if (row0 + m < p.M) {
               float v = 0.0f;
               for (int s = 0; s < contributors; ++s) {
@@ -508,7 +551,7 @@ w4a16_gemv_kernel(GemvParams p) {
   }
 }
 
-template <int G, Act A, int MT, GemvMode MODE>
+template <int G, Act A, int MT, GemvMode MODE, int CW>
 hipError_t launch_t(const GemvLaunch& l, hipStream_t stream) {
   GemvParams p;
   p.x = static_cast<const uint16_t*>(l.x);
@@ -530,29 +573,42 @@ hipError_t launch_t(const GemvLaunch& l, hipStream_t stream) {
   if (MODE == GemvMode::kPartials) {
     grid = p.tiles * p.mtiles * p.splits;
   } else {
-    const long long total = static_cast<long long>(p.tiles) * p.mtiles * p.NG;
+    const long long total = static_cast<long long>(p.tiles) * (kTileCols / CW) * p.mtiles * p.NG;
     grid = static_cast<int>((total + p.per - 1) / p.per);
   }
   p.xcd_remap = (grid % 8 == 0) ? 1 : 0;
-  hipLaunchKernelGGL((w4a16_gemv_kernel<G, A, MT, MODE>), dim3(grid), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((w4a16_gemv_kernel<G, A, MT, MODE, CW>), dim3(grid), dim3(kThreads), 0,
+                     stream, p);
   return hipGetLastError();
 }
 
-template <int G, Act A, GemvMode MODE>
-hipError_t dispatch_mt(const GemvLaunch& l, hipStream_t stream) {
-  switch (l.m_tile) {
-    case 1: return launch_t<G, A, 1, MODE>(l, stream);
-    case 2: return launch_t<G, A, 2, MODE>(l, stream);
-    case 4: return launch_t<G, A, 4, MODE>(l, stream);
-    default: return launch_t<G, A, 8, MODE>(l, stream);
+template <int G, Act A, int MT>
+hipError_t dispatch_cw(const GemvLaunch& l, hipStream_t stream) {
+  if (l.mode == GemvMode::kPartials) {
+    return launch_t<G, A, MT, GemvMode::kPartials, kTileCols>(l, stream);
   }
+  // Narrow slices serve the small-N shapes of decode (one or two activation rows); with more rows
+  // a tile's registers per lane grow with MT and the narrow-slice buffers would spill.
+  if constexpr (MT <= 2) {
+    switch (l.slice_cols) {
+      case 32: return launch_t<G, A, MT, GemvMode::kStreamK, 32>(l, stream);
+      case 64: return launch_t<G, A, MT, GemvMode::kStreamK, 64>(l, stream);
+      default: break;
+    }
+  }
+  if (l.slice_cols != kTileCols) {
+    return hipErrorInvalidValue;
+  }
+  return launch_t<G, A, MT, GemvMode::kStreamK, kTileCols>(l, stream);
 }
 
 template <int G, Act A>
-hipError_t dispatch_mode(const GemvLaunch& l, hipStream_t stream) {
-  switch (l.mode) {
-    case GemvMode::kStreamK: return dispatch_mt<G, A, GemvMode::kStreamK>(l, stream);
-    default: return dispatch_mt<G, A, GemvMode::kPartials>(l, stream);
+hipError_t dispatch_mt(const GemvLaunch& l, hipStream_t stream) {
+  switch (l.m_tile) {
+    case 1: return dispatch_cw<G, A, 1>(l, stream);
+    case 2: return dispatch_cw<G, A, 2>(l, stream);
+    case 4: return dispatch_cw<G, A, 4>(l, stream);
+    default: return dispatch_cw<G, A, 8>(l, stream);
   }
 }
 
@@ -566,12 +622,18 @@ int gemv_m_tile_for_batch(int batch) {
 }
 
 hipError_t launch_w4a16_gemv(const GemvLaunch& l, hipStream_t stream) {
-  if (l.group_size == 64) {
-    return l.act == Act::kF16 ? dispatch_mode<64, Act::kF16>(l, stream)
-                              : dispatch_mode<64, Act::kBF16>(l, stream);
+  if (l.slice_cols != 32 && l.slice_cols != 64 && l.slice_cols != kTileCols) {
+    return hipErrorInvalidValue;
   }
-  return l.act == Act::kF16 ? dispatch_mode<128, Act::kF16>(l, stream)
-                            : dispatch_mode<128, Act::kBF16>(l, stream);
+  if (l.mode == GemvMode::kPartials && l.slice_cols != kTileCols) {
+    return hipErrorInvalidValue;
+  }
+  if (l.group_size == 64) {
+    return l.act == Act::kF16 ? dispatch_mt<64, Act::kF16>(l, stream)
+                              : dispatch_mt<64, Act::kBF16>(l, stream);
+  }
+  return l.act == Act::kF16 ? dispatch_mt<128, Act::kF16>(l, stream)
+                            : dispatch_mt<128, Act::kBF16>(l, stream);
 }
 
 }  // namespace fk

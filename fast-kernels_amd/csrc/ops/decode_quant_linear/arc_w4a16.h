@@ -70,13 +70,14 @@ struct ArcW4A16Plan {
   int m_tile;                   // activation rows per tile
   int workgroups;               // grid size
   int groups_per_workgroup;     // stream-K run length in (tile, group) units
-  int max_tile_contributors;    // workgroups that can share one tile
+  int max_tile_contributors;    // workgroups that can share one slice
   std::size_t workspace_bytes;  // caller workspace needed by arc_w4a16_forward_ex
+  int slice_cols;               // columns per workgroup slice of a tile (128, 64 or 32)
 };
 
 // The launch the GEMV will use for this shape on the current device. split_k_slices = 0 picks
-// the built-in policy; S > 0 gives every workgroup ceil(K / G / S) groups (each tile is then
-// shared by about S workgroups).
+// the built-in policy; S > 0 gives every workgroup ceil(K / G / S) groups of whole 128-column
+// tiles (each tile is then shared by about S workgroups).
 ArcW4A16Plan plan_arc_w4a16(int batch, int n, int k, int group_size, int activation_dtype,
                             int split_k_slices);
 // The same policy for a given CU count, with no device query (host-only, testable without a GPU).

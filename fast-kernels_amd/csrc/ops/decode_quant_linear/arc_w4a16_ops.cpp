@@ -115,6 +115,11 @@ int device_cu_count() {
 // Smallest run per workgroup: two groups per wave, so every wave has a buffered group behind
 // the one it computes.
 constexpr int kMinGroupsPerWorkgroup = 8;
+// Longest run the automatic policy gives a workgroup before splitting K further: one staging
+// chunk of activations for narrow slices.
+constexpr int kMaxRunGroups = 64;
+// Narrowest column slice (the GEMV kernel serves 128, 64 and 32 columns per workgroup).
+constexpr int kMaxSlicesPerTile = 4;
 
 }  // namespace
 
@@ -132,35 +137,52 @@ ArcW4A16Plan plan_arc_w4a16_for_cu_count(int batch, int n, int k, int group_size
   plan.m_tile = fk::gemv_m_tile_for_batch(batch);
   const int num_groups = k / group_size;
   const long long tiles = static_cast<long long>(fk::gemv_tiles(n, batch, plan.m_tile));
-  const long long units = tiles * num_groups;
+  long long slices = 1;
   long long per = 0;
   if (split_k_slices > 0) {
     const int s_req = std::min(split_k_slices, num_groups);
     per = (num_groups + s_req - 1) / s_req;
   } else {
-    // Split each tile into the largest power-of-two number of runs that still leaves at most one
-    // workgroup per CU and at least kMinGroupsPerWorkgroup groups per run. Measured on MI355X
-    // (Llama-7B/8B/70B decode shapes): one workgroup per CU streams at ~18-25 GB/s, a second
-    // one per CU adds little, and every extra run costs a fix-up round trip, so fewer, longer
-    // runs win once the CUs are covered; shapes with more tiles than CUs are not split.
+    // Measured on MI355X over the Llama-7B/8B/70B decode shapes (M = 1): one workgroup per CU
+    // with long runs is best. Shapes with at least as many tiles as half the CUs run whole tiles
+    // over all of K. Otherwise K is split (power of two) until runs are at most kMaxRunGroups
+    // long while the runs still fit on the CUs, and then tiles are cut into 64- or 32-column
+    // slices while those fit: narrow slices add workgroups without the cross-workgroup fix-up a
+    // K split costs. With several activation rows per tile (more arithmetic per byte) K is split
+    // further while workgroups still fit.
     long long s_split = 1;
-    while (tiles * s_split * 2 <= cu_count && num_groups / (s_split * 2) >= kMinGroupsPerWorkgroup) {
+    auto can_split = [&](long long s) {
+      return tiles * slices * s * 2 <= cu_count && num_groups / (s * 2) >= kMinGroupsPerWorkgroup;
+    };
+    while (num_groups / s_split > kMaxRunGroups && can_split(s_split)) {
       s_split *= 2;
+    }
+    if (plan.m_tile <= 2) {
+      while (slices < kMaxSlicesPerTile && tiles * s_split * slices * 2 <= cu_count) {
+        slices *= 2;
+      }
+    }
+    if (plan.m_tile > 1) {
+      while (can_split(s_split)) {
+        s_split *= 2;
+      }
     }
     per = (num_groups + s_split - 1) / s_split;
   }
+  plan.slice_cols = static_cast<int>(fk::kTileCols / slices);
+  const long long units = tiles * slices * num_groups;
   const long long workgroups = (units + per - 1) / per;
   if (workgroups > 0x7fffffffLL || per > 0x7fffffffLL) {
     throw_invalid("shape too large for one launch");
   }
   plan.workgroups = static_cast<int>(workgroups);
   plan.groups_per_workgroup = static_cast<int>(per);
-  const bool aligned = per % num_groups == 0;  // every tile lies inside one run
+  const bool aligned = per % num_groups == 0;  // every slice lies inside one run
   plan.max_tile_contributors = aligned ? 1 : static_cast<int>((num_groups + per - 1) / per + 1);
   if (aligned) {
     plan.workspace_bytes = 0;
   } else {
-    if (static_cast<std::size_t>(tiles) > kMaxFixupCounters) {
+    if (static_cast<std::size_t>(tiles * slices) > kMaxFixupCounters) {
       throw_invalid("n * ceil(batch / m_tile) / 128 exceeds the split tile capacity (16384)");
     }
     plan.workspace_bytes =
@@ -222,6 +244,7 @@ void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::u
   l.mode = fk::GemvMode::kStreamK;
   l.units_per_workgroup = plan.groups_per_workgroup;
   l.max_contributors = plan.max_tile_contributors;
+  l.slice_cols = plan.slice_cols;
   if (plan.workspace_bytes > 0) {
     l.counters = workspace;
     l.partials = static_cast<char*>(workspace) + kCounterRegionBytes;

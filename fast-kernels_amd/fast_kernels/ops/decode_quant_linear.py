@@ -155,7 +155,8 @@ def arc_w4a16_plan(
     split_k_slices: int = 0,
     cu_count: int = 0,
 ) -> dict[str, int]:
-    """Launch plan (m_tile, split_k_slices, groups_per_slice, workgroups, workspace_bytes)."""
+    """Launch plan: m_tile, workgroups, groups_per_workgroup, max_tile_contributors,
+    workspace_bytes and slice_cols (columns of a tile per workgroup)."""
     native = native_module()
     return dict(
         native.arc_w4a16_plan(

@@ -104,8 +104,9 @@ typedef struct fk_arc_w4a16_plan {
   int m_tile;                /* activation rows per 128-column tile */
   int workgroups;            /* grid size */
   int groups_per_workgroup;  /* run of (tile, group) units each workgroup streams */
-  int max_tile_contributors; /* workgroups that can share one tile (1 = none shared) */
+  int max_tile_contributors; /* workgroups that can share one slice (1 = none shared) */
   size_t workspace_bytes;    /* workspace fk_arc_w4a16_forward_ex needs */
+  int slice_cols;            /* columns of a tile per workgroup slice: 128, 64 or 32 */
 } fk_arc_w4a16_plan;
 
 /* Launch plan for a shape. split_k_slices = 0 selects the built-in policy (one resident round of

@@ -53,6 +53,7 @@ class Plan(ctypes.Structure):
         ("groups_per_workgroup", ctypes.c_int),
         ("max_tile_contributors", ctypes.c_int),
         ("workspace_bytes", ctypes.c_size_t),
+        ("slice_cols", ctypes.c_int),
     ]
 
 
@@ -63,30 +64,31 @@ def _plan(lib, batch, n, k, g, act=0, split=0, cu=256):
 
 
 @pytest.mark.parametrize(
-    "shape,want_runs_per_tile",
+    "shape,want_runs_per_tile,want_slice_cols",
     [
-        ((1, 57344, 8192, 128), 1),  # 448 tiles >= 256 CUs: whole tiles, no fix-up
-        ((1, 10240, 8192, 128), 2),  # 80 tiles -> 160 workgroups
-        ((1, 8192, 8192, 128), 4),   # 64 tiles -> 256 workgroups
-        ((1, 8192, 28672, 128), 4),  # 64 tiles -> 256 workgroups of 56 groups
-        ((1, 4096, 4096, 128), 4),   # 32 groups per tile: runs stay >= 8 groups
-        ((1, 4096, 14336, 128), 8),
+        ((1, 57344, 8192, 128), 1, 128),  # 448 tiles >= 128: whole tiles over all of K, no fix-up
+        ((1, 10240, 8192, 128), 1, 64),   # 80 tiles -> 160 64-column slices
+        ((1, 8192, 8192, 128), 1, 32),    # 64 tiles -> 256 32-column slices
+        ((1, 8192, 28672, 128), 4, 128),  # 224 groups: runs of 56 groups, 256 workgroups
+        ((1, 4096, 4096, 128), 1, 32),    # 32 tiles -> 128 slices, no K split
+        ((1, 4096, 14336, 128), 2, 32),   # 112 groups: runs of 56, 4 slices -> 256 workgroups
     ],
 )
-def test_plan_policy_without_gpu(lib: ctypes.CDLL, shape, want_runs_per_tile) -> None:
+def test_plan_policy_without_gpu(lib: ctypes.CDLL, shape, want_runs_per_tile, want_slice_cols) -> None:
     batch, n, k, g = shape
     rc, p = _plan(lib, batch, n, k, g)
     assert rc == 0
     ng = k // g
-    tiles = n // 128
+    slices = (n // 128) * (128 // want_slice_cols)
     assert p.m_tile == 1
+    assert p.slice_cols == want_slice_cols
     assert p.groups_per_workgroup == -(-ng // want_runs_per_tile)
-    assert p.workgroups == -(-(tiles * ng) // p.groups_per_workgroup)
+    assert p.workgroups == -(-(slices * ng) // p.groups_per_workgroup)
     assert p.workgroups <= 256 or want_runs_per_tile == 1
     if want_runs_per_tile == 1:
         assert p.max_tile_contributors == 1 and p.workspace_bytes == 0
     else:
-        assert p.workspace_bytes >= 65536 + tiles * 128 * 4 * p.max_tile_contributors
+        assert p.workspace_bytes >= 65536 + (n // 128) * 128 * 4 * p.max_tile_contributors
 
 
 def test_plan_batch_tiles_and_forced_split(lib: ctypes.CDLL) -> None:
@@ -96,7 +98,7 @@ def test_plan_batch_tiles_and_forced_split(lib: ctypes.CDLL) -> None:
     assert rc == 0 and p.m_tile == 4
     # S = 7 slices of a 64-group tile: runs of ceil(64/7) = 10 groups straddle tile boundaries
     rc, p = _plan(lib, 1, 1024, 8192, 128, split=7)
-    assert rc == 0 and p.groups_per_workgroup == 10
+    assert rc == 0 and p.groups_per_workgroup == 10 and p.slice_cols == 128
     assert p.workgroups == -(-(8 * 64) // 10)
     assert p.max_tile_contributors == 8
 

@@ -150,6 +150,30 @@ def test_forward_baseline_shapes_match_oracle(shape: tuple[int, int, int, int]) 
     _assert_gemv_close(y, ref, case, f"{shape}")
 
 
+@pytest.mark.parametrize(
+    "shape,act,asym,want",
+    [
+        # (batch, n, k, G), activation, asymmetric, (slice_cols, groups per workgroup) on 256 CUs
+        ((1, 1024, 2048, 128), "f16", False, (32, 16)),    # 8 tiles -> 32 narrow slices
+        ((1, 10240, 4096, 128), "f16", True, (64, 32)),    # 80 tiles -> 160 64-column slices
+        ((1, 4096, 14336, 128), "bf16", False, (32, 56)),  # narrow slices + K split (fix-up)
+        ((2, 4096, 4096, 64), "f16", True, (32, 32)),      # two rows, narrow slices + K split
+        ((2, 1024, 8192, 64), "bf16", True, (32, 16)),     # two rows, 8 runs per slice
+    ],
+)
+def test_forward_column_slices_match_oracle(shape, act, asym, want) -> None:
+    """The automatic plan's 64- and 32-column slices, alone and with K split across workgroups."""
+    batch, n, k, g = shape
+    plan = arc_w4a16_plan(batch=batch, n=n, k=k, group_size=g,
+                          activation_dtype=torch.float16 if act == "f16" else torch.bfloat16)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert (plan["slice_cols"], plan["groups_per_workgroup"]) == want
+    case = make_case(batch, n, k, g, act=act, asymmetric=asym)
+    y = _run_forward(case)
+    ref, _ = oracle.gemv(case.x, case.q_u8, case.alpha, case.beta, g, act)
+    _assert_gemv_close(y, ref, case, f"{shape} {act} plan={plan}")
+
+
 @pytest.mark.parametrize("act", ["f16", "bf16"])
 @pytest.mark.parametrize("shape", [(1, 57344, 8192, 128), (1, 8192, 28672, 128)])
 def test_forward_llama70b_large_rows_subset(act: str, shape: tuple[int, int, int, int]) -> None:
