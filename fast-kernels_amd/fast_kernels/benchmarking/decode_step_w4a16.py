@@ -1,0 +1,231 @@
+"""Runner of the decode_step_w4a16 suite family: a sustained decode-step stream.
+
+A stack of ``metadata.layers`` Llama-style layers, each with the suite's projection shapes
+(qkv, o, gate_up, down) and its own seeded int4 weights, is laid out in HBM as ARC packets. All
+GEMVs of one decode step (layers x projections) are captured in one HIP graph and replayed; the
+step's weights (3.6 GB for the 32-layer 8B stack) exceed every cache, so each replay streams them
+from HBM. Reported per suite shape: device microseconds per GEMV (a graph of that projection
+over all layers) and, as the extra shape "decode_step", microseconds per whole step and aggregate
+effective HBM GB/s. The torch reference baseline (dequantize + matmul per GEMV) is timed eagerly.
+
+Correctness: after the timed replays, the outputs of the first and the last layer are compared
+with the explicit fp32 formula (alpha*q + beta weights, fp32 matmul) within the suite tolerances.
+
+Weights and activations are drawn on the GPU from a seeded torch generator (codes U{0..15},
+alpha U[0.001, 0.02], zero point 8 so beta = -8 alpha exactly, x ~ N(0, 1)): the benchmark
+configuration's recipe, generated where it is used instead of copied from the host.
+"""
+
+from __future__ import annotations
+
+import math
+from statistics import median
+from typing import Any
+
+from fast_kernels.benchmarking.decode_linear_w4a16 import (
+    PEAK_HBM_GBS,
+    _case,
+    _check_close,
+    _explicit_reference,
+    _max_err,
+    _p95,
+)
+from fast_kernels.benchmarking.inputs import algorithmic_bytes, seed_for_case
+from fast_kernels.schemas import BenchmarkCase, BenchmarkSuite
+
+GRAPH_REPLAYS = 20
+DEVICE_TIMING_BLOCKS = 5
+REFERENCE_SUBJECT = "torch/reference_w4a16_linear"
+STEP_SHAPE = "decode_step"
+
+
+def _all(suite: BenchmarkSuite, status: str, reason: str) -> list[BenchmarkCase]:
+    cases = []
+    for dtype in suite.dtypes:
+        for layout in suite.layouts:
+            names = [s.name for s in suite.shapes] + [STEP_SHAPE]
+            for name in names:
+                dims = next((s.dimensions() for s in suite.shapes if s.name == name), {"batch": 1})
+                for kind, ids in (("kernel", suite.kernels.ids), ("baseline", suite.baselines.ids)):
+                    cases += [_case(kind, sid, dtype, layout, name, dims, status, reason=reason)
+                              for sid in ids]
+    return cases
+
+
+def run_decode_step_w4a16_suite(suite: BenchmarkSuite) -> tuple[list[BenchmarkCase], list[str]]:
+    layers = int(suite.metadata.get("layers", 32))
+    notes = [
+        f"{layers} layers x {len(suite.shapes)} projections, distinct seeded weights per layer, "
+        "one HIP graph per measured stream, replays timed with HIP events.",
+    ]
+    try:
+        import torch
+    except ImportError:
+        return _all(suite, "skipped", "PyTorch is not installed."), notes
+    from fast_kernels.ops import hip_decode_available
+
+    if not hip_decode_available():
+        return _all(suite, "skipped", "Native module is not built with HIP support."), notes
+    if not torch.cuda.is_available():
+        return _all(suite, "skipped", "torch.cuda.is_available() is false on this machine."), notes
+    cases: list[BenchmarkCase] = []
+    for dtype in suite.dtypes:
+        for layout in suite.layouts:
+            cases += _run_stack(torch, suite, dtype, layout, layers)
+    return cases, notes
+
+
+def _run_stack(torch: Any, suite: BenchmarkSuite, dtype: str, layout: str, layers: int) -> list[BenchmarkCase]:
+    from fast_kernels.ops import (
+        arc_w4a16_forward,
+        dequant_w4a16_to_fp16,
+        group_size_for_layout,
+        pack_arc_w4a16_packets,
+    )
+
+    act_dtype = {"fp16": torch.float16, "bf16": torch.bfloat16}.get(dtype)
+    if act_dtype is None:
+        return [c for c in _all(suite, "skipped", f"dtype {dtype!r} is not supported")
+                if c.dtype == dtype and c.layout == layout]
+    device = torch.device("cuda")
+    group_size = group_size_for_layout(layout)
+    atol, rtol = suite.tolerances.atol, suite.tolerances.rtol
+    shapes = [(s.name, s.require_dimension("n"), s.require_dimension("k"), s.dimensions())
+              for s in suite.shapes]
+    try:
+        weights: dict[tuple[int, str], tuple[Any, Any, Any, Any]] = {}
+        keep_raw = {0, layers - 1}
+        for layer in range(layers):
+            for name, n, k, _ in shapes:
+                gen = torch.Generator(device=device)
+                gen.manual_seed(seed_for_case(1, n, k, group_size) * 131 + layer)
+                q = torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device=device, generator=gen)
+                alpha = torch.empty((n, k // group_size), device=device).uniform_(
+                    0.001, 0.02, generator=gen).half()
+                beta = (alpha.float() * -8.0).half()
+                packets = pack_arc_w4a16_packets(q, alpha, beta, group_size=group_size)
+                weights[(layer, name)] = (packets, q, alpha, beta) if layer in keep_raw else (packets, None, None, None)
+        gen = torch.Generator(device=device)
+        gen.manual_seed(12345)
+        xs = {k: torch.randn((1, k), device=device, generator=gen).to(act_dtype)
+              for k in sorted({k for _, _, k, _ in shapes})}
+        outs = {(layer, name): torch.empty((1, n), device=device, dtype=act_dtype)
+                for layer in range(layers) for name, n, _, _ in shapes}
+        stream = torch.cuda.Stream()
+
+        def launch(selection: list[str]) -> None:
+            for layer in range(layers):
+                for name, n, k, _ in shapes:
+                    if name in selection:
+                        arc_w4a16_forward(xs[k], weights[(layer, name)][0], n=n, k=k,
+                                          group_size=group_size, output=outs[(layer, name)])
+
+        def graph_for(selection: list[str]) -> Any:
+            with torch.cuda.stream(stream):
+                launch(selection)  # warm-up: plans and the library workspace exist before capture
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                launch(selection)
+            return graph
+
+        def time_graph(graph: Any) -> tuple[float, float]:
+            with torch.cuda.stream(stream):
+                for _ in range(2):
+                    graph.replay()
+                torch.cuda.synchronize()
+                samples = []
+                for _ in range(DEVICE_TIMING_BLOCKS):
+                    start = torch.cuda.Event(enable_timing=True)
+                    end = torch.cuda.Event(enable_timing=True)
+                    start.record(stream)
+                    for _ in range(GRAPH_REPLAYS):
+                        graph.replay()
+                    end.record(stream)
+                    end.synchronize()
+                    samples.append(start.elapsed_time(end) * 1e3 / GRAPH_REPLAYS)
+            return float(median(samples)), _p95(samples)
+
+        step_graph = graph_for([name for name, _, _, _ in shapes])
+        step_med, step_p95 = time_graph(step_graph)
+        # Check a replayed step: every output of the first and the last layer.
+        errors: dict[str, float] = {}
+        for layer in sorted(keep_raw):
+            for name, n, k, _ in shapes:
+                _, q, alpha, beta = weights[(layer, name)]
+                ref = _explicit_reference(torch, xs[k], q, alpha, beta, group_size)
+                _check_close(outs[(layer, name)], ref, atol, rtol, f"layer {layer} {name}")
+                errors[name] = max(errors.get(name, 0.0), _max_err(outs[(layer, name)], ref))
+        per_shape = {}
+        for name, _, _, _ in shapes:
+            per_shape[name] = time_graph(graph_for([name]))
+    except Exception as exc:  # noqa: BLE001 - reported as failed cases
+        return [c.model_copy(update={"status": "failed", "reason": str(exc)})
+                for c in _all(suite, "failed", "") if c.dtype == dtype and c.layout == layout]
+
+    cases: list[BenchmarkCase] = []
+    kernel_id = suite.kernels.ids[0]
+    step_bytes = 0
+    for name, n, k, dims in shapes:
+        med, p95 = per_shape[name]
+        alg = algorithmic_bytes(1, n, k, group_size)
+        step_bytes += alg * layers
+        us = med / layers
+        cases.append(_case("kernel", kernel_id, dtype, layout, name, dims, "ok",
+                           latency_us_median=us, latency_us_p95=p95 / layers,
+                           device_latency_us_median=us, device_latency_us_p95=p95 / layers,
+                           throughput=1e6 / us, decode_tokens_per_second=1e6 / us,
+                           metrics={"hbm_gbs": alg / us / 1e3,
+                                    "pct_hbm_peak": 100 * alg / us / 1e3 / PEAK_HBM_GBS,
+                                    "algorithmic_bytes": float(alg), "layers": float(layers),
+                                    "max_abs_err": errors.get(name, math.nan)}))
+    cases.append(_case("kernel", kernel_id, dtype, layout, STEP_SHAPE,
+                       {"batch": 1, "layers": layers, "gemvs": layers * len(shapes)}, "ok",
+                       latency_us_median=step_med, latency_us_p95=step_p95,
+                       device_latency_us_median=step_med, device_latency_us_p95=step_p95,
+                       throughput=1e6 / step_med, decode_tokens_per_second=1e6 / step_med,
+                       metrics={"hbm_gbs": step_bytes / step_med / 1e3,
+                                "pct_hbm_peak": 100 * step_bytes / step_med / 1e3 / PEAK_HBM_GBS,
+                                "algorithmic_bytes": float(step_bytes),
+                                "us_per_step": step_med}))
+    for kid in suite.kernels.ids[1:]:
+        cases += [_case("kernel", kid, dtype, layout, name, dims, "not_implemented",
+                        reason="the decode-step stream times the automatic dispatch only")
+                  for name, _, _, dims in shapes]
+
+    # torch reference: dequantize + matmul for every GEMV of one step, eager, a few steps.
+    for baseline_id in suite.baselines.ids:
+        if baseline_id != REFERENCE_SUBJECT:
+            cases += [_case("baseline", baseline_id, dtype, layout, name, dims, "not_implemented",
+                            reason=f"{baseline_id} has no decode-step runner")
+                      for name, _, _, dims in shapes]
+            continue
+        wbuf = {name: torch.empty((n, k), device=device, dtype=torch.float16) for name, n, k, _ in shapes}
+
+        def ref_step() -> None:
+            # Layer 0's weights stand in for every layer: the traffic per GEMV is the same.
+            for _layer in range(layers):
+                for name, n, k, _ in shapes:
+                    _, q, alpha, beta = weights[(0, name)]
+                    dequant_w4a16_to_fp16(q, alpha, beta, group_size=group_size, output=wbuf[name])
+                    torch.mm(xs[k].float(), wbuf[name].t().float())
+
+        ref_step()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(3):
+            ref_step()
+        end.record()
+        end.synchronize()
+        ref_us = start.elapsed_time(end) * 1e3 / 3
+        cases.append(_case("baseline", baseline_id, dtype, layout, STEP_SHAPE,
+                           {"batch": 1, "layers": layers}, "ok",
+                           latency_us_median=ref_us, device_latency_us_median=ref_us,
+                           throughput=1e6 / ref_us, decode_tokens_per_second=1e6 / ref_us,
+                           metrics={"hbm_gbs": step_bytes / ref_us / 1e3}))
+        for c in cases:
+            if c.subject_kind == "kernel" and c.shape_name == STEP_SHAPE and c.status == "ok":
+                c.speedup_vs = {baseline_id: ref_us / c.device_latency_us_median}
+    return cases

@@ -66,9 +66,19 @@ def make_case(
     act: str = "f16",
     asymmetric: bool = False,
     seed: int | None = None,
+    recipe: str = "baseline",
 ) -> W4A16Case:
+    """recipe "baseline": the distributions in this module's docstring. recipe "reference": the
+    reference suite's own distributions (decode_linear_w4a16.py:152-174): x = 0.25 N(0, 1),
+    alpha U[0.02, 0.2], zero points U{0..15} (always asymmetric); the values differ from the
+    reference's (it draws them from torch's CUDA generator), the distributions do not."""
     if act not in {"f16", "bf16"}:
         raise ValueError("act must be 'f16' or 'bf16'")
+    if recipe not in {"baseline", "reference"}:
+        raise ValueError("recipe must be 'baseline' or 'reference'")
+    alpha_lo, alpha_hi, x_scale = (0.001, 0.02, 1.0) if recipe == "baseline" else (0.02, 0.2, 0.25)
+    if recipe == "reference":
+        asymmetric = True
     if k % group_size != 0 or k % 2 != 0:
         raise ValueError("k must be a multiple of group_size")
     if seed is None:
@@ -76,7 +86,7 @@ def make_case(
     rng = np.random.default_rng(seed)
     ng = k // group_size
     q_u8 = rng.integers(0, 256, size=(n, k // 2), dtype=np.uint8)
-    alpha16 = rng.uniform(0.001, 0.02, size=(n, ng)).astype(np.float16)
+    alpha16 = rng.uniform(alpha_lo, alpha_hi, size=(n, ng)).astype(np.float16)
     if asymmetric:
         zp = rng.integers(0, 16, size=(n, ng), dtype=np.uint8)
     else:
@@ -84,6 +94,8 @@ def make_case(
     # half_rn(alpha * zp): the fp32 product of an fp16 and a small integer is exact
     beta16 = (-(alpha16.astype(np.float32) * zp.astype(np.float32))).astype(np.float16)
     x32 = rng.standard_normal(size=(batch, k), dtype=np.float32)
+    if x_scale != 1.0:
+        x32 *= np.float32(x_scale)
     x = x32.astype(np.float16).view(np.uint16) if act == "f16" else f32_to_bf16_bits(x32)
     return W4A16Case(
         x=np.ascontiguousarray(x),

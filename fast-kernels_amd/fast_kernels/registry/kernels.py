@@ -1,0 +1,61 @@
+"""Kernel ids the suites may name (reference: src/fast_kernels/registry/kernels.py:15-136).
+
+The decode/w4a16_linear* ids keep the reference's names, so its suite files verify here; each
+maps to an implementation of this package. Ids of the reference's other kernel families are not
+registered: suites naming them fail ``fk verify`` with "unknown kernel id".
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+
+@dataclass(frozen=True)
+class KernelSpec:
+    kernel_id: str
+    family: str
+    description: str
+    maturity: str
+    impl: str | None = None  # arc_w4a16_forward impl name; None = automatic dispatch
+
+
+def kernel_registry() -> dict[str, KernelSpec]:
+    specs = [
+        KernelSpec(
+            "decode/w4a16_linear",
+            "decode_quant_linear",
+            "Automatically dispatched W4A16 decode GEMV over ARC packets (gfx950 HIP).",
+            "experimental",
+            None,
+        ),
+        KernelSpec(
+            "decode/w4a16_linear_scalar",
+            "decode_quant_linear",
+            "Stream-K W4A16 GEMV: 128-bit packet loads, in-register nibble dequant, v_dot2 fp32 "
+            "accumulation, in-kernel activation sums and split-K fix-up (gfx950 HIP).",
+            "experimental",
+            "scalar",
+        ),
+        KernelSpec(
+            "decode/w4a16_linear_tc",
+            "decode_quant_linear",
+            "Matrix-core path: packet dequant to fp16, then a hipBLASLt fp16 GEMM.",
+            "experimental",
+            "tc",
+        ),
+        KernelSpec(
+            "decode/w4a16_linear_wgmma",
+            "decode_quant_linear",
+            "Reference id of a Hopper-only (wgmma) path; skipped on AMD GPUs.",
+            "unsupported",
+            "wgmma",
+        ),
+        KernelSpec(
+            "template/noop_gemm",
+            "gemm",
+            "Scaffold-only GEMM entry point for wiring suite definitions.",
+            "scaffold",
+            None,
+        ),
+    ]
+    return {spec.kernel_id: spec for spec in specs}
