@@ -95,4 +95,124 @@ __device__ __forceinline__ uint4 pair_activations(uint4 x) {
   return p;
 }
 
+
+// s_waitcnt immediate for gfx9 waiting until at most n vector-memory operations are outstanding:
+// vmcnt in bits 3:0 and 15:14, expcnt (6:4) and lgkmcnt (11:8) left at their maximum (no wait).
+constexpr int wait_vmcnt(int n) {
+  return (n & 0xF) | (((n >> 4) & 0x3) << 14) | 0x0F70;
+}
+constexpr int kWaitVmcnt0 = wait_vmcnt(0);
+// Largest bf16 biased exponent whose values all fit in fp16 (2^15 * (2 - 2^-7) < 65504).
+constexpr int kMaxFp16SafeBf16Exp = 142;
+
+// Larger of the biased exponents of the two bf16 values in a word.
+__device__ __forceinline__ uint32_t bf16_exp(uint32_t pair_word) {
+  return max((pair_word >> 7) & 0xffu, (pair_word >> 23) & 0xffu);
+}
+
+// Two bf16 values, each multiplied by s (a power of two), as an fp16 pair.
+__device__ __forceinline__ uint32_t bf16_pair_to_half_pair(uint32_t w, float s) {
+  const uint32_t lo = float_to_half_bits(bf16_bits_to_float(static_cast<uint16_t>(w)) * s);
+  const uint32_t hi = float_to_half_bits(bf16_bits_to_float(static_cast<uint16_t>(w >> 16)) * s);
+  return lo | (hi << 16);
+}
+
+// A value the compiler must keep in a VGPR and cannot fold: gfx9 VOP3 encodings take no literal,
+// so masks held this way let (w & mask) | bias select a single v_and_or_b32.
+__device__ __forceinline__ uint32_t vgpr_constant(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+
+// Cross-lane reductions over aligned groups of N in {8, 16} lanes (inside one 16-lane DPP row)
+// with DPP moves, so each step is one VALU instruction instead of an LDS round trip: xor 1 and
+// xor 2 (quad permutes), then the half-row mirror (lane i <-> 7 - i) and, for 16, the row mirror
+// (i <-> 15 - i). Every lane of the group ends with the group's total.
+namespace dpp {
+constexpr int kQuadXor1 = 0xB1;  // quad_perm [1, 0, 3, 2]
+constexpr int kQuadXor2 = 0x4E;  // quad_perm [2, 3, 0, 1]
+constexpr int kRowHalfMirror = 0x141;
+constexpr int kRowMirror = 0x140;
+
+template <int kCtrl>
+__device__ __forceinline__ float move(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl,
+                                                                0xF, 0xF, false));
+}
+template <int kCtrl>
+__device__ __forceinline__ uint32_t move(uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, 0xF, 0xF, false));
+}
+}  // namespace dpp
+
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(N == 8 || N == 16, "group of 8 or 16 lanes");
+  v += dpp::move<dpp::kQuadXor1>(v);
+  v += dpp::move<dpp::kQuadXor2>(v);
+  v += dpp::move<dpp::kRowHalfMirror>(v);
+  if constexpr (N == 16) {
+    v += dpp::move<dpp::kRowMirror>(v);
+  }
+  return v;
+}
+
+template <int N>
+__device__ __forceinline__ uint32_t group_max(uint32_t v) {
+  static_assert(N == 8 || N == 16, "group of 8 or 16 lanes");
+  v = max(v, dpp::move<dpp::kQuadXor1>(v));
+  v = max(v, dpp::move<dpp::kQuadXor2>(v));
+  v = max(v, dpp::move<dpp::kRowHalfMirror>(v));
+  if constexpr (N == 16) {
+    v = max(v, dpp::move<dpp::kRowMirror>(v));
+  }
+  return v;
+}
+
+// Last-contributor sum of a split tile's fp32 partials: acc[i] = sum over s = 0 .. n-1, in that
+// order, of ws[s * count + e] for this thread's elements e = tid + i * threads (e < count). The
+// loads are relaxed agent-scope atomics (coherent across XCDs); the loads of 4 contributors for all
+// of the thread's elements are issued before the first add, so the hand-off costs one memory
+// round trip per 4 contributors rather than one per element and contributor.
+template <int kPer, int kThreadCount>
+__device__ __forceinline__ void sum_tile_partials(const float* ws, int count, int n, int tid,
+                                                  float (&acc)[kPer]) {
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    acc[i] = 0.0f;
+  }
+  for (int s0 = 0; s0 < n; s0 += 4) {
+    float v[kPer][4];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int e = tid + i * kThreadCount;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[i][j] = 0.0f;
+        if (s0 + j < n && e < count) {
+          v[i][j] = __hip_atomic_load(ws + static_cast<size_t>(s0 + j) * count + e, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (s0 + j < n) {
+          acc[i] += v[i][j];
+        }
+      }
+    }
+  }
+}
+
 }  // namespace fk

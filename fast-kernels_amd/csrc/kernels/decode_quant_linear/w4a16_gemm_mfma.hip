@@ -1,0 +1,402 @@
+// W4A16 small-batch GEMM (8-16 activation rows) on the gfx950 matrix cores.
+//
+// Same math and packet layout as w4a16_gemv.hip; with 8 or more rows the dot2 loop there is bound
+// by VALU issue (four v_dot2 per code word per row), so here the products run on
+// v_mfma_f32_16x16x32_f16 and the VALU only unpacks nibbles:
+//
+//  * One MFMA multiplies A = 16 activation rows x 32 k by B = 32 k x 16 output columns. Lane l
+//    supplies A row l % 16 and B column l % 16, both for k = 8*(l / 16) .. +7, i.e. one code word
+//    per lane. A wave-wide dwordx4 load gives lane l the words of 4 consecutive columns
+//    (4*(l % 16) + j, j = 0..3) of word row l / 16, so 4 MFMAs (one per j) cover 64 columns x
+//    4 word rows; MFMA j's output column c maps to packet column 4*c + j.
+//  * A code word unpacks into the fp16 values 1024 + q in the k order (0,4)(1,5)(2,6)(3,7),
+//    which is the order the staged activations are paired in, so A and B agree slot by slot.
+//  * The 1024 bias and the group's scale and offset are applied once per (group, row, column):
+//    y += alpha * D + (beta - 1024 alpha) * S, with D the MFMA sum over the group and S the
+//    group's activation sum.
+//  * Work split, XCD remap and the cross-workgroup fix-up are those of the GEMV kernel
+//    (stream-K over (tile, group) units, last contributor finishes the tile).
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "w4a16_device.h"
+#include "w4a16_gemv.h"
+
+namespace fk {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kRows = kMfmaRows;  // activation rows per m-tile (MFMA M)
+constexpr int kWordRowBytes = kTileCols * 4;
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+template <int G>
+struct MfmaSmem {
+  static constexpr int kWordRows = G / 8;
+  static constexpr int kChunk = 1024 / G;  // groups staged per barrier (16 KB of activations)
+  // Paired fp16 activations, row fastest; one spare row per word row staggers the LDS banks of
+  // the staging stores (consecutive lanes store consecutive word rows of one activation row).
+  uint4 xs[kChunk][kWordRows][kRows + 1];
+  float sums[kChunk][kRows];               // sum of the group's (staged) activations per row
+  float scale[kChunk][kRows];              // power of two undoing the bf16 staging scale
+  float red[kWaves][kRows][kTileCols];     // cross-wave reduction
+  int last;
+};
+
+struct MfmaParams {
+  const uint16_t* x;
+  const uint8_t* packets;
+  uint16_t* out;
+  float* partials;
+  uint32_t* counters;
+  int M, N, K, NG, tiles, mtiles, per, max_contrib, xcd_remap;
+};
+
+template <int G>
+struct MfmaStage {
+  static constexpr int kUnits = MfmaSmem<G>::kChunk * (G / 8) * kRows;
+  static constexpr int kPerThread = kUnits / kThreads;
+  uint4 raw[kPerThread];
+};
+
+// Unit u = ((row * kChunk) + gl) * WR + w: word rows of one (row, group) are consecutive, so the
+// global loads are contiguous and the per-(row, group) reductions are xor-shuffles within WR lanes.
+template <int G>
+__device__ __forceinline__ void mfma_stage_load(MfmaStage<G>& st, const MfmaParams& p, int row0,
+                                                int g0, int n_chunk) {
+  constexpr int WR = G / 8;
+  constexpr int kChunk = MfmaSmem<G>::kChunk;
+  const int tid = static_cast<int>(threadIdx.x);
+#pragma unroll
+  for (int it = 0; it < MfmaStage<G>::kPerThread; ++it) {
+    const int u = it * kThreads + tid;
+    const int w = u % WR;
+    const int gl = (u / WR) % kChunk;
+    const int r = u / (WR * kChunk);
+    st.raw[it] = make_uint4(0u, 0u, 0u, 0u);
+    if (gl < n_chunk && row0 + r < p.M) {
+      st.raw[it] = *reinterpret_cast<const uint4*>(
+          p.x + static_cast<size_t>(row0 + r) * p.K + static_cast<size_t>(g0 + gl) * G + w * 8);
+    }
+  }
+}
+
+template <int G, Act A>
+__device__ __forceinline__ void mfma_stage_store(MfmaSmem<G>& sm, MfmaStage<G>& st, int n_chunk) {
+  constexpr int WR = G / 8;
+  constexpr int kChunk = MfmaSmem<G>::kChunk;
+  const int tid = static_cast<int>(threadIdx.x);
+#pragma unroll
+  for (int it = 0; it < MfmaStage<G>::kPerThread; ++it) {
+    const int u = it * kThreads + tid;
+    const int w = u % WR;
+    const int gl = (u / WR) % kChunk;
+    const int r = u / (WR * kChunk);
+    uint4 v = st.raw[it];
+    float undo = 1.0f;
+    if constexpr (A == Act::kBF16) {
+      const uint32_t e = group_max<WR>(
+          max(max(bf16_exp(v.x), bf16_exp(v.y)), max(bf16_exp(v.z), bf16_exp(v.w))));
+      const int shift = max(0, static_cast<int>(e) - kMaxFp16SafeBf16Exp);
+      const float s = __builtin_bit_cast(float, static_cast<uint32_t>(127 - shift) << 23);
+      undo = __builtin_bit_cast(float, static_cast<uint32_t>(127 + shift) << 23);
+      v.x = bf16_pair_to_half_pair(v.x, s);
+      v.y = bf16_pair_to_half_pair(v.y, s);
+      v.z = bf16_pair_to_half_pair(v.z, s);
+      v.w = bf16_pair_to_half_pair(v.w, s);
+    }
+    float sum = 0.0f;
+    const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      sum += half_bits_to_float(static_cast<uint16_t>(words[q])) +
+             half_bits_to_float(static_cast<uint16_t>(words[q] >> 16));
+    }
+    sum = group_sum<WR>(sum);
+    if (gl < n_chunk) {
+      sm.xs[gl][w][r] = pair_activations(v);
+      if (w == 0) {
+        sm.sums[gl][r] = sum;
+        sm.scale[gl][r] = undo;
+      }
+    }
+  }
+}
+
+template <int G>
+struct MfmaGroupLoad {
+  static constexpr int KB = G / 32;  // MFMA k-blocks per group
+  uint4 w[2][KB];                    // [half of the tile][k-block]
+  uint2 alpha[2];
+  uint2 beta[2];
+};
+
+template <int G>
+__device__ __forceinline__ void mfma_load_group(MfmaGroupLoad<G>& gl, const uint8_t* packet, int lane) {
+  constexpr int QB = kTileCols * G / 2;
+  const int col4 = 4 * (lane % 16);
+  const int code = (lane / 16) * kWordRowBytes + col4 * 4;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    gl.alpha[h] = *reinterpret_cast<const uint2*>(packet + QB + (h * 64 + col4) * 2);
+    gl.beta[h] = *reinterpret_cast<const uint2*>(packet + QB + kTileCols * 2 + (h * 64 + col4) * 2);
+#pragma unroll
+    for (int kb = 0; kb < MfmaGroupLoad<G>::KB; ++kb) {
+      gl.w[h][kb] = *reinterpret_cast<const uint4*>(packet + code + kb * 4 * kWordRowBytes + h * 256);
+    }
+  }
+}
+
+// Code word -> 8 fp16 values 1024 + q in the slot order (k0,k4)(k1,k5)(k2,k6)(k3,k7).
+__device__ __forceinline__ half8_t unpack_word(uint32_t w, uint32_t mask) {
+  constexpr uint32_t kBias = 0x64006400u;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 v;
+  v.x = (w & mask) | kBias;
+  v.y = ((w >> 4) & mask) | kBias;
+  v.z = ((w >> 8) & mask) | kBias;
+  v.w = ((w >> 12) & mask) | kBias;
+  return __builtin_bit_cast(half8_t, v);
+}
+
+template <int G, Act A>
+__device__ __forceinline__ void mfma_compute_group(const MfmaSmem<G>& sm, const MfmaGroupLoad<G>& ld,
+                                                   int gl, int lane, uint32_t mask,
+                                                   float (&y)[2][4][4]) {
+  constexpr int KB = MfmaGroupLoad<G>::KB;
+  half8_t a[KB];
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    a[kb] = __builtin_bit_cast(half8_t, sm.xs[gl][kb * 4 + lane / 16][lane % 16]);
+  }
+  const int r0 = 4 * (lane / 16);  // output rows r0 .. r0+3 of this lane
+  const float4 s4 = *reinterpret_cast<const float4*>(&sm.sums[gl][r0]);
+  float4 sc4 = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+  if constexpr (A == Act::kBF16) {
+    sc4 = *reinterpret_cast<const float4*>(&sm.scale[gl][r0]);
+  }
+  const float s[4] = {s4.x, s4.y, s4.z, s4.w};
+  const float sc[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    float4_t d[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      d[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      const uint32_t words[4] = {ld.w[h][kb].x, ld.w[h][kb].y, ld.w[h][kb].z, ld.w[h][kb].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        d[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[kb], unpack_word(words[j], mask), d[j], 0, 0, 0);
+      }
+    }
+    const uint16_t ab[4] = {static_cast<uint16_t>(ld.alpha[h].x), static_cast<uint16_t>(ld.alpha[h].x >> 16),
+                            static_cast<uint16_t>(ld.alpha[h].y), static_cast<uint16_t>(ld.alpha[h].y >> 16)};
+    const uint16_t bb[4] = {static_cast<uint16_t>(ld.beta[h].x), static_cast<uint16_t>(ld.beta[h].x >> 16),
+                            static_cast<uint16_t>(ld.beta[h].y), static_cast<uint16_t>(ld.beta[h].y >> 16)};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float alpha = half_bits_to_float(ab[j]);
+      const float c = fmaf(-1024.0f, alpha, half_bits_to_float(bb[j]));  // beta - 1024 alpha
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float t = fmaf(alpha, d[j][r], c * s[r]);
+        if constexpr (A == Act::kBF16) {
+          t *= sc[r];
+        }
+        y[h][j][r] += t;
+      }
+    }
+  }
+}
+
+template <int G, Act A>
+__device__ __forceinline__ void mfma_stream_groups(MfmaSmem<G>& sm, const MfmaParams& p,
+                                                   const uint8_t* tile_packets, int row0, int g_lo,
+                                                   int g_hi, int lane, int wave, uint32_t mask,
+                                                   float (&y)[2][4][4]) {
+  constexpr int kChunk = MfmaSmem<G>::kChunk;
+  const size_t stride = static_cast<size_t>(packet_stride_bytes(G));
+  for (int g0 = g_lo; g0 < g_hi; g0 += kChunk) {
+    const int n_chunk = min(kChunk, g_hi - g0);
+    if (g0 != g_lo) {
+      lds_barrier();
+    }
+    MfmaStage<G> st;
+    mfma_stage_load<G>(st, p, row0, g0, n_chunk);
+    // This wave's groups: gl = wave + 4t, t < n_w, through two register buffers; loads are
+    // unconditional (a wave past its last group re-reads that group and does not compute it) so
+    // the compiler can count the loads behind each buffer.
+    const int n_w = n_chunk > wave ? (n_chunk - wave + kWaves - 1) / kWaves : 0;
+    const int t_last = max(n_w - 1, 0);
+    const int gl_base = n_w > 0 ? wave : n_chunk - 1;
+    const uint8_t* gp = tile_packets + static_cast<size_t>(g0 + gl_base) * stride;
+    const size_t step = static_cast<size_t>(kWaves) * stride;
+    MfmaGroupLoad<G> buf[2];
+    mfma_load_group<G>(buf[0], gp, lane);
+    mfma_load_group<G>(buf[1], gp + static_cast<size_t>(min(1, t_last)) * step, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_stage_store<G, A>(sm, st, n_chunk);
+    lds_barrier();
+    const int n_blocks = (n_w + 1) / 2;
+    int t0 = 0;
+    for (int blk = 0; blk + 1 < n_blocks; ++blk, t0 += 2) {
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        mfma_compute_group<G, A>(sm, buf[d], wave + (t0 + d) * kWaves, lane, mask, y);
+        mfma_load_group<G>(buf[d], gp + static_cast<size_t>(min(t0 + 2 + d, t_last)) * step, lane);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      if (t0 + d < n_w) {
+        mfma_compute_group<G, A>(sm, buf[d], wave + (t0 + d) * kWaves, lane, mask, y);
+      }
+    }
+  }
+}
+
+template <int G, Act A>
+__global__ void __launch_bounds__(kThreads, 1) w4a16_gemm_mfma_kernel(MfmaParams p) {
+  constexpr int kOut = kRows * kTileCols;
+  __shared__ MfmaSmem<G> sm;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t mask = vgpr_constant(0x000f000fu);
+  const size_t stride = static_cast<size_t>(packet_stride_bytes(G));
+  const int grid = static_cast<int>(gridDim.x);
+  int b = static_cast<int>(blockIdx.x);
+  if (p.xcd_remap) {
+    b = (b & 7) * (grid >> 3) + (b >> 3);
+  }
+  const long long total_units = static_cast<long long>(p.tiles) * p.mtiles * p.NG;
+  const long long u_begin = static_cast<long long>(b) * p.per;
+  const long long u_end = min(total_units, u_begin + p.per);
+  long long u = u_begin;
+  while (u < u_end) {
+    const int T = static_cast<int>(u / p.NG);
+    const int g_lo = static_cast<int>(u - static_cast<long long>(T) * p.NG);
+    const int g_hi = static_cast<int>(min(static_cast<long long>(p.NG), g_lo + (u_end - u)));
+    const int tile = T % p.tiles;
+    const int row0 = (T / p.tiles) * kRows;
+    const int col_base = tile * kTileCols;
+    float y[2][4][4] = {};
+    const uint8_t* tile_packets = p.packets + static_cast<size_t>(tile) * p.NG * stride;
+    mfma_stream_groups<G, A>(sm, p, tile_packets, row0, g_lo, g_hi, lane, wave, mask, y);
+    // Lane l holds rows 4*(l/16)+r and columns h*64 + 4*(l%16) + j.
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        *reinterpret_cast<float4*>(&sm.red[wave][4 * (lane / 16) + r][h * 64 + 4 * (lane % 16)]) =
+            make_float4(y[h][0][r], y[h][1][r], y[h][2][r], y[h][3][r]);
+      }
+    }
+    __syncthreads();
+    auto red_sum = [&](int idx) {
+      const int r = idx / kTileCols;
+      const int c = idx % kTileCols;
+      float v = sm.red[0][r][c];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) {
+        v += sm.red[w][r][c];
+      }
+      return v;
+    };
+    const long long tile_u0 = static_cast<long long>(T) * p.NG;
+    const int first = static_cast<int>(tile_u0 / p.per);
+    const int last = static_cast<int>((tile_u0 + p.NG - 1) / p.per);
+    if (first == last) {
+      for (int idx = tid; idx < kOut; idx += kThreads) {
+        const int r = idx / kTileCols;
+        if (row0 + r < p.M) {
+          p.out[static_cast<size_t>(row0 + r) * p.N + col_base + idx % kTileCols] =
+              float_to_act_bits<A>(red_sum(idx));
+        }
+      }
+    } else {
+      // Same hand-off as the GEMV kernel: relaxed agent-scope atomics, stores complete before the
+      // barrier that precedes the counter increment, last arriver sums in workgroup order.
+      const int contributors = last - first + 1;
+      float* ws = p.partials + static_cast<size_t>(T) * p.max_contrib * kOut;
+      for (int idx = tid; idx < kOut; idx += kThreads) {
+        __hip_atomic_store(&ws[static_cast<size_t>(b - first) * kOut + idx], red_sum(idx),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      __syncthreads();
+      if (tid == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(&p.counters[T], 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        sm.last = (prev == static_cast<uint32_t>(contributors - 1)) ? 1 : 0;
+      }
+      __syncthreads();
+      if (sm.last) {
+        constexpr int kPer = kOut / kThreads;
+        float acc[kPer];
+        sum_tile_partials<kPer, kThreads>(ws, kOut, contributors, tid, acc);
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+          const int idx = tid + i * kThreads;
+          const int r = idx / kTileCols;
+          if (row0 + r < p.M) {
+            p.out[static_cast<size_t>(row0 + r) * p.N + col_base + idx % kTileCols] =
+                float_to_act_bits<A>(acc[i]);
+          }
+        }
+        if (tid == 0) {
+          __hip_atomic_store(&p.counters[T], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+    __syncthreads();
+    u += g_hi - g_lo;
+  }
+}
+
+template <int G, Act A>
+hipError_t launch_mfma_t(const GemvLaunch& l, hipStream_t stream) {
+  MfmaParams p;
+  p.x = static_cast<const uint16_t*>(l.x);
+  p.packets = static_cast<const uint8_t*>(l.packets);
+  p.out = static_cast<uint16_t*>(l.out);
+  p.partials = static_cast<float*>(l.partials);
+  p.counters = static_cast<uint32_t*>(l.counters);
+  p.M = l.M;
+  p.N = l.N;
+  p.K = l.K;
+  p.NG = l.K / G;
+  p.tiles = l.N / kTileCols;
+  p.mtiles = (l.M + kRows - 1) / kRows;
+  p.per = l.units_per_workgroup;
+  p.max_contrib = l.max_contributors;
+  const long long total = static_cast<long long>(p.tiles) * p.mtiles * p.NG;
+  const int grid = static_cast<int>((total + p.per - 1) / p.per);
+  p.xcd_remap = (grid % 8 == 0) ? 1 : 0;
+  hipLaunchKernelGGL((w4a16_gemm_mfma_kernel<G, A>), dim3(grid), dim3(kThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_w4a16_gemm_mfma(const GemvLaunch& l, hipStream_t stream) {
+  if (l.m_tile != kRows || l.mode != GemvMode::kStreamK || l.slice_cols != kTileCols) {
+    return hipErrorInvalidValue;
+  }
+  if (l.group_size == 64) {
+    return l.act == Act::kF16 ? launch_mfma_t<64, Act::kF16>(l, stream)
+                              : launch_mfma_t<64, Act::kBF16>(l, stream);
+  }
+  return l.act == Act::kF16 ? launch_mfma_t<128, Act::kF16>(l, stream)
+                            : launch_mfma_t<128, Act::kBF16>(l, stream);
+}
+
+}  // namespace fk

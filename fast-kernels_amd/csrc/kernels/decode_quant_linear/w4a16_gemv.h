@@ -30,7 +30,13 @@ struct GemvLaunch {
   int slice_cols = kTileCols;   // kStreamK: columns per workgroup slice (128, 64 or 32)
 };
 
+// Activation rows per m-tile for a batch: 1, 2, 4, 8 on the dot2 GEMV kernel, kMfmaRows (from
+// kMfmaMinBatch rows) on the matrix-core kernel.
+constexpr int kMfmaRows = 16;
+constexpr int kMfmaMinBatch = 8;
 int gemv_m_tile_for_batch(int batch);
+// m-tile of the reference split-K protocol (kPartials), served by the dot2 kernel only.
+int gemv_partials_m_tile_for_batch(int batch);
 
 // Tiles (128 columns x m_tile rows) of a launch; the stream-K scratch holds one counter per slice
 // (tiles x 128 / slice_cols) and max_contributors fp32 partial slots of m_tile x 128 floats per
@@ -43,5 +49,8 @@ inline size_t gemv_streamk_partial_floats(int n, int batch, int m_tile, int max_
 }
 
 hipError_t launch_w4a16_gemv(const GemvLaunch& launch, hipStream_t stream);
+// Matrix-core kernel for m_tile == kMfmaRows (w4a16_gemm_mfma.hip); launch_w4a16_gemv forwards
+// such launches to it.
+hipError_t launch_w4a16_gemm_mfma(const GemvLaunch& launch, hipStream_t stream);
 
 }  // namespace fk

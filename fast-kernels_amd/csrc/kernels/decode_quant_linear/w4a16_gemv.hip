@@ -46,14 +46,6 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kWordRowBytes = kTileCols * 4;
 
-// s_waitcnt immediate for gfx9 waiting until at most n vector-memory operations are outstanding:
-// vmcnt in bits 3:0 and 15:14, expcnt (6:4) and lgkmcnt (11:8) left at their maximum (no wait).
-constexpr int wait_vmcnt(int n) {
-  return (n & 0xF) | (((n >> 4) & 0x3) << 14) | 0x0F70;
-}
-constexpr int kWaitVmcnt0 = wait_vmcnt(0);
-// Largest bf16 biased exponent whose values all fit in fp16 (2^15 * (2 - 2^-7) < 65504).
-constexpr int kMaxFp16SafeBf16Exp = 142;
 
 // Geometry of a CW-column slice of a G-group packet.
 template <int G, int CW>
@@ -129,15 +121,6 @@ __device__ __forceinline__ void stage_load(StageRegs<G, MT, CW>& st, const GemvP
   }
 }
 
-__device__ __forceinline__ uint32_t bf16_exp(uint32_t pair_word) {
-  return max((pair_word >> 7) & 0xffu, (pair_word >> 23) & 0xffu);
-}
-
-__device__ __forceinline__ uint32_t bf16_pair_to_half_pair(uint32_t w, float s) {
-  const uint32_t lo = float_to_half_bits(bf16_bits_to_float(static_cast<uint16_t>(w)) * s);
-  const uint32_t hi = float_to_half_bits(bf16_bits_to_float(static_cast<uint16_t>(w >> 16)) * s);
-  return lo | (hi << 16);
-}
 
 // Convert (bf16) and re-pair the staged activations into LDS and reduce the per-(row, group,
 // word row mod R) sums, R = word rows per load. Word rows of one (m, group) are WR consecutive,
@@ -158,11 +141,8 @@ __device__ __forceinline__ void stage_store(Smem<G, MT, CW>& sm, StageRegs<G, MT
     uint4 r = st.raw[it];
     float undo = 1.0f;
     if constexpr (A == Act::kBF16) {
-      uint32_t e = max(max(bf16_exp(r.x), bf16_exp(r.y)), max(bf16_exp(r.z), bf16_exp(r.w)));
-#pragma unroll
-      for (int off = 1; off < WR; off <<= 1) {
-        e = max(e, static_cast<uint32_t>(__shfl_xor(static_cast<int>(e), off)));
-      }
+      const uint32_t e = group_max<WR>(
+          max(max(bf16_exp(r.x), bf16_exp(r.y)), max(bf16_exp(r.z), bf16_exp(r.w))));
       const int shift = max(0, static_cast<int>(e) - kMaxFp16SafeBf16Exp);
       const float s = __builtin_bit_cast(float, static_cast<uint32_t>(127 - shift) << 23);
       undo = __builtin_bit_cast(float, static_cast<uint32_t>(127 + shift) << 23);
@@ -180,10 +160,21 @@ __device__ __forceinline__ void stage_store(Smem<G, MT, CW>& sm, StageRegs<G, MT
                half_bits_to_float(static_cast<uint16_t>(r.y >> 16)) +
                half_bits_to_float(static_cast<uint16_t>(r.z >> 16)) +
                half_bits_to_float(static_cast<uint16_t>(r.w >> 16));
+    if constexpr (R == 2) {
+      // Even and odd word rows: two masked DPP reductions per value instead of three shuffles.
+      const bool odd = (w & 1) != 0;
+      const float se_odd = group_sum<WR>(odd ? se : 0.0f);
+      const float so_odd = group_sum<WR>(odd ? so : 0.0f);
+      const float se_even = group_sum<WR>(odd ? 0.0f : se);
+      const float so_even = group_sum<WR>(odd ? 0.0f : so);
+      se = odd ? se_odd : se_even;
+      so = odd ? so_odd : so_even;
+    } else {
 #pragma unroll
-    for (int off = R; off < WR; off <<= 1) {
-      se += __shfl_xor(se, off);
-      so += __shfl_xor(so, off);
+      for (int off = R; off < WR; off <<= 1) {
+        se += __shfl_xor(se, off);
+        so += __shfl_xor(so, off);
+      }
     }
     if (u < StageRegs<G, MT, CW>::kUnits && gl < n_chunk) {
       sm.xs[m][gl][w] = pair_activations(r);
@@ -197,18 +188,6 @@ __device__ __forceinline__ void stage_store(Smem<G, MT, CW>& sm, StageRegs<G, MT
   }
 }
 
-// A value the compiler must keep in a VGPR and cannot fold: gfx9 VOP3 encodings take no literal,
-// so masks held this way let (w & mask) | bias select a single v_and_or_b32.
-__device__ __forceinline__ uint32_t vgpr_constant(uint32_t v) {
-  asm volatile("" : "+v"(v));
-  return v;
-}
-
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 template <int G, int CW>
 struct GroupLoad {
@@ -528,16 +507,16 @@ w4a16_gemv_kernel(GemvParams p) {
         }
         __syncthreads();
         if (sm.last) {
-          for (int idx = tid; idx < kOut; idx += kThreads) {
+          constexpr int kPer = (kOut + kThreads - 1) / kThreads;
+          float acc[kPer];
+          sum_tile_partials<kPer, kThreads>(ws, kOut, contributors, tid, acc);
+#pragma unroll
+          for (int i = 0; i < kPer; ++i) {
+            const int idx = tid + i * kThreads;
             const int m = idx / CW;
             const int c = idx % CW;
-            if (row0 + m < p.M) {
-              float v = 0.0f;
-              for (int s = 0; s < contributors; ++s) {
-                v += __hip_atomic_load(&ws[static_cast<size_t>(s) * kOut + idx], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-              }
-              p.out[static_cast<size_t>(row0 + m) * p.N + col_base + c] = float_to_act_bits<A>(v);
+            if (idx < kOut && row0 + m < p.M) {
+              p.out[static_cast<size_t>(row0 + m) * p.N + col_base + c] = float_to_act_bits<A>(acc[i]);
             }
           }
           if (tid == 0) {
@@ -615,6 +594,11 @@ hipError_t dispatch_mt(const GemvLaunch& l, hipStream_t stream) {
 }  // namespace
 
 int gemv_m_tile_for_batch(int batch) {
+  if (batch >= kMfmaMinBatch) return kMfmaRows;
+  return gemv_partials_m_tile_for_batch(batch);
+}
+
+int gemv_partials_m_tile_for_batch(int batch) {
   if (batch <= 1) return 1;
   if (batch <= 2) return 2;
   if (batch <= 4) return 4;
@@ -622,6 +606,9 @@ int gemv_m_tile_for_batch(int batch) {
 }
 
 hipError_t launch_w4a16_gemv(const GemvLaunch& l, hipStream_t stream) {
+  if (l.m_tile == kMfmaRows) {
+    return launch_w4a16_gemm_mfma(l, stream);
+  }
   if (l.slice_cols != 32 && l.slice_cols != 64 && l.slice_cols != kTileCols) {
     return hipErrorInvalidValue;
   }

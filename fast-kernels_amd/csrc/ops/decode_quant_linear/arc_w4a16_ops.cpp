@@ -143,27 +143,27 @@ ArcW4A16Plan plan_arc_w4a16_for_cu_count(int batch, int n, int k, int group_size
     const int s_req = std::min(split_k_slices, num_groups);
     per = (num_groups + s_req - 1) / s_req;
   } else {
-    // Measured on MI355X over the Llama-7B/8B/70B decode shapes (M = 1): one workgroup per CU
-    // with long runs is best. Shapes with at least as many tiles as half the CUs run whole tiles
-    // over all of K. Otherwise K is split (power of two) until runs are at most kMaxRunGroups
-    // long while the runs still fit on the CUs, and then tiles are cut into 64- or 32-column
-    // slices while those fit: narrow slices add workgroups without the cross-workgroup fix-up a
-    // K split costs. With several activation rows per tile (more arithmetic per byte) K is split
-    // further while workgroups still fit.
+    // Measured on MI355X over the Llama-7B/8B/70B decode shapes. One activation row: one
+    // workgroup per CU with long runs is best. Shapes with at least as many tiles as half the
+    // CUs run whole tiles over all of K. Otherwise K is split (power of two) until runs are at
+    // most kMaxRunGroups long while the runs still fit on the CUs, and then tiles are cut into
+    // 64- or 32-column slices while those fit: narrow slices add workgroups without the
+    // cross-workgroup fix-up a K split costs. Several rows (more arithmetic per byte): two
+    // workgroups per CU, from K splits alone, runs of at least kMinGroupsPerWorkgroup groups.
     long long s_split = 1;
-    auto can_split = [&](long long s) {
-      return tiles * slices * s * 2 <= cu_count && num_groups / (s * 2) >= kMinGroupsPerWorkgroup;
-    };
-    while (num_groups / s_split > kMaxRunGroups && can_split(s_split)) {
-      s_split *= 2;
-    }
-    if (plan.m_tile <= 2) {
+    if (plan.m_tile == 1) {
+      auto can_split = [&](long long s) {
+        return tiles * s * 2 <= cu_count && num_groups / (s * 2) >= kMinGroupsPerWorkgroup;
+      };
+      while (num_groups / s_split > kMaxRunGroups && can_split(s_split)) {
+        s_split *= 2;
+      }
       while (slices < kMaxSlicesPerTile && tiles * s_split * slices * 2 <= cu_count) {
         slices *= 2;
       }
-    }
-    if (plan.m_tile > 1) {
-      while (can_split(s_split)) {
+    } else {
+      while (tiles * s_split * 2 <= 2LL * cu_count &&
+             num_groups / (s_split * 2) >= kMinGroupsPerWorkgroup) {
         s_split *= 2;
       }
     }
@@ -422,7 +422,7 @@ void arc_w4a16_forward_split_k(std::uintptr_t activations_ptr, std::uintptr_t pa
   l.group_size = group_size;
   l.act = fk::Act::kF16;
   l.mode = fk::GemvMode::kPartials;
-  l.m_tile = fk::gemv_m_tile_for_batch(batch);
+  l.m_tile = fk::gemv_partials_m_tile_for_batch(batch);
   l.splits = split_k_slices;
   l.gps = (num_groups + split_k_slices - 1) / split_k_slices;
   check_hip(fk::launch_w4a16_gemv(l, reinterpret_cast<hipStream_t>(stream_ptr)),

@@ -93,6 +93,8 @@ def test_plan_policy_without_gpu(lib: ctypes.CDLL, shape, want_runs_per_tile, wa
 
 def test_plan_batch_tiles_and_forced_split(lib: ctypes.CDLL) -> None:
     rc, p = _plan(lib, 16, 14336, 4096, 64)
+    assert rc == 0 and p.m_tile == 16  # matrix-core kernel from 8 rows
+    rc, p = _plan(lib, 7, 14336, 4096, 64)
     assert rc == 0 and p.m_tile == 8
     rc, p = _plan(lib, 3, 14336, 4096, 64, act=1)
     assert rc == 0 and p.m_tile == 4

@@ -122,7 +122,7 @@ def _run_forward(case, **kwargs) -> np.ndarray:
 
 
 @pytest.mark.parametrize("group_size", [64, 128])
-@pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 8, 16])
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 7, 8, 12, 16, 33])
 @pytest.mark.parametrize("asym", [False, True])
 def test_forward_small_matches_oracle(group_size: int, batch: int, asym: bool) -> None:
     case = make_case(batch, 256, 8 * group_size, group_size, asymmetric=asym)
@@ -157,12 +157,13 @@ def test_forward_baseline_shapes_match_oracle(shape: tuple[int, int, int, int]) 
         ((1, 1024, 2048, 128), "f16", False, (32, 16)),    # 8 tiles -> 32 narrow slices
         ((1, 10240, 4096, 128), "f16", True, (64, 32)),    # 80 tiles -> 160 64-column slices
         ((1, 4096, 14336, 128), "bf16", False, (32, 56)),  # narrow slices + K split (fix-up)
-        ((2, 4096, 4096, 64), "f16", True, (32, 32)),      # two rows, narrow slices + K split
-        ((2, 1024, 8192, 64), "bf16", True, (32, 16)),     # two rows, 8 runs per slice
+        ((2, 4096, 4096, 64), "f16", True, (128, 8)),      # two rows: whole tiles, 8 runs per tile
+        ((2, 1024, 8192, 64), "bf16", True, (128, 8)),     # two rows, 16 runs per tile
     ],
 )
 def test_forward_column_slices_match_oracle(shape, act, asym, want) -> None:
-    """The automatic plan's 64- and 32-column slices, alone and with K split across workgroups."""
+    """The automatic plan's 64- and 32-column slices, alone and with K split across workgroups,
+    and its K splits for several rows."""
     batch, n, k, g = shape
     plan = arc_w4a16_plan(batch=batch, n=n, k=k, group_size=g,
                           activation_dtype=torch.float16 if act == "f16" else torch.bfloat16)
@@ -194,7 +195,7 @@ def test_forward_llama70b_large_rows_subset(act: str, shape: tuple[int, int, int
 
 
 @pytest.mark.parametrize("group_size", [64, 128])
-@pytest.mark.parametrize("batch", [1, 2, 4, 8])
+@pytest.mark.parametrize("batch", [1, 2, 4, 8, 16])
 def test_forward_bf16_matches_oracle(group_size: int, batch: int) -> None:
     case = make_case(batch, 1024, 16 * group_size, group_size, act="bf16")
     y = _run_forward(case)
