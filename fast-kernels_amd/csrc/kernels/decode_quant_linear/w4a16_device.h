@@ -165,6 +165,24 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Sums over the lanes of a 16-lane row that share lane index mod R (R in {1, 2, 4, 8}): rotating
+// the row by R, 2R, ... keeps every lane inside its residue class.
+template <int R>
+__device__ __forceinline__ float row_strided_sum(float v) {
+  static_assert(R == 1 || R == 2 || R == 4 || R == 8, "stride 1, 2, 4 or 8");
+  if constexpr (R <= 1) {
+    v += dpp::move<0x121>(v);  // row_ror:1
+  }
+  if constexpr (R <= 2) {
+    v += dpp::move<0x122>(v);  // row_ror:2
+  }
+  if constexpr (R <= 4) {
+    v += dpp::move<0x124>(v);  // row_ror:4
+  }
+  v += dpp::move<0x128>(v);    // row_ror:8
+  return v;
+}
+
 template <int N>
 __device__ __forceinline__ uint32_t group_max(uint32_t v) {
   static_assert(N == 8 || N == 16, "group of 8 or 16 lanes");

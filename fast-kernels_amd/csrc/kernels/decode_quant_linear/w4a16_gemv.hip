@@ -160,8 +160,12 @@ __device__ __forceinline__ void stage_store(Smem<G, MT, CW>& sm, StageRegs<G, MT
                half_bits_to_float(static_cast<uint16_t>(r.y >> 16)) +
                half_bits_to_float(static_cast<uint16_t>(r.z >> 16)) +
                half_bits_to_float(static_cast<uint16_t>(r.w >> 16));
-    if constexpr (R == 2) {
-      // Even and odd word rows: two masked DPP reductions per value instead of three shuffles.
+    if constexpr (WR == 16 && R < WR) {
+      // One 16-lane DPP row per (row, group): rotations by R, 2R, ... (one VALU op each).
+      se = row_strided_sum<R>(se);
+      so = row_strided_sum<R>(so);
+    } else if constexpr (R == 2) {
+      // Even and odd word rows of an 8-lane group: masked 8-lane DPP reductions.
       const bool odd = (w & 1) != 0;
       const float se_odd = group_sum<WR>(odd ? se : 0.0f);
       const float so_odd = group_sum<WR>(odd ? so : 0.0f);
