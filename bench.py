@@ -4,7 +4,10 @@ Workload (benchmark configuration 2): one Llama-70B-class layer's four M=1 decod
 group size 128, symmetric int4 (zp = 8), bf16 activations and outputs:
     qkv 10240x8192, o 8192x8192, gate_up 57344x8192, down 8192x28672.
 A "step" is one pass over the four GEMVs. Weights are random int4 codes (synthetic, seeded on the
-device), packed once into the reference packet layout. Each shape has R rotated weight copies
+device), packed once into the reference packet layout (--packets arc, the default) or converted
+from it to the native symmetric packets (--packets native_sym: the same codes and alpha without
+the fp16 beta, which zp = 8 fixes); the other format is measured too and reported under
+"other_packets". Each shape has R rotated weight copies
 whose total exceeds twice the 256 MiB Infinity Cache, and consecutive steps use different copies,
 so every launch streams its weights from HBM.
 
@@ -68,6 +71,18 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--eager", action="store_true", help="launch without a HIP graph")
     p.add_argument(
+        "--packets",
+        choices=["arc", "native_sym"],
+        default="arc",
+        help="packet format of the headline value: the reference's (arc) or the native symmetric "
+        "one (codes and alpha only)",
+    )
+    p.add_argument(
+        "--no-other-packets",
+        action="store_true",
+        help="skip measuring the other packet format (reported under 'other_packets')",
+    )
+    p.add_argument(
         "--copy-calibration",
         action="store_true",
         help="only run a plain 256 MiB device-to-device copy 10 times (scales rocprofv3 "
@@ -91,11 +106,13 @@ def copy_calibration(torch) -> int:
 
 
 class ShapeBuffers:
-    def __init__(self, torch, native, name, n, k, g, batch, act, rotations, split_k):
-        from fast_kernels.ops import arc_packet_stride_bytes
+    def __init__(self, torch, native, name, n, k, g, batch, act, rotations, split_k, packets="arc"):
+        from fast_kernels.ops import PACKET_FORMATS, arc_packet_stride_bytes, packet_stride_bytes
 
         self.name, self.n, self.k, self.g, self.batch = name, n, k, g, batch
         self.stride = arc_packet_stride_bytes(g)
+        self.format = PACKET_FORMATS[packets]
+        self.native_stride = packet_stride_bytes(g, packets)
         self.act_code = 1 if act == "bf16" else 0
         dtype = torch.bfloat16 if act == "bf16" else torch.float16
         dev = torch.device("cuda")
@@ -112,6 +129,14 @@ class ShapeBuffers:
                 q.data_ptr(), alpha.data_ptr(), beta.data_ptr(), pk.data_ptr(), n, k, g,
                 self.stride, torch.cuda.current_stream().cuda_stream,
             )
+            if self.format != PACKET_FORMATS["arc"]:
+                arc = pk
+                pk = torch.empty(((n // 128) * ng, self.native_stride), device=dev, dtype=torch.uint8)
+                native.convert_arc_to_native_packets(
+                    arc.data_ptr(), pk.data_ptr(), n, k, g, self.format,
+                    torch.cuda.current_stream().cuda_stream,
+                )
+                del arc
             self.packets.append(pk)
             del q, alpha, beta
         self.x = torch.randn((batch, k), device=dev, generator=gen).to(dtype)
@@ -121,11 +146,18 @@ class ShapeBuffers:
         self.bytes = algorithmic_bytes(batch, n, k, g)
 
     def launch(self, native, torch, ws, r):
-        native.arc_w4a16_forward_ex(
-            self.x.data_ptr(), self.packets[r % len(self.packets)].data_ptr(), self.out.data_ptr(),
-            ws.data_ptr(), ws.numel(), self.batch, self.n, self.k, self.g, self.stride,
-            self.act_code, self.split_k, torch.cuda.current_stream().cuda_stream,
-        )
+        stream = torch.cuda.current_stream().cuda_stream
+        pk = self.packets[r % len(self.packets)].data_ptr()
+        if self.format == 0:
+            native.arc_w4a16_forward_ex(
+                self.x.data_ptr(), pk, self.out.data_ptr(), ws.data_ptr(), ws.numel(), self.batch,
+                self.n, self.k, self.g, self.stride, self.act_code, self.split_k, stream,
+            )
+        else:
+            native.arc_w4a16_forward_native(
+                self.x.data_ptr(), pk, self.out.data_ptr(), ws.data_ptr(), ws.numel(), self.batch,
+                self.n, self.k, self.g, self.format, self.act_code, self.split_k, stream,
+            )
 
 
 def rotations_for(total_packet_bytes: int) -> int:
@@ -213,40 +245,19 @@ def cpu_baseline(workload: str, batch: int, seconds: float) -> dict:
     }
 
 
-def main() -> int:
-    args = parse_args()
-    if args.gpus != 1:
-        print(
-            f"bench.py measures one GPU only: this build has no multi-GPU path (asked for "
-            f"--gpus {args.gpus}). Run with --gpus 1.",
-            file=sys.stderr,
-        )
-        return 2
-    import torch
-
-    from fast_kernels.native import native_module
-
-    native = native_module()
-    if not torch.cuda.is_available():
-        print("bench.py needs a GPU", file=sys.stderr)
-        return 2
-    if args.copy_calibration:
-        return copy_calibration(torch)
-    act, g, shapes = WORKLOADS[args.workload]
-    if args.only:
-        keep = set(args.only.split(","))
-        shapes = [s for s in shapes if s[0] in keep]
-
+def measure(torch, native, args, act, g, shapes, packets):
+    """Per-shape and whole-step timing over packets of one format. The buffers are freed before
+    returning except for what the report needs (plans, byte counts)."""
     bufs = []
     for name, n, k in shapes:
         pk_bytes = (n // 128) * (k // g) * (128 * g // 2 + 512)
         bufs.append(
-            ShapeBuffers(torch, native, name, n, k, g, args.batch, act, rotations_for(pk_bytes), args.split_k)
+            ShapeBuffers(torch, native, name, n, k, g, args.batch, act, rotations_for(pk_bytes),
+                         args.split_k, packets)
         )
     ws_bytes = max(max(b.plan["workspace_bytes"] for b in bufs), 1)
     ws = torch.zeros(ws_bytes + 256, device="cuda", dtype=torch.uint8)
     torch.cuda.synchronize()
-
     # Per-shape timing: each shape's own graph over its R rotations.
     per_shape = {}
     for b in bufs:
@@ -288,6 +299,45 @@ def main() -> int:
     step_bytes = sum(b.bytes for b in bufs)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
+    for b in bufs:
+        b.packets = [None] * len(b.packets)
+    del ws
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return bufs, per_shape, value, ms_per_step, steps, cycles_warm, R_step
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU only: this build has no multi-GPU path (asked for "
+            f"--gpus {args.gpus}). Run with --gpus 1.",
+            file=sys.stderr,
+        )
+        return 2
+    import torch
+
+    from fast_kernels.native import native_module
+
+    native = native_module()
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    if args.copy_calibration:
+        return copy_calibration(torch)
+    act, g, shapes = WORKLOADS[args.workload]
+    if args.only:
+        keep = set(args.only.split(","))
+        shapes = [s for s in shapes if s[0] in keep]
+
+    first = measure(torch, native, args, act, g, shapes, args.packets)
+    other = None
+    if not args.no_other_packets:
+        other_format = "native_sym" if args.packets == "arc" else "arc"
+        other = measure(torch, native, args, act, g, shapes, other_format)
+    bufs, per_shape, value, ms_per_step, steps, cycles_warm, R_step = first
+
     dominant = max(bufs, key=lambda b: b.bytes)
     dom = per_shape[dominant.name]
     achieved = dom["gbs"]
@@ -311,6 +361,7 @@ def main() -> int:
             "shapes": {b.name: [b.n, b.k] for b in bufs},
             "step": "one pass over the listed GEMVs, launched from a HIP graph",
             "cache_busting": "rotated weight copies > 2 x 256 MiB per shape",
+            "packets": args.packets,
         },
         "pct_peak": round(100.0 * value / PEAK_HBM_GBS, 1),
         "per_shape": per_shape,
@@ -324,6 +375,17 @@ def main() -> int:
             "traffic": measured_traffic(args.workload, dominant.name),
         },
     }
+    if other is not None:
+        o_bufs, o_per_shape, o_value, o_ms, _, _, _ = other
+        result["other_packets"] = {
+            "packets": "native_sym" if args.packets == "arc" else "arc",
+            "value": round(o_value, 1),
+            "unit": "GB/s",
+            "ms_per_step": round(o_ms, 5),
+            "pct_peak": round(100.0 * o_value / PEAK_HBM_GBS, 1),
+            "per_shape_us": {k: v["us_per_call"] for k, v in o_per_shape.items()},
+            "note": "same step and algorithmic bytes over the other packet format",
+        }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.workload, args.batch, args.cpu_seconds)
     print(json.dumps(result), flush=True)

@@ -236,4 +236,70 @@ PYBIND11_MODULE(_native, m) {
       py::arg("workspace_ptr"), py::arg("workspace_bytes"), py::arg("batch"), py::arg("n"),
       py::arg("k"), py::arg("group_size"), py::arg("packet_stride_bytes"),
       py::arg("activation_dtype"), py::arg("split_k_slices"), py::arg("stream_ptr"));
+  m.attr("PACKET_ARC") = FK_PACKET_ARC;
+  m.attr("PACKET_NATIVE_SYM") = FK_PACKET_NATIVE_SYM;
+  m.attr("PACKET_NATIVE_ASYM") = FK_PACKET_NATIVE_ASYM;
+  m.def(
+      "packet_stride_bytes",
+      [](int group_size, int packet_format) {
+        const int stride = fk_packet_stride_bytes(group_size, packet_format);
+        if (stride < 0) {
+          throw std::invalid_argument(fk_last_error());
+        }
+        return stride;
+      },
+      py::arg("group_size"), py::arg("packet_format"));
+  m.def(
+      "pack_native_w4a16_packets",
+      [](std::uintptr_t q_ptr, std::uintptr_t alpha_ptr, std::uintptr_t zero_points_ptr,
+         std::uintptr_t packets_ptr, int n, int k, int group_size, int packet_format,
+         std::uintptr_t stream_ptr) {
+        call([&] {
+          return fk_pack_native_w4a16_packets(cp(q_ptr), cp(alpha_ptr), cp(zero_points_ptr),
+                                              mp(packets_ptr), n, k, group_size, packet_format,
+                                              mp(stream_ptr));
+        });
+      },
+      py::arg("q_ptr"), py::arg("alpha_ptr"), py::arg("zero_points_ptr"), py::arg("packets_ptr"),
+      py::arg("n"), py::arg("k"), py::arg("group_size"), py::arg("packet_format"),
+      py::arg("stream_ptr"));
+  m.def(
+      "convert_arc_to_native_packets",
+      [](std::uintptr_t arc_packets_ptr, std::uintptr_t native_packets_ptr, int n, int k,
+         int group_size, int packet_format, std::uintptr_t stream_ptr) {
+        call([&] {
+          return fk_convert_arc_to_native_packets(cp(arc_packets_ptr), mp(native_packets_ptr), n,
+                                                  k, group_size, packet_format, mp(stream_ptr));
+        });
+      },
+      py::arg("arc_packets_ptr"), py::arg("native_packets_ptr"), py::arg("n"), py::arg("k"),
+      py::arg("group_size"), py::arg("packet_format"), py::arg("stream_ptr"));
+  m.def(
+      "convert_native_to_arc_packets",
+      [](std::uintptr_t native_packets_ptr, std::uintptr_t arc_packets_ptr, int n, int k,
+         int group_size, int packet_format, std::uintptr_t stream_ptr) {
+        call([&] {
+          return fk_convert_native_to_arc_packets(cp(native_packets_ptr), mp(arc_packets_ptr), n,
+                                                  k, group_size, packet_format, mp(stream_ptr));
+        });
+      },
+      py::arg("native_packets_ptr"), py::arg("arc_packets_ptr"), py::arg("n"), py::arg("k"),
+      py::arg("group_size"), py::arg("packet_format"), py::arg("stream_ptr"));
+  m.def(
+      "arc_w4a16_forward_native",
+      [](std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::uintptr_t output_ptr,
+         std::uintptr_t workspace_ptr, std::size_t workspace_bytes, int batch, int n, int k,
+         int group_size, int packet_format, int activation_dtype, int split_k_slices,
+         std::uintptr_t stream_ptr) {
+        call([&] {
+          return fk_arc_w4a16_forward_native(cp(activations_ptr), cp(packets_ptr), mp(output_ptr),
+                                             mp(workspace_ptr), workspace_bytes, batch, n, k,
+                                             group_size, packet_format, activation_dtype,
+                                             split_k_slices, mp(stream_ptr));
+        });
+      },
+      py::arg("activations_ptr"), py::arg("packets_ptr"), py::arg("output_ptr"),
+      py::arg("workspace_ptr"), py::arg("workspace_bytes"), py::arg("batch"), py::arg("n"),
+      py::arg("k"), py::arg("group_size"), py::arg("packet_format"), py::arg("activation_dtype"),
+      py::arg("split_k_slices"), py::arg("stream_ptr"));
 }

@@ -166,4 +166,47 @@ int fk_arc_w4a16_forward_ex(const void* activations, const void* packets, void* 
   });
 }
 
+int fk_packet_stride_bytes(int group_size, int packet_format) {
+  int stride = -1;
+  const int status =
+      guarded([&] { stride = ops::packet_format_stride_bytes(group_size, packet_format); });
+  return status == FK_OK ? stride : -1;
+}
+
+int fk_pack_native_w4a16_packets(const void* q, const void* alpha, const void* zero_points,
+                                 void* packets, int n, int k, int group_size, int packet_format,
+                                 void* stream) {
+  return guarded([&] {
+    ops::pack_native_w4a16_packets(P(q), P(alpha), P(zero_points), P(packets), n, k, group_size,
+                                   packet_format, P(stream));
+  });
+}
+
+int fk_convert_arc_to_native_packets(const void* arc_packets, void* native_packets, int n, int k,
+                                     int group_size, int packet_format, void* stream) {
+  return guarded([&] {
+    ops::convert_arc_w4a16_packets_to_native(P(arc_packets), P(native_packets), n, k, group_size,
+                                             packet_format, P(stream));
+  });
+}
+
+int fk_convert_native_to_arc_packets(const void* native_packets, void* arc_packets, int n, int k,
+                                     int group_size, int packet_format, void* stream) {
+  return guarded([&] {
+    ops::convert_native_w4a16_packets_to_arc(P(native_packets), P(arc_packets), n, k, group_size,
+                                             packet_format, P(stream));
+  });
+}
+
+int fk_arc_w4a16_forward_native(const void* activations, const void* packets, void* output,
+                                void* workspace, size_t workspace_bytes, int batch, int n, int k,
+                                int group_size, int packet_format, int activation_dtype,
+                                int split_k_slices, void* stream) {
+  return guarded([&] {
+    ops::arc_w4a16_forward_native(P(activations), P(packets), P(output), P(workspace),
+                                  workspace_bytes, batch, n, k, group_size, packet_format,
+                                  activation_dtype, split_k_slices, P(stream));
+  });
+}
+
 }  // extern "C"

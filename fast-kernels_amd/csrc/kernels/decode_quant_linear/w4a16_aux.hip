@@ -151,6 +151,116 @@ unsigned int blocks_for(size_t n, int threads) {
   return static_cast<unsigned int>((n + threads - 1) / threads);
 }
 
+
+// Native packets (PacketFormat in w4a16_device.h) from q_u8 / alpha / zero points: the code words
+// and alpha exactly as in pack_packets_kernel, then (kNativeAsym) the 128 zero points as nibbles,
+// column c in byte c/2 (even c low). zero_points is uint8 [N, NG] (values 0..15), unused for
+// kNativeSym.
+template <int G, PacketFormat F>
+__global__ void __launch_bounds__(kTileCols)
+pack_native_kernel(const uint8_t* __restrict__ q, const uint16_t* __restrict__ alpha,
+                   const uint8_t* __restrict__ zero_points, uint8_t* __restrict__ packets, int k,
+                   int num_groups) {
+  constexpr int kGroupBytes = G / 2;
+  constexpr int kVecs = kGroupBytes / 16;
+  constexpr int QB = kTileCols * kGroupBytes;
+  const int tile = static_cast<int>(blockIdx.x);
+  const int g = static_cast<int>(blockIdx.y);
+  const int c = static_cast<int>(threadIdx.x);
+  const size_t row = static_cast<size_t>(tile) * kTileCols + c;
+  const size_t stride = static_cast<size_t>(format_packet_stride(G, F));
+  uint8_t* packet = packets + (static_cast<size_t>(tile) * num_groups + g) * stride;
+  const uint4* src = reinterpret_cast<const uint4*>(q + row * (k / 2) + static_cast<size_t>(g) * kGroupBytes);
+  uint32_t* words = reinterpret_cast<uint32_t*>(packet);
+#pragma unroll
+  for (int v = 0; v < kVecs; ++v) {
+    const uint4 d = src[v];
+    words[(4 * v + 0) * kTileCols + c] = d.x;
+    words[(4 * v + 1) * kTileCols + c] = d.y;
+    words[(4 * v + 2) * kTileCols + c] = d.z;
+    words[(4 * v + 3) * kTileCols + c] = d.w;
+  }
+  reinterpret_cast<uint16_t*>(packet + QB)[c] = alpha[row * num_groups + g];
+  if constexpr (F == PacketFormat::kNativeAsym) {
+    if ((c & 1) == 0) {
+      const uint32_t lo = zero_points[row * num_groups + g] & 0xFu;
+      const uint32_t hi = zero_points[(row + 1) * num_groups + g] & 0xFu;
+      packet[QB + kTileCols * 2 + c / 2] = static_cast<uint8_t>(lo | (hi << 4));
+    }
+  }
+}
+
+// Reference packets -> native packets. The zero point of a (column, group) is the integer
+// zp in 0..15 with half_rn(-alpha * zp) == beta (bit for bit); kNativeSym requires zp = 8.
+// (column, group)s with no such zp raise *bad, and the caller rejects the conversion.
+template <int G, PacketFormat F>
+__global__ void __launch_bounds__(kTileCols)
+arc_to_native_kernel(const uint8_t* __restrict__ arc, uint8_t* __restrict__ native, int num_groups,
+                     uint32_t* __restrict__ bad) {
+  constexpr int QB = kTileCols * G / 2;
+  const int tile = static_cast<int>(blockIdx.x);
+  const int g = static_cast<int>(blockIdx.y);
+  const int c = static_cast<int>(threadIdx.x);
+  const size_t unit = static_cast<size_t>(tile) * num_groups + g;
+  const uint8_t* src = arc + unit * static_cast<size_t>(packet_stride_bytes(G));
+  uint8_t* dst = native + unit * static_cast<size_t>(format_packet_stride(G, F));
+  const uint32_t* sw = reinterpret_cast<const uint32_t*>(src);
+  uint32_t* dw = reinterpret_cast<uint32_t*>(dst);
+#pragma unroll
+  for (int w = 0; w < G / 8; ++w) {
+    dw[w * kTileCols + c] = sw[w * kTileCols + c];
+  }
+  const uint16_t a_bits = reinterpret_cast<const uint16_t*>(src + QB)[c];
+  const uint16_t b_bits = reinterpret_cast<const uint16_t*>(src + QB)[kTileCols + c];
+  reinterpret_cast<uint16_t*>(dst + QB)[c] = a_bits;
+  int zp = -1;
+  if constexpr (F == PacketFormat::kNativeSym) {
+    zp = neg_alpha_zp_bits(a_bits, 8) == b_bits ? 8 : -1;
+  } else {
+    for (int z = 0; z < 16; ++z) {
+      if (zp < 0 && neg_alpha_zp_bits(a_bits, static_cast<uint32_t>(z)) == b_bits) {
+        zp = z;
+      }
+    }
+  }
+  if (zp < 0) {
+    __hip_atomic_fetch_or(bad, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    zp = 0;
+  }
+  if constexpr (F == PacketFormat::kNativeAsym) {
+    const int other = __shfl_xor(zp, 1);
+    if ((c & 1) == 0) {
+      dst[QB + kTileCols * 2 + c / 2] = static_cast<uint8_t>(zp | (other << 4));
+    }
+  }
+}
+
+// Native packets -> reference packets: the same codes and alpha, beta = half_rn(-alpha * zp).
+template <int G, PacketFormat F>
+__global__ void __launch_bounds__(kTileCols)
+native_to_arc_kernel(const uint8_t* __restrict__ native, uint8_t* __restrict__ arc, int num_groups) {
+  constexpr int QB = kTileCols * G / 2;
+  const int tile = static_cast<int>(blockIdx.x);
+  const int g = static_cast<int>(blockIdx.y);
+  const int c = static_cast<int>(threadIdx.x);
+  const size_t unit = static_cast<size_t>(tile) * num_groups + g;
+  const uint8_t* src = native + unit * static_cast<size_t>(format_packet_stride(G, F));
+  uint8_t* dst = arc + unit * static_cast<size_t>(packet_stride_bytes(G));
+  const uint32_t* sw = reinterpret_cast<const uint32_t*>(src);
+  uint32_t* dw = reinterpret_cast<uint32_t*>(dst);
+#pragma unroll
+  for (int w = 0; w < G / 8; ++w) {
+    dw[w * kTileCols + c] = sw[w * kTileCols + c];
+  }
+  const uint16_t a_bits = reinterpret_cast<const uint16_t*>(src + QB)[c];
+  uint32_t zp = 8;
+  if constexpr (F == PacketFormat::kNativeAsym) {
+    zp = (src[QB + kTileCols * 2 + c / 2] >> (4 * (c & 1))) & 0xFu;
+  }
+  reinterpret_cast<uint16_t*>(dst + QB)[c] = a_bits;
+  reinterpret_cast<uint16_t*>(dst + QB)[kTileCols + c] = neg_alpha_zp_bits(a_bits, zp);
+}
+
 }  // namespace
 
 hipError_t launch_pack_packets(const void* q, const void* alpha, const void* beta, void* packets,
@@ -224,6 +334,68 @@ hipError_t launch_reduce_partials(const void* partials, void* out, int batch, in
   const size_t total = static_cast<size_t>(batch) * n;
   hipLaunchKernelGGL(reduce_partials_kernel, dim3(blocks_for(total, kAuxThreads)), dim3(kAuxThreads), 0, stream,
                      static_cast<const float*>(partials), static_cast<uint16_t*>(out), total, split_k_slices);
+  return hipGetLastError();
+}
+
+
+hipError_t launch_pack_native(const void* q, const void* alpha, const void* zero_points,
+                              void* packets, int n, int k, int group_size, PacketFormat format,
+                              hipStream_t stream) {
+  const int ng = k / group_size;
+  const dim3 grid(static_cast<unsigned int>(n / kTileCols), static_cast<unsigned int>(ng));
+  auto* qp = static_cast<const uint8_t*>(q);
+  auto* ap = static_cast<const uint16_t*>(alpha);
+  auto* zp = static_cast<const uint8_t*>(zero_points);
+  auto* pp = static_cast<uint8_t*>(packets);
+  const bool g64 = group_size == 64;
+  if (format == PacketFormat::kNativeSym) {
+    if (g64) hipLaunchKernelGGL((pack_native_kernel<64, PacketFormat::kNativeSym>), grid, dim3(kTileCols), 0, stream, qp, ap, zp, pp, k, ng);
+    else hipLaunchKernelGGL((pack_native_kernel<128, PacketFormat::kNativeSym>), grid, dim3(kTileCols), 0, stream, qp, ap, zp, pp, k, ng);
+  } else if (format == PacketFormat::kNativeAsym) {
+    if (g64) hipLaunchKernelGGL((pack_native_kernel<64, PacketFormat::kNativeAsym>), grid, dim3(kTileCols), 0, stream, qp, ap, zp, pp, k, ng);
+    else hipLaunchKernelGGL((pack_native_kernel<128, PacketFormat::kNativeAsym>), grid, dim3(kTileCols), 0, stream, qp, ap, zp, pp, k, ng);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_arc_to_native(const void* arc, void* native, int n, int k, int group_size,
+                                PacketFormat format, void* bad_flag, hipStream_t stream) {
+  const int ng = k / group_size;
+  const dim3 grid(static_cast<unsigned int>(n / kTileCols), static_cast<unsigned int>(ng));
+  auto* src = static_cast<const uint8_t*>(arc);
+  auto* dst = static_cast<uint8_t*>(native);
+  auto* bad = static_cast<uint32_t*>(bad_flag);
+  const bool g64 = group_size == 64;
+  if (format == PacketFormat::kNativeSym) {
+    if (g64) hipLaunchKernelGGL((arc_to_native_kernel<64, PacketFormat::kNativeSym>), grid, dim3(kTileCols), 0, stream, src, dst, ng, bad);
+    else hipLaunchKernelGGL((arc_to_native_kernel<128, PacketFormat::kNativeSym>), grid, dim3(kTileCols), 0, stream, src, dst, ng, bad);
+  } else if (format == PacketFormat::kNativeAsym) {
+    if (g64) hipLaunchKernelGGL((arc_to_native_kernel<64, PacketFormat::kNativeAsym>), grid, dim3(kTileCols), 0, stream, src, dst, ng, bad);
+    else hipLaunchKernelGGL((arc_to_native_kernel<128, PacketFormat::kNativeAsym>), grid, dim3(kTileCols), 0, stream, src, dst, ng, bad);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_native_to_arc(const void* native, void* arc, int n, int k, int group_size,
+                                PacketFormat format, hipStream_t stream) {
+  const int ng = k / group_size;
+  const dim3 grid(static_cast<unsigned int>(n / kTileCols), static_cast<unsigned int>(ng));
+  auto* src = static_cast<const uint8_t*>(native);
+  auto* dst = static_cast<uint8_t*>(arc);
+  const bool g64 = group_size == 64;
+  if (format == PacketFormat::kNativeSym) {
+    if (g64) hipLaunchKernelGGL((native_to_arc_kernel<64, PacketFormat::kNativeSym>), grid, dim3(kTileCols), 0, stream, src, dst, ng);
+    else hipLaunchKernelGGL((native_to_arc_kernel<128, PacketFormat::kNativeSym>), grid, dim3(kTileCols), 0, stream, src, dst, ng);
+  } else if (format == PacketFormat::kNativeAsym) {
+    if (g64) hipLaunchKernelGGL((native_to_arc_kernel<64, PacketFormat::kNativeAsym>), grid, dim3(kTileCols), 0, stream, src, dst, ng);
+    else hipLaunchKernelGGL((native_to_arc_kernel<128, PacketFormat::kNativeAsym>), grid, dim3(kTileCols), 0, stream, src, dst, ng);
+  } else {
+    return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -31,6 +31,19 @@ __host__ __device__ constexpr int packet_stride_bytes(int group_size) {
   return kTileCols * (group_size / 2) + 2 * kTileCols * 2;
 }
 
+// Packet formats. kArc: the reference's (codes, alpha[128], beta[128] fp16). The native formats
+// keep the codes and alpha and drop the fp16 offsets, which the kernels rebuild exactly:
+// kNativeSym (zero point 8 for every group: beta = half_rn(-8 alpha)) stores nothing more;
+// kNativeAsym stores the 128 int4 zero points (column c in byte c/2, even c in the low nibble)
+// and beta = half_rn(-alpha * zp), the reference recipe's definition of beta.
+enum class PacketFormat : int { kArc = 0, kNativeSym = 1, kNativeAsym = 2 };
+
+__host__ __device__ constexpr int format_packet_stride(int group_size, PacketFormat format) {
+  return kTileCols * (group_size / 2) + kTileCols * 2 +
+         (format == PacketFormat::kArc ? kTileCols * 2
+                                       : (format == PacketFormat::kNativeAsym ? kTileCols / 2 : 0));
+}
+
 __device__ __forceinline__ float half_bits_to_float(uint16_t bits) {
   return static_cast<float>(__builtin_bit_cast(_Float16, bits));
 }
@@ -52,6 +65,16 @@ __device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
 // fp32 -> fp16, round to nearest even (v_cvt_f16_f32 under the default round mode).
 __device__ __forceinline__ uint16_t float_to_half_bits(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// Bits of half_rn(-alpha * zp) for an fp16 alpha and an integer zp in 0..15, signed zeros
+// included. alpha * zp is exact in 15 bits, so one fp16 multiply rounds it exactly as the
+// reference's fp32 product then fp16 conversion does; the negation is a sign flip. (Written as
+// "(half)(-(float)alpha * zp)" the compiler may fold the conversion into an fma with a +0
+// addend, which turns the -0 of zp = 0 into +0.)
+__device__ __forceinline__ uint16_t neg_alpha_zp_bits(uint16_t alpha_bits, uint32_t zp) {
+  const _Float16 p = __builtin_bit_cast(_Float16, alpha_bits) * static_cast<_Float16>(zp);
+  return static_cast<uint16_t>(__builtin_bit_cast(uint16_t, p) ^ 0x8000u);
 }
 
 template <Act A>
@@ -81,6 +104,18 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
   } else {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf162_t, a),
                                            __builtin_bit_cast(bf162_t, b), acc, false);
+  }
+}
+
+// fp16 value of a group's offset for one column: read (kArc) or rebuilt from alpha and the zero
+// point (native formats) with the same rounding the quantizer used.
+template <PacketFormat F>
+__device__ __forceinline__ float group_offset(float alpha, uint16_t beta_bits, uint32_t zero_point) {
+  if constexpr (F == PacketFormat::kArc) {
+    return half_bits_to_float(beta_bits);
+  } else {
+    const float zp = F == PacketFormat::kNativeSym ? 8.0f : static_cast<float>(zero_point);
+    return half_bits_to_float(float_to_half_bits(-alpha * zp));  // -alpha*zp is exact in fp32
   }
 }
 

@@ -133,10 +133,10 @@ struct MfmaGroupLoad {
   static constexpr int KB = G / 32;  // MFMA k-blocks per group
   uint4 w[2][KB];                    // [half of the tile][k-block]
   uint2 alpha[2];
-  uint2 beta[2];
+  uint2 beta[2];  // kArc: 4 fp16 offsets; kNativeAsym: 4 int4 zero points in beta[h].x
 };
 
-template <int G>
+template <int G, PacketFormat F>
 __device__ __forceinline__ void mfma_load_group(MfmaGroupLoad<G>& gl, const uint8_t* packet, int lane) {
   constexpr int QB = kTileCols * G / 2;
   const int col4 = 4 * (lane % 16);
@@ -144,7 +144,11 @@ __device__ __forceinline__ void mfma_load_group(MfmaGroupLoad<G>& gl, const uint
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     gl.alpha[h] = *reinterpret_cast<const uint2*>(packet + QB + (h * 64 + col4) * 2);
-    gl.beta[h] = *reinterpret_cast<const uint2*>(packet + QB + kTileCols * 2 + (h * 64 + col4) * 2);
+    if constexpr (F == PacketFormat::kArc) {
+      gl.beta[h] = *reinterpret_cast<const uint2*>(packet + QB + kTileCols * 2 + (h * 64 + col4) * 2);
+    } else if constexpr (F == PacketFormat::kNativeAsym) {
+      gl.beta[h].x = *reinterpret_cast<const uint16_t*>(packet + QB + kTileCols * 2 + (h * 64 + col4) / 2);
+    }
 #pragma unroll
     for (int kb = 0; kb < MfmaGroupLoad<G>::KB; ++kb) {
       gl.w[h][kb] = *reinterpret_cast<const uint4*>(packet + code + kb * 4 * kWordRowBytes + h * 256);
@@ -164,7 +168,7 @@ __device__ __forceinline__ half8_t unpack_word(uint32_t w, uint32_t mask) {
   return __builtin_bit_cast(half8_t, v);
 }
 
-template <int G, Act A>
+template <int G, Act A, PacketFormat F>
 __device__ __forceinline__ void mfma_compute_group(const MfmaSmem<G>& sm, const MfmaGroupLoad<G>& ld,
                                                    int gl, int lane, uint32_t mask,
                                                    float (&y)[2][4][4]) {
@@ -204,7 +208,8 @@ __device__ __forceinline__ void mfma_compute_group(const MfmaSmem<G>& sm, const 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float alpha = half_bits_to_float(ab[j]);
-      const float c = fmaf(-1024.0f, alpha, half_bits_to_float(bb[j]));  // beta - 1024 alpha
+      const float beta = group_offset<F>(alpha, bb[j], (ld.beta[h].x >> (4 * j)) & 0xFu);
+      const float c = fmaf(-1024.0f, alpha, beta);  // beta - 1024 alpha
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         float t = fmaf(alpha, d[j][r], c * s[r]);
@@ -217,13 +222,13 @@ __device__ __forceinline__ void mfma_compute_group(const MfmaSmem<G>& sm, const 
   }
 }
 
-template <int G, Act A>
+template <int G, Act A, PacketFormat F>
 __device__ __forceinline__ void mfma_stream_groups(MfmaSmem<G>& sm, const MfmaParams& p,
                                                    const uint8_t* tile_packets, int row0, int g_lo,
                                                    int g_hi, int lane, int wave, uint32_t mask,
                                                    float (&y)[2][4][4]) {
   constexpr int kChunk = MfmaSmem<G>::kChunk;
-  const size_t stride = static_cast<size_t>(packet_stride_bytes(G));
+  const size_t stride = static_cast<size_t>(format_packet_stride(G, F));
   for (int g0 = g_lo; g0 < g_hi; g0 += kChunk) {
     const int n_chunk = min(kChunk, g_hi - g0);
     if (g0 != g_lo) {
@@ -240,8 +245,8 @@ __device__ __forceinline__ void mfma_stream_groups(MfmaSmem<G>& sm, const MfmaPa
     const uint8_t* gp = tile_packets + static_cast<size_t>(g0 + gl_base) * stride;
     const size_t step = static_cast<size_t>(kWaves) * stride;
     MfmaGroupLoad<G> buf[2];
-    mfma_load_group<G>(buf[0], gp, lane);
-    mfma_load_group<G>(buf[1], gp + static_cast<size_t>(min(1, t_last)) * step, lane);
+    mfma_load_group<G, F>(buf[0], gp, lane);
+    mfma_load_group<G, F>(buf[1], gp + static_cast<size_t>(min(1, t_last)) * step, lane);
     __builtin_amdgcn_sched_barrier(0);
     mfma_stage_store<G, A>(sm, st, n_chunk);
     lds_barrier();
@@ -250,20 +255,20 @@ __device__ __forceinline__ void mfma_stream_groups(MfmaSmem<G>& sm, const MfmaPa
     for (int blk = 0; blk + 1 < n_blocks; ++blk, t0 += 2) {
 #pragma unroll
       for (int d = 0; d < 2; ++d) {
-        mfma_compute_group<G, A>(sm, buf[d], wave + (t0 + d) * kWaves, lane, mask, y);
-        mfma_load_group<G>(buf[d], gp + static_cast<size_t>(min(t0 + 2 + d, t_last)) * step, lane);
+        mfma_compute_group<G, A, F>(sm, buf[d], wave + (t0 + d) * kWaves, lane, mask, y);
+        mfma_load_group<G, F>(buf[d], gp + static_cast<size_t>(min(t0 + 2 + d, t_last)) * step, lane);
       }
     }
 #pragma unroll
     for (int d = 0; d < 2; ++d) {
       if (t0 + d < n_w) {
-        mfma_compute_group<G, A>(sm, buf[d], wave + (t0 + d) * kWaves, lane, mask, y);
+        mfma_compute_group<G, A, F>(sm, buf[d], wave + (t0 + d) * kWaves, lane, mask, y);
       }
     }
   }
 }
 
-template <int G, Act A>
+template <int G, Act A, PacketFormat F>
 __global__ void __launch_bounds__(kThreads, 1) w4a16_gemm_mfma_kernel(MfmaParams p) {
   constexpr int kOut = kRows * kTileCols;
   __shared__ MfmaSmem<G> sm;
@@ -271,7 +276,7 @@ __global__ void __launch_bounds__(kThreads, 1) w4a16_gemm_mfma_kernel(MfmaParams
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t mask = vgpr_constant(0x000f000fu);
-  const size_t stride = static_cast<size_t>(packet_stride_bytes(G));
+  const size_t stride = static_cast<size_t>(format_packet_stride(G, F));
   const int grid = static_cast<int>(gridDim.x);
   int b = static_cast<int>(blockIdx.x);
   if (p.xcd_remap) {
@@ -290,7 +295,7 @@ __global__ void __launch_bounds__(kThreads, 1) w4a16_gemm_mfma_kernel(MfmaParams
     const int col_base = tile * kTileCols;
     float y[2][4][4] = {};
     const uint8_t* tile_packets = p.packets + static_cast<size_t>(tile) * p.NG * stride;
-    mfma_stream_groups<G, A>(sm, p, tile_packets, row0, g_lo, g_hi, lane, wave, mask, y);
+    mfma_stream_groups<G, A, F>(sm, p, tile_packets, row0, g_lo, g_hi, lane, wave, mask, y);
     // Lane l holds rows 4*(l/16)+r and columns h*64 + 4*(l%16) + j.
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -362,7 +367,7 @@ __global__ void __launch_bounds__(kThreads, 1) w4a16_gemm_mfma_kernel(MfmaParams
   }
 }
 
-template <int G, Act A>
+template <int G, Act A, PacketFormat F>
 hipError_t launch_mfma_t(const GemvLaunch& l, hipStream_t stream) {
   MfmaParams p;
   p.x = static_cast<const uint16_t*>(l.x);
@@ -381,8 +386,28 @@ hipError_t launch_mfma_t(const GemvLaunch& l, hipStream_t stream) {
   const long long total = static_cast<long long>(p.tiles) * p.mtiles * p.NG;
   const int grid = static_cast<int>((total + p.per - 1) / p.per);
   p.xcd_remap = (grid % 8 == 0) ? 1 : 0;
-  hipLaunchKernelGGL((w4a16_gemm_mfma_kernel<G, A>), dim3(grid), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((w4a16_gemm_mfma_kernel<G, A, F>), dim3(grid), dim3(kThreads), 0, stream, p);
   return hipGetLastError();
+}
+
+template <int G, PacketFormat F>
+hipError_t dispatch_act(const GemvLaunch& l, hipStream_t stream) {
+  return l.act == Act::kF16 ? launch_mfma_t<G, Act::kF16, F>(l, stream)
+                            : launch_mfma_t<G, Act::kBF16, F>(l, stream);
+}
+
+template <PacketFormat F>
+hipError_t dispatch_group(const GemvLaunch& l, hipStream_t stream) {
+  return l.group_size == 64 ? dispatch_act<64, F>(l, stream) : dispatch_act<128, F>(l, stream);
+}
+
+hipError_t dispatch_format(const GemvLaunch& l, hipStream_t stream) {
+  switch (l.format) {
+    case PacketFormat::kArc: return dispatch_group<PacketFormat::kArc>(l, stream);
+    case PacketFormat::kNativeSym: return dispatch_group<PacketFormat::kNativeSym>(l, stream);
+    case PacketFormat::kNativeAsym: return dispatch_group<PacketFormat::kNativeAsym>(l, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace
@@ -391,12 +416,7 @@ hipError_t launch_w4a16_gemm_mfma(const GemvLaunch& l, hipStream_t stream) {
   if (l.m_tile != kRows || l.mode != GemvMode::kStreamK || l.slice_cols != kTileCols) {
     return hipErrorInvalidValue;
   }
-  if (l.group_size == 64) {
-    return l.act == Act::kF16 ? launch_mfma_t<64, Act::kF16>(l, stream)
-                              : launch_mfma_t<64, Act::kBF16>(l, stream);
-  }
-  return l.act == Act::kF16 ? launch_mfma_t<128, Act::kF16>(l, stream)
-                            : launch_mfma_t<128, Act::kBF16>(l, stream);
+  return dispatch_format(l, stream);
 }
 
 }  // namespace fk

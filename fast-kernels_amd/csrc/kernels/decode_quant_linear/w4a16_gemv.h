@@ -28,6 +28,7 @@ struct GemvLaunch {
   int units_per_workgroup = 0;  // kStreamK: group units per workgroup
   int max_contributors = 0;     // kStreamK: partial slots per slice in the scratch
   int slice_cols = kTileCols;   // kStreamK: columns per workgroup slice (128, 64 or 32)
+  PacketFormat format = PacketFormat::kArc;  // kStreamK: packet format of `packets`
 };
 
 // Activation rows per m-tile for a batch: 1, 2, 4, 8 on the dot2 GEMV kernel, kMfmaRows (from
@@ -49,8 +50,9 @@ inline size_t gemv_streamk_partial_floats(int n, int batch, int m_tile, int max_
 }
 
 hipError_t launch_w4a16_gemv(const GemvLaunch& launch, hipStream_t stream);
-// Matrix-core kernel for m_tile == kMfmaRows (w4a16_gemm_mfma.hip); launch_w4a16_gemv forwards
-// such launches to it.
+// Matrix-core kernel for m_tile == kMfmaRows (w4a16_gemm_mfma.hip) and the dot2 kernels over the
+// native packet formats (w4a16_gemv_native.hip); launch_w4a16_gemv forwards such launches.
 hipError_t launch_w4a16_gemm_mfma(const GemvLaunch& launch, hipStream_t stream);
+hipError_t launch_w4a16_gemv_native(const GemvLaunch& launch, hipStream_t stream);
 
 }  // namespace fk

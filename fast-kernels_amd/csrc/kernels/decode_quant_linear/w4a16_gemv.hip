@@ -1,601 +1,10 @@
-// W4A16 GEMV / small-batch GEMM over the reference's packet layout, hand-written for gfx950.
-//
-// Computes y[m,n] = round( sum_g sum_{k in g} (alpha[n,g]*q[n,k] + beta[n,g]) * x[m,k] ), fp32
-// accumulation, output in the activation dtype (fp16 or bf16). Follows the math of the reference
-// hot loop (arc_w4a16.cu:222-297, accumulate_arc_group_range) but not its structure:
-//
-//  * 128-bit loads over column slices. A packet (arc_w4a16.cu:87-122) stores word w of column c
-//    at byte (w*128 + c)*4, so a word row is 512 contiguous bytes. A workgroup owns a slice of
-//    CW in {128, 64, 32} columns of a 128-column tile; one 64-lane dwordx4 load covers 256/CW word
-//    rows of the slice (CW*4 contiguous bytes each, whole 128-byte lines), and lane l holds the
-//    four columns 4*(l % (CW/4)) .. +3 of word row l / (CW/4). Narrow slices give small-N shapes
-//    enough workgroups to fill the chip without splitting K across workgroups.
-//  * A wave streams its own groups of the slice through D register buffers of one group each
-//    (D*G*CW/2048 = 16 dwordx4 loads in flight whatever CW), refilling each buffer as soon as
-//    it is consumed.
-//  * Register dequant with no per-element conversion: nibbles are OR-ed into fp16 mantissas
-//    (see w4a16_device.h) and multiplied by v_dot2_f32_f16 (fp32 accumulation) against
-//    activations re-paired once per workgroup in LDS. The constant bias the trick adds (1024 for
-//    low nibbles, 1024 + 16x scale for high nibbles) is removed once per group and column with
-//    per-group activation sums: sum((1024 + s*q) x) = 1024*sum(x) + s*sum(q x).
-//  * bf16 activations are converted to fp16 when staged, after scaling each (row, group) by a
-//    power of two that keeps its largest magnitude inside fp16's range; the scale is re-applied
-//    to the group's fp32 partial. Every bf16 value whose scaled magnitude is >= 2^-17 converts
-//    exactly (bf16 has 8 significant bits, fp16 normals 11), so bf16 runs the same fp16 inner
-//    loop.
-//  * Stream-K work split: the grid is sized to be resident on the chip at once and each
-//    workgroup takes an equal run of (slice, group) units, crossing slice boundaries; slices
-//    shared by several workgroups are finished in-kernel by their last contributor (see the
-//    kernel).
-//  * Logical workgroup order is remapped so that consecutive logical workgroups (the
-//    contributors of one slice) run on the same XCD: the hardware dispatches workgroup b to
-//    XCD b % 8.
-#include "w4a16_gemv.h"
-
-#include <hip/hip_runtime.h>
-
-#include <cstddef>
-#include <cstdint>
-
-#include "w4a16_device.h"
+// W4A16 GEMV launch entry points. The kernels are in w4a16_gemv_kernels.h; this file instantiates
+// the reference packet format (kArc, stream-K and the reference split-K protocol) and routes every
+// launch: 16-row m-tiles to the matrix-core kernel (w4a16_gemm_mfma.hip), native packet formats
+// to w4a16_gemv_native.hip.
+#include "w4a16_gemv_kernels.h"
 
 namespace fk {
-namespace {
-
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
-constexpr int kWordRowBytes = kTileCols * 4;
-
-
-// Geometry of a CW-column slice of a G-group packet.
-template <int G, int CW>
-struct Slice {
-  static constexpr int kLanesPerRow = CW / 4;             // lanes covering one word row
-  static constexpr int kRowsPerLoad = 64 / kLanesPerRow;  // word rows per wave-wide load
-  static constexpr int kWordRows = G / 8;                 // word rows per group
-  static constexpr int kLoads = kWordRows / kRowsPerLoad;  // dwordx4 loads per group and lane
-  static constexpr int kDepth = 16 / kLoads;              // register buffers (groups in flight)
-  static constexpr int kSlices = kTileCols / CW;
-  static_assert(kLoads >= 1 && kWordRows % kRowsPerLoad == 0, "unsupported slice");
-};
-
-// Groups whose activations are staged in LDS at once. Wide slices run two workgroups per CU, so
-// their staging area stays small; narrow slices are used when there are fewer slices than CUs
-// (one workgroup per CU) and stage more of K per barrier.
-template <int MT, int CW>
-constexpr int chunk_groups() {
-  return MT > 1 ? 16 : (CW == kTileCols ? 32 : 64);
-}
-
-template <int G, int MT, int CW>
-struct Smem {
-  static constexpr int kChunk = chunk_groups<MT, CW>();
-  static constexpr int kWordRows = G / 8;
-  static constexpr int kRowsPerLoad = Slice<G, CW>::kRowsPerLoad;
-  uint4 xs[MT][kChunk][kWordRows];        // re-paired fp16 activations, 16 B per word row
-  float2 sums[MT][kChunk][kRowsPerLoad];  // {even, odd} sums over word rows r mod kRowsPerLoad
-  float scale[MT][kChunk];                // power of two undoing the bf16 staging scale
-  float red[kWaves][MT][CW];              // cross-wave reduction
-  int last;                               // this workgroup finishes the slice
-};
-
-struct GemvParams {
-  const uint16_t* x;       // [M, K] activations (fp16 or bf16 bits)
-  const uint8_t* packets;  // [(N/128) * NG, S]
-  uint16_t* out;           // [M, N] (unused in partials mode)
-  float* partials;         // fix-up scratch or reference split-K partials [S_k, M, N]
-  uint32_t* counters;      // fix-up arrival counters, one per (slice, m-tile)
-  int M, N, K, NG;
-  int tiles, mtiles, splits, gps;  // kPartials: fixed split of every tile
-  int per;                          // stream-K: group units per workgroup
-  int max_contrib;                  // stream-K: partial slots per slice in the scratch
-  int xcd_remap;
-};
-
-template <int G, int MT, int CW>
-struct StageRegs {
-  static constexpr int kUnits = MT * chunk_groups<MT, CW>() * (G / 8);
-  static constexpr int kPerThread = (kUnits + kThreads - 1) / kThreads;
-  uint4 raw[kPerThread];
-};
-
-// Issue the global loads of one chunk's activations (16 B = one word row per unit).
-template <int G, int MT, int CW>
-__device__ __forceinline__ void stage_load(StageRegs<G, MT, CW>& st, const GemvParams& p, int row0,
-                                           int g0, int n_chunk) {
-  constexpr int WR = G / 8;
-  constexpr int kChunk = chunk_groups<MT, CW>();
-  const int tid = static_cast<int>(threadIdx.x);
-#pragma unroll
-  for (int it = 0; it < StageRegs<G, MT, CW>::kPerThread; ++it) {
-    const int u = it * kThreads + tid;
-    const int w = u % WR;
-    const int gl = (u / WR) % kChunk;
-    const int m = u / (WR * kChunk);
-    st.raw[it] = make_uint4(0u, 0u, 0u, 0u);
-    if (u < StageRegs<G, MT, CW>::kUnits && gl < n_chunk && row0 + m < p.M) {
-      const size_t off = static_cast<size_t>(row0 + m) * p.K +
-                         static_cast<size_t>(g0 + gl) * G + static_cast<size_t>(w) * 8;
-      st.raw[it] = *reinterpret_cast<const uint4*>(p.x + off);
-    }
-  }
-}
-
-
-// Convert (bf16) and re-pair the staged activations into LDS and reduce the per-(row, group,
-// word row mod R) sums, R = word rows per load. Word rows of one (m, group) are WR consecutive,
-// WR-aligned lanes, so xor-shuffles over R..WR/2 stay inside the group.
-template <int G, Act A, int MT, int CW>
-__device__ __forceinline__ void stage_store(Smem<G, MT, CW>& sm, StageRegs<G, MT, CW>& st,
-                                            int n_chunk) {
-  constexpr int WR = G / 8;
-  constexpr int R = Slice<G, CW>::kRowsPerLoad;
-  constexpr int kChunk = chunk_groups<MT, CW>();
-  const int tid = static_cast<int>(threadIdx.x);
-#pragma unroll
-  for (int it = 0; it < StageRegs<G, MT, CW>::kPerThread; ++it) {
-    const int u = it * kThreads + tid;
-    const int w = u % WR;
-    const int gl = (u / WR) % kChunk;
-    const int m = u / (WR * kChunk);
-    uint4 r = st.raw[it];
-    float undo = 1.0f;
-    if constexpr (A == Act::kBF16) {
-      const uint32_t e = group_max<WR>(
-          max(max(bf16_exp(r.x), bf16_exp(r.y)), max(bf16_exp(r.z), bf16_exp(r.w))));
-      const int shift = max(0, static_cast<int>(e) - kMaxFp16SafeBf16Exp);
-      const float s = __builtin_bit_cast(float, static_cast<uint32_t>(127 - shift) << 23);
-      undo = __builtin_bit_cast(float, static_cast<uint32_t>(127 + shift) << 23);
-      r.x = bf16_pair_to_half_pair(r.x, s);
-      r.y = bf16_pair_to_half_pair(r.y, s);
-      r.z = bf16_pair_to_half_pair(r.z, s);
-      r.w = bf16_pair_to_half_pair(r.w, s);
-    }
-    // even k: x0 x2 x4 x6 (low halves), odd k: x1 x3 x5 x7 (high halves)
-    float se = half_bits_to_float(static_cast<uint16_t>(r.x)) +
-               half_bits_to_float(static_cast<uint16_t>(r.y)) +
-               half_bits_to_float(static_cast<uint16_t>(r.z)) +
-               half_bits_to_float(static_cast<uint16_t>(r.w));
-    float so = half_bits_to_float(static_cast<uint16_t>(r.x >> 16)) +
-               half_bits_to_float(static_cast<uint16_t>(r.y >> 16)) +
-               half_bits_to_float(static_cast<uint16_t>(r.z >> 16)) +
-               half_bits_to_float(static_cast<uint16_t>(r.w >> 16));
-    if constexpr (WR == 16 && R < WR) {
-      // One 16-lane DPP row per (row, group): rotations by R, 2R, ... (one VALU op each).
-      se = row_strided_sum<R>(se);
-      so = row_strided_sum<R>(so);
-    } else if constexpr (R == 2) {
-      // Even and odd word rows of an 8-lane group: masked 8-lane DPP reductions.
-      const bool odd = (w & 1) != 0;
-      const float se_odd = group_sum<WR>(odd ? se : 0.0f);
-      const float so_odd = group_sum<WR>(odd ? so : 0.0f);
-      const float se_even = group_sum<WR>(odd ? 0.0f : se);
-      const float so_even = group_sum<WR>(odd ? 0.0f : so);
-      se = odd ? se_odd : se_even;
-      so = odd ? so_odd : so_even;
-    } else {
-#pragma unroll
-      for (int off = R; off < WR; off <<= 1) {
-        se += __shfl_xor(se, off);
-        so += __shfl_xor(so, off);
-      }
-    }
-    if (u < StageRegs<G, MT, CW>::kUnits && gl < n_chunk) {
-      sm.xs[m][gl][w] = pair_activations(r);
-      if (w < R) {
-        sm.sums[m][gl][w] = make_float2(se, so);
-      }
-      if (w == 0) {
-        sm.scale[m][gl] = undo;
-      }
-    }
-  }
-}
-
-
-template <int G, int CW>
-struct GroupLoad {
-  static constexpr int NL = Slice<G, CW>::kLoads;
-  uint4 w[NL];
-  uint2 alpha;
-  uint2 beta;
-};
-
-// Per-lane constant parts of a group's addresses inside its packet.
-struct LaneAddr {
-  int code;   // byte offset of the lane's first 16 B of codes
-  int scale;  // byte offset of the lane's 4 alphas (the betas follow 256 bytes later)
-};
-
-template <int G, int CW>
-__device__ __forceinline__ LaneAddr lane_addr(int lane, int slice) {
-  constexpr int LPR = Slice<G, CW>::kLanesPerRow;
-  const int col = slice * CW + 4 * (lane % LPR);
-  LaneAddr a;
-  a.code = (lane / LPR) * kWordRowBytes + col * 4;
-  a.scale = kTileCols * G / 2 + col * 2;
-  return a;
-}
-
-template <int G, int CW>
-__device__ __forceinline__ void load_group(GroupLoad<G, CW>& gl, const uint8_t* packet,
-                                           LaneAddr la) {
-  constexpr int R = Slice<G, CW>::kRowsPerLoad;
-  gl.alpha = *reinterpret_cast<const uint2*>(packet + la.scale);
-  gl.beta = *reinterpret_cast<const uint2*>(packet + la.scale + kTileCols * 2);
-#pragma unroll
-  for (int i = 0; i < GroupLoad<G, CW>::NL; ++i) {
-    gl.w[i] = *reinterpret_cast<const uint4*>(packet + la.code + i * R * kWordRowBytes);
-  }
-}
-
-// One group: multiply-accumulate its codes against the staged activations, then apply the
-// group's scales and remove the unpack bias:
-// y += alpha * (acc_e - 1024 S_e) + alpha/16 * (acc_o - 1024 S_o) + beta * (S_e + S_o).
-template <int G, Act A, int MT, int CW>
-__device__ __forceinline__ void compute_group(const Smem<G, MT, CW>& sm, const GroupLoad<G, CW>& ld,
-                                              int gl, int sub, uint32_t mask_lo, uint32_t mask_hi,
-                                              float (&y)[MT][4]) {
-  constexpr int NL = GroupLoad<G, CW>::NL;
-  constexpr int R = Slice<G, CW>::kRowsPerLoad;
-  constexpr uint32_t kBias = 0x64006400u;  // fp16 1024.0 pair
-  float acc_e[MT][4];
-  float acc_o[MT][4];
-#pragma unroll
-  for (int m = 0; m < MT; ++m) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      acc_e[m][j] = 0.0f;
-      acc_o[m][j] = 0.0f;
-    }
-  }
-
-#pragma unroll
-  for (int i = 0; i < NL; ++i) {
-    const int wrow = i * R + sub;
-    uint4 xp[MT];
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      xp[m] = sm.xs[m][gl][wrow];
-    }
-    const uint32_t words[4] = {ld.w[i].x, ld.w[i].y, ld.w[i].z, ld.w[i].w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t wv = words[j];
-      const uint32_t e0 = (wv & mask_lo) | kBias;  // 1024+q for k0,k4
-      const uint32_t o0 = (wv & mask_hi) | kBias;  // 1024+16q for k1,k5
-      const uint32_t w8 = wv >> 8;
-      const uint32_t e1 = (w8 & mask_lo) | kBias;  // k2,k6
-      const uint32_t o1 = (w8 & mask_hi) | kBias;  // k3,k7
-#pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        acc_e[m][j] = dot2<Act::kF16>(e0, xp[m].x, acc_e[m][j]);
-        acc_o[m][j] = dot2<Act::kF16>(o0, xp[m].y, acc_o[m][j]);
-        acc_e[m][j] = dot2<Act::kF16>(e1, xp[m].z, acc_e[m][j]);
-        acc_o[m][j] = dot2<Act::kF16>(o1, xp[m].w, acc_o[m][j]);
-      }
-    }
-  }
-
-  const uint16_t a_bits[4] = {static_cast<uint16_t>(ld.alpha.x), static_cast<uint16_t>(ld.alpha.x >> 16),
-                              static_cast<uint16_t>(ld.alpha.y), static_cast<uint16_t>(ld.alpha.y >> 16)};
-  const uint16_t b_bits[4] = {static_cast<uint16_t>(ld.beta.x), static_cast<uint16_t>(ld.beta.x >> 16),
-                              static_cast<uint16_t>(ld.beta.y), static_cast<uint16_t>(ld.beta.y >> 16)};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float a = half_bits_to_float(a_bits[j]);
-    const float b = half_bits_to_float(b_bits[j]);
-    const float a16 = a * 0.0625f;
-    const float ce = fmaf(-1024.0f, a, b);  // beta - 1024 alpha
-    const float co = fmaf(-64.0f, a, b);    // beta - 64 alpha
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const float2 s = sm.sums[m][gl][sub];
-      float t = fmaf(a, acc_e[m][j], ce * s.x);
-      t = fmaf(a16, acc_o[m][j], t);
-      t = fmaf(co, s.y, t);
-      if constexpr (A == Act::kBF16) {
-        t *= sm.scale[m][gl];
-      }
-      y[m][j] += t;
-    }
-  }
-}
-
-// Waves per SIMD the M=1 kernel must fit (caps its VGPRs at 512 / waves). Two is the measured
-// optimum: the pipelined loop needs ~170-190 VGPRs, and capping lower spills registers.
-template <int MT>
-constexpr int min_waves_per_eu() {
-  return MT == 1 ? 2 : 1;
-}
-
-// Accumulate groups [g_lo, g_hi) of one slice into y: stage the activations of up to kChunk
-// groups in LDS, then each wave streams groups g_lo + wave, g_lo + wave + 4, ... through D
-// register buffers.
-template <int G, Act A, int MT, int CW>
-__device__ __forceinline__ void stream_groups(Smem<G, MT, CW>& sm, const GemvParams& p,
-                                              const uint8_t* tile_packets, LaneAddr la, int row0,
-                                              int g_lo, int g_hi, int wave, int sub,
-                                              uint32_t mask_lo, uint32_t mask_hi,
-                                              float (&y)[MT][4]) {
-  constexpr int kChunk = chunk_groups<MT, CW>();
-  constexpr int D = Slice<G, CW>::kDepth;
-  const size_t stride = static_cast<size_t>(packet_stride_bytes(G));
-  for (int g0 = g_lo; g0 < g_hi; g0 += kChunk) {
-    const int n_chunk = min(kChunk, g_hi - g0);
-    if (g0 != g_lo) {
-      lds_barrier();  // previous chunk's readers are done with xs / sums
-    }
-    // Activation loads first, then the first D weight groups of this wave, so the LDS writes
-    // below only wait for the activations while the weights stay in flight across the barrier.
-    StageRegs<G, MT, CW> st;
-    stage_load<G, MT, CW>(st, p, row0, g0, n_chunk);
-    // This wave's groups in the chunk: gl = wave + 4t, t < n_w; buffer d holds t = d mod D.
-    // Loads are unconditional (past its last group a wave re-reads that group, an L2 hit it
-    // does not compute), so the compiler can count the loads behind any buffer and wait for that
-    // buffer alone.
-    const int n_w = n_chunk > wave ? (n_chunk - wave + kWaves - 1) / kWaves : 0;
-    const int t_last = max(n_w - 1, 0);
-    const int gl_base = n_w > 0 ? wave : n_chunk - 1;
-    const uint8_t* gp = tile_packets + static_cast<size_t>(g0 + gl_base) * stride;
-    const size_t step = static_cast<size_t>(kWaves) * stride;
-    GroupLoad<G, CW> buf[D];
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      load_group<G, CW>(buf[d], gp + static_cast<size_t>(min(d, t_last)) * step, la);
-    }
-    __builtin_amdgcn_sched_barrier(0);  // keep every load above the first use of the activations
-    stage_store<G, A, MT, CW>(sm, st, n_chunk);
-    lds_barrier();
-    // Blocks of D groups; every block but the last refills each buffer right after computing it.
-    const int n_blocks = (n_w + D - 1) / D;
-    int t0 = 0;
-    for (int blk = 0; blk + 1 < n_blocks; ++blk, t0 += D) {
-#pragma unroll
-      for (int d = 0; d < D; ++d) {
-        compute_group<G, A, MT, CW>(sm, buf[d], wave + (t0 + d) * kWaves, sub, mask_lo, mask_hi, y);
-        load_group<G, CW>(buf[d], gp + static_cast<size_t>(min(t0 + D + d, t_last)) * step, la);
-      }
-    }
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      if (t0 + d < n_w) {
-        compute_group<G, A, MT, CW>(sm, buf[d], wave + (t0 + d) * kWaves, sub, mask_lo, mask_hi, y);
-      }
-    }
-  }
-}
-
-// Sum y over the lanes that share columns (different word rows) and over the waves into sm.red.
-template <int G, int MT, int CW>
-__device__ __forceinline__ void reduce_to_lds(Smem<G, MT, CW>& sm, float (&y)[MT][4], int lane,
-                                              int wave) {
-  constexpr int LPR = Slice<G, CW>::kLanesPerRow;
-#pragma unroll
-  for (int m = 0; m < MT; ++m) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int off = LPR; off < 64; off <<= 1) {
-        y[m][j] += __shfl_xor(y[m][j], off);
-      }
-    }
-  }
-  if (lane < LPR) {
-    const int c0 = lane * 4;
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      *reinterpret_cast<float4*>(&sm.red[wave][m][c0]) = make_float4(y[m][0], y[m][1], y[m][2], y[m][3]);
-    }
-  }
-  __syncthreads();
-}
-
-template <int G, int MT, int CW>
-__device__ __forceinline__ float red_sum(const Smem<G, MT, CW>& sm, int m, int c) {
-  float v = sm.red[0][m][c];
-#pragma unroll
-  for (int w = 1; w < kWaves; ++w) {
-    v += sm.red[w][m][c];
-  }
-  return v;
-}
-
-// Work decomposition. A "slice" is CW columns of a 128-column tile for one m-tile of rows; the
-// slices laid end to end (slices of a tile, then tiles, then m-tiles) form a line of T*NG group
-// units. Workgroup b owns units [b*per, (b+1)*per): "stream-K", every workgroup gets the same
-// number of groups whatever the shape, and the grid is sized to fit on the chip at once, so no
-// workgroup waits for a second round. A slice whose units all belong to one workgroup is written
-// directly. A slice split between workgroups is finished by the last of its contributors to
-// arrive (device-scope counter), which adds the fp32 partials in workgroup order, so results do
-// not depend on arrival order; it also resets the counter, so no memset is needed between calls
-// (graph-capture friendly).
-//
-// kPartials (the reference split-K protocol, whole tiles) instead writes each workgroup's fp32
-// partial to partials[split, m, n] with split = b % splits over a fixed per-tile split.
-template <int G, Act A, int MT, GemvMode MODE, int CW>
-__global__ void __launch_bounds__(kThreads, min_waves_per_eu<MT>())
-w4a16_gemv_kernel(GemvParams p) {
-  constexpr int kOut = MT * CW;
-  constexpr int kSlices = Slice<G, CW>::kSlices;
-  __shared__ Smem<G, MT, CW> sm;
-  const int tid = static_cast<int>(threadIdx.x);
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
-  const int sub = lane / Slice<G, CW>::kLanesPerRow;         // word row within a load
-  const uint32_t mask_lo = vgpr_constant(0x000f000fu);
-  const uint32_t mask_hi = vgpr_constant(0x00f000f0u);
-  const size_t stride = static_cast<size_t>(packet_stride_bytes(G));
-
-  // Logical workgroup id: keep consecutive ids (the contributors of one slice) on one XCD.
-  const int grid = static_cast<int>(gridDim.x);
-  int b = static_cast<int>(blockIdx.x);
-  if (p.xcd_remap) {
-    b = (b & 7) * (grid >> 3) + (b >> 3);
-  }
-
-  if constexpr (MODE == GemvMode::kPartials) {
-    static_assert(CW == kTileCols, "the partials protocol runs on whole tiles");
-    const int split = b % p.splits;
-    const int T = b / p.splits;
-    const int tile = T % p.tiles;
-    const int row0 = (T / p.tiles) * MT;
-    const int g_lo = split * p.gps;
-    const int g_hi = min(p.NG, g_lo + p.gps);
-    float y[MT][4] = {};
-    const uint8_t* tile_packets = p.packets + static_cast<size_t>(tile) * p.NG * stride;
-    stream_groups<G, A, MT, CW>(sm, p, tile_packets, lane_addr<G, CW>(lane, 0), row0, g_lo, g_hi,
-                                wave, sub, mask_lo, mask_hi, y);
-    reduce_to_lds<G, MT, CW>(sm, y, lane, wave);
-    for (int idx = tid; idx < kOut; idx += kThreads) {
-      const int m = idx / CW;
-      const int c = idx % CW;
-      if (row0 + m < p.M) {
-        p.partials[(static_cast<size_t>(split) * p.M + row0 + m) * p.N + tile * kTileCols + c] =
-            red_sum(sm, m, c);
-      }
-    }
-    return;
-  } else {
-    const long long total_units = static_cast<long long>(p.tiles) * kSlices * p.mtiles * p.NG;
-    const long long u_begin = static_cast<long long>(b) * p.per;
-    const long long u_end = min(total_units, u_begin + p.per);
-    long long u = u_begin;
-    while (u < u_end) {
-      const int T = static_cast<int>(u / p.NG);
-      const int g_lo = static_cast<int>(u - static_cast<long long>(T) * p.NG);
-      const int g_hi = static_cast<int>(min(static_cast<long long>(p.NG), g_lo + (u_end - u)));
-      const int slice = T % kSlices;
-      const int tile = (T / kSlices) % p.tiles;
-      const int row0 = (T / (kSlices * p.tiles)) * MT;
-      const int col_base = tile * kTileCols + slice * CW;
-      float y[MT][4] = {};
-      const uint8_t* tile_packets = p.packets + static_cast<size_t>(tile) * p.NG * stride;
-      stream_groups<G, A, MT, CW>(sm, p, tile_packets, lane_addr<G, CW>(lane, slice), row0, g_lo,
-                                  g_hi, wave, sub, mask_lo, mask_hi, y);
-      reduce_to_lds<G, MT, CW>(sm, y, lane, wave);
-
-      const long long slice_u0 = static_cast<long long>(T) * p.NG;
-      const int first = static_cast<int>(slice_u0 / p.per);
-      const int last = static_cast<int>((slice_u0 + p.NG - 1) / p.per);
-      if (first == last) {
-        for (int idx = tid; idx < kOut; idx += kThreads) {
-          const int m = idx / CW;
-          const int c = idx % CW;
-          if (row0 + m < p.M) {
-            p.out[static_cast<size_t>(row0 + m) * p.N + col_base + c] =
-                float_to_act_bits<A>(red_sum(sm, m, c));
-          }
-        }
-      } else {
-        // Cross-workgroup hand-off without cache-wide maintenance: the partials and the counter
-        // are accessed only through agent-scope relaxed atomics, which the gfx950 memory model
-        // serves coherently across XCDs (their L2s are not coherent with each other) without
-        // the whole-L2 write-back / invalidate an agent-scope fence costs. Ordering between the
-        // partial stores and the counter increment comes from waiting for the stores to
-        // complete (vmcnt(0)) before the workgroup barrier that precedes the increment.
-        const int contributors = last - first + 1;
-        float* ws = p.partials + static_cast<size_t>(T) * p.max_contrib * kOut;
-        for (int idx = tid; idx < kOut; idx += kThreads) {
-          const int m = idx / CW;
-          const int c = idx % CW;
-          __hip_atomic_store(&ws[static_cast<size_t>(b - first) * kOut + idx], red_sum(sm, m, c),
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-        __syncthreads();
-        if (tid == 0) {
-          const uint32_t prev = __hip_atomic_fetch_add(&p.counters[T], 1u, __ATOMIC_RELAXED,
-                                                       __HIP_MEMORY_SCOPE_AGENT);
-          sm.last = (prev == static_cast<uint32_t>(contributors - 1)) ? 1 : 0;
-        }
-        __syncthreads();
-        if (sm.last) {
-          constexpr int kPer = (kOut + kThreads - 1) / kThreads;
-          float acc[kPer];
-          sum_tile_partials<kPer, kThreads>(ws, kOut, contributors, tid, acc);
-#pragma unroll
-          for (int i = 0; i < kPer; ++i) {
-            const int idx = tid + i * kThreads;
-            const int m = idx / CW;
-            const int c = idx % CW;
-            if (idx < kOut && row0 + m < p.M) {
-              p.out[static_cast<size_t>(row0 + m) * p.N + col_base + c] = float_to_act_bits<A>(acc[i]);
-            }
-          }
-          if (tid == 0) {
-            __hip_atomic_store(&p.counters[T], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-        }
-      }
-      __syncthreads();  // sm.red / sm.last are reused by the next segment
-      u += g_hi - g_lo;
-    }
-  }
-}
-
-template <int G, Act A, int MT, GemvMode MODE, int CW>
-hipError_t launch_t(const GemvLaunch& l, hipStream_t stream) {
-  GemvParams p;
-  p.x = static_cast<const uint16_t*>(l.x);
-  p.packets = static_cast<const uint8_t*>(l.packets);
-  p.out = static_cast<uint16_t*>(l.out);
-  p.partials = static_cast<float*>(l.partials);
-  p.counters = static_cast<uint32_t*>(l.counters);
-  p.M = l.M;
-  p.N = l.N;
-  p.K = l.K;
-  p.NG = l.K / G;
-  p.tiles = l.N / kTileCols;
-  p.mtiles = (l.M + MT - 1) / MT;
-  p.splits = l.splits;
-  p.gps = l.gps;
-  p.per = l.units_per_workgroup;
-  p.max_contrib = l.max_contributors;
-  int grid = 0;
-  if (MODE == GemvMode::kPartials) {
-    grid = p.tiles * p.mtiles * p.splits;
-  } else {
-    const long long total = static_cast<long long>(p.tiles) * (kTileCols / CW) * p.mtiles * p.NG;
-    grid = static_cast<int>((total + p.per - 1) / p.per);
-  }
-  p.xcd_remap = (grid % 8 == 0) ? 1 : 0;
-  hipLaunchKernelGGL((w4a16_gemv_kernel<G, A, MT, MODE, CW>), dim3(grid), dim3(kThreads), 0,
-                     stream, p);
-  return hipGetLastError();
-}
-
-template <int G, Act A, int MT>
-hipError_t dispatch_cw(const GemvLaunch& l, hipStream_t stream) {
-  if (l.mode == GemvMode::kPartials) {
-    return launch_t<G, A, MT, GemvMode::kPartials, kTileCols>(l, stream);
-  }
-  // Narrow slices serve the small-N shapes of decode (one or two activation rows); with more rows
-  // a tile's registers per lane grow with MT and the narrow-slice buffers would spill.
-  if constexpr (MT <= 2) {
-    switch (l.slice_cols) {
-      case 32: return launch_t<G, A, MT, GemvMode::kStreamK, 32>(l, stream);
-      case 64: return launch_t<G, A, MT, GemvMode::kStreamK, 64>(l, stream);
-      default: break;
-    }
-  }
-  if (l.slice_cols != kTileCols) {
-    return hipErrorInvalidValue;
-  }
-  return launch_t<G, A, MT, GemvMode::kStreamK, kTileCols>(l, stream);
-}
-
-template <int G, Act A>
-hipError_t dispatch_mt(const GemvLaunch& l, hipStream_t stream) {
-  switch (l.m_tile) {
-    case 1: return dispatch_cw<G, A, 1>(l, stream);
-    case 2: return dispatch_cw<G, A, 2>(l, stream);
-    case 4: return dispatch_cw<G, A, 4>(l, stream);
-    default: return dispatch_cw<G, A, 8>(l, stream);
-  }
-}
-
-}  // namespace
 
 int gemv_m_tile_for_batch(int batch) {
   if (batch >= kMfmaMinBatch) return kMfmaRows;
@@ -613,18 +22,10 @@ hipError_t launch_w4a16_gemv(const GemvLaunch& l, hipStream_t stream) {
   if (l.m_tile == kMfmaRows) {
     return launch_w4a16_gemm_mfma(l, stream);
   }
-  if (l.slice_cols != 32 && l.slice_cols != 64 && l.slice_cols != kTileCols) {
-    return hipErrorInvalidValue;
+  if (l.format != PacketFormat::kArc) {
+    return launch_w4a16_gemv_native(l, stream);
   }
-  if (l.mode == GemvMode::kPartials && l.slice_cols != kTileCols) {
-    return hipErrorInvalidValue;
-  }
-  if (l.group_size == 64) {
-    return l.act == Act::kF16 ? dispatch_mt<64, Act::kF16>(l, stream)
-                              : dispatch_mt<64, Act::kBF16>(l, stream);
-  }
-  return l.act == Act::kF16 ? dispatch_mt<128, Act::kF16>(l, stream)
-                            : dispatch_mt<128, Act::kBF16>(l, stream);
+  return launch_format<PacketFormat::kArc>(l, stream);
 }
 
 }  // namespace fk

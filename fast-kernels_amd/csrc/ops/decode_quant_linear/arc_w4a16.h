@@ -66,6 +66,12 @@ void cublaslt_fp16_after_dequant(std::uintptr_t activations_ptr, std::uintptr_t 
 
 enum ActivationDtype : int { kActivationF16 = 0, kActivationBF16 = 1 };
 
+// Packet formats: the reference's (codes, alpha, beta) and the native gfx950 packets, which keep
+// the reference's code and alpha layout and drop the fp16 beta: symmetric (zero point 8, nothing
+// more) or asymmetric (128 int4 zero points after alpha). Strides: 64*G + 512, 64*G + 256,
+// 64*G + 320 bytes per packet.
+enum PacketFormatCode : int { kPacketArc = 0, kPacketNativeSym = 1, kPacketNativeAsym = 2 };
+
 struct ArcW4A16Plan {
   int m_tile;                   // activation rows per tile
   int workgroups;               // grid size
@@ -92,5 +98,37 @@ void arc_w4a16_forward_ex(std::uintptr_t activations_ptr, std::uintptr_t packets
                           std::size_t workspace_bytes, int batch, int n, int k, int group_size,
                           int packet_stride_bytes, int activation_dtype, int split_k_slices,
                           std::uintptr_t stream_ptr);
+
+// Bytes per packet of a format.
+int packet_format_stride_bytes(int group_size, int packet_format);
+
+// Native packets from q_u8 [N, K/2], alpha [N, K/G] fp16 and (asymmetric only) zero_points uint8
+// [N, K/G] with values 0..15 (zero_points_ptr is ignored for the symmetric format).
+void pack_native_w4a16_packets(std::uintptr_t q_ptr, std::uintptr_t alpha_ptr,
+                               std::uintptr_t zero_points_ptr, std::uintptr_t packets_ptr, int n,
+                               int k, int group_size, int packet_format, std::uintptr_t stream_ptr);
+
+// Reference packets -> native packets. Every beta must be half_rn(-alpha * zp) for an integer
+// zp in 0..15 (zp = 8 for the symmetric format), otherwise std::invalid_argument. Synchronises
+// the stream (the check reads a device flag back).
+void convert_arc_w4a16_packets_to_native(std::uintptr_t arc_packets_ptr,
+                                         std::uintptr_t native_packets_ptr, int n, int k,
+                                         int group_size, int packet_format,
+                                         std::uintptr_t stream_ptr);
+
+// Native packets -> reference packets (beta = half_rn(-alpha * zp)); the inverse of the above,
+// bit for bit.
+void convert_native_w4a16_packets_to_arc(std::uintptr_t native_packets_ptr,
+                                         std::uintptr_t arc_packets_ptr, int n, int k,
+                                         int group_size, int packet_format,
+                                         std::uintptr_t stream_ptr);
+
+// arc_w4a16_forward_ex over packets of any format (kPacketArc, kPacketNativeSym,
+// kPacketNativeAsym); same plan, workspace contract and results.
+void arc_w4a16_forward_native(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
+                              std::uintptr_t output_ptr, std::uintptr_t workspace_ptr,
+                              std::size_t workspace_bytes, int batch, int n, int k, int group_size,
+                              int packet_format, int activation_dtype, int split_k_slices,
+                              std::uintptr_t stream_ptr);
 
 }  // namespace fast_kernels::decode_quant_linear

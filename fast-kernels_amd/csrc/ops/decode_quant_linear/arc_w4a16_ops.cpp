@@ -230,7 +230,8 @@ void* library_workspace(std::size_t bytes, hipStream_t stream) {
 
 void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::uintptr_t output_ptr,
               void* workspace, const ArcW4A16Plan& plan, int batch, int n, int k, int group_size,
-              int activation_dtype, hipStream_t stream) {
+              int activation_dtype, hipStream_t stream,
+              fk::PacketFormat format = fk::PacketFormat::kArc) {
   fk::GemvLaunch l;
   l.x = reinterpret_cast<const void*>(activations_ptr);
   l.packets = reinterpret_cast<const void*>(packets_ptr);
@@ -245,6 +246,7 @@ void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::u
   l.units_per_workgroup = plan.groups_per_workgroup;
   l.max_contributors = plan.max_tile_contributors;
   l.slice_cols = plan.slice_cols;
+  l.format = format;
   if (plan.workspace_bytes > 0) {
     l.counters = workspace;
     l.partials = static_cast<char*>(workspace) + kCounterRegionBytes;
@@ -520,13 +522,27 @@ ArcW4A16Plan plan_arc_w4a16(int batch, int n, int k, int group_size, int activat
                                      device_cu_count());
 }
 
-void arc_w4a16_forward_ex(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
-                          std::uintptr_t output_ptr, std::uintptr_t workspace_ptr,
-                          std::size_t workspace_bytes, int batch, int n, int k, int group_size,
-                          int packet_stride_bytes, int activation_dtype, int split_k_slices,
-                          std::uintptr_t stream_ptr) {
-  validate_dimensions(batch, n, k, group_size);
-  validate_packet_stride(group_size, packet_stride_bytes);
+namespace {
+
+fk::PacketFormat to_packet_format(int packet_format, bool allow_arc) {
+  switch (packet_format) {
+    case kPacketArc:
+      if (allow_arc) return fk::PacketFormat::kArc;
+      break;
+    case kPacketNativeSym: return fk::PacketFormat::kNativeSym;
+    case kPacketNativeAsym: return fk::PacketFormat::kNativeAsym;
+    default: break;
+  }
+  throw_invalid(allow_arc ? "packet_format must be 0 (reference), 1 (native symmetric) or 2 "
+                            "(native asymmetric)"
+                          : "packet_format must be 1 (native symmetric) or 2 (native asymmetric)");
+}
+
+void forward_with_format(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
+                         std::uintptr_t output_ptr, std::uintptr_t workspace_ptr,
+                         std::size_t workspace_bytes, int batch, int n, int k, int group_size,
+                         fk::PacketFormat format, int activation_dtype, int split_k_slices,
+                         std::uintptr_t stream_ptr) {
   validate_activation_dtype(activation_dtype);
   validate_forward_buffers(activations_ptr, packets_ptr, output_ptr);
   if (split_k_slices < 0) {
@@ -544,7 +560,113 @@ void arc_w4a16_forward_ex(std::uintptr_t activations_ptr, std::uintptr_t packets
     }
   }
   run_gemv(activations_ptr, packets_ptr, output_ptr, reinterpret_cast<void*>(workspace_ptr), plan,
-           batch, n, k, group_size, activation_dtype, reinterpret_cast<hipStream_t>(stream_ptr));
+           batch, n, k, group_size, activation_dtype, reinterpret_cast<hipStream_t>(stream_ptr),
+           format);
+}
+
+// One uint32 flag per device for arc -> native conversions, allocated on first use.
+void* conversion_flag() {
+  static std::array<void*, kMaxDevices> flags{};
+  static std::mutex mutex;
+  int device = 0;
+  check_hip(hipGetDevice(&device), "hipGetDevice");
+  std::lock_guard<std::mutex> lock(mutex);
+  if (flags[device] == nullptr) {
+    check_hip(hipMalloc(&flags[device], sizeof(std::uint32_t)), "hipMalloc(flag)");
+  }
+  return flags[device];
+}
+
+}  // namespace
+
+void arc_w4a16_forward_ex(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
+                          std::uintptr_t output_ptr, std::uintptr_t workspace_ptr,
+                          std::size_t workspace_bytes, int batch, int n, int k, int group_size,
+                          int packet_stride_bytes, int activation_dtype, int split_k_slices,
+                          std::uintptr_t stream_ptr) {
+  validate_dimensions(batch, n, k, group_size);
+  validate_packet_stride(group_size, packet_stride_bytes);
+  forward_with_format(activations_ptr, packets_ptr, output_ptr, workspace_ptr, workspace_bytes,
+                      batch, n, k, group_size, fk::PacketFormat::kArc, activation_dtype,
+                      split_k_slices, stream_ptr);
+}
+
+int packet_format_stride_bytes(int group_size, int packet_format) {
+  if (group_size != 64 && group_size != 128) {
+    throw_invalid("group_size must be 64 or 128");
+  }
+  return fk::format_packet_stride(group_size, to_packet_format(packet_format, true));
+}
+
+void pack_native_w4a16_packets(std::uintptr_t q_ptr, std::uintptr_t alpha_ptr,
+                               std::uintptr_t zero_points_ptr, std::uintptr_t packets_ptr, int n,
+                               int k, int group_size, int packet_format, std::uintptr_t stream_ptr) {
+  validate_dimensions(1, n, k, group_size);
+  const fk::PacketFormat format = to_packet_format(packet_format, false);
+  validate_pointer(q_ptr, 16, "q");
+  validate_pointer(alpha_ptr, 2, "alpha");
+  validate_pointer(packets_ptr, 16, "packets");
+  if (format == fk::PacketFormat::kNativeAsym) {
+    validate_pointer(zero_points_ptr, 1, "zero_points");
+  }
+  check_hip(fk::launch_pack_native(reinterpret_cast<const void*>(q_ptr),
+                                   reinterpret_cast<const void*>(alpha_ptr),
+                                   reinterpret_cast<const void*>(zero_points_ptr),
+                                   reinterpret_cast<void*>(packets_ptr), n, k, group_size, format,
+                                   reinterpret_cast<hipStream_t>(stream_ptr)),
+            "pack_native launch");
+}
+
+void convert_arc_w4a16_packets_to_native(std::uintptr_t arc_packets_ptr,
+                                         std::uintptr_t native_packets_ptr, int n, int k,
+                                         int group_size, int packet_format,
+                                         std::uintptr_t stream_ptr) {
+  validate_dimensions(1, n, k, group_size);
+  const fk::PacketFormat format = to_packet_format(packet_format, false);
+  validate_pointer(arc_packets_ptr, 16, "arc_packets");
+  validate_pointer(native_packets_ptr, 16, "native_packets");
+  const auto stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  void* flag = conversion_flag();
+  check_hip(hipMemsetAsync(flag, 0, sizeof(std::uint32_t), stream), "hipMemsetAsync(flag)");
+  check_hip(fk::launch_arc_to_native(reinterpret_cast<const void*>(arc_packets_ptr),
+                                     reinterpret_cast<void*>(native_packets_ptr), n, k, group_size,
+                                     format, flag, stream),
+            "arc_to_native launch");
+  std::uint32_t bad = 0;
+  check_hip(hipMemcpyAsync(&bad, flag, sizeof(bad), hipMemcpyDeviceToHost, stream),
+            "hipMemcpyAsync(flag)");
+  check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  if (bad != 0) {
+    throw_invalid(format == fk::PacketFormat::kNativeSym
+                      ? "packets are not symmetric: some beta is not half_rn(-8 * alpha)"
+                      : "packets are not affine int4: some beta is not half_rn(-alpha * zp) for "
+                        "an integer zero point 0..15");
+  }
+}
+
+void convert_native_w4a16_packets_to_arc(std::uintptr_t native_packets_ptr,
+                                         std::uintptr_t arc_packets_ptr, int n, int k,
+                                         int group_size, int packet_format,
+                                         std::uintptr_t stream_ptr) {
+  validate_dimensions(1, n, k, group_size);
+  const fk::PacketFormat format = to_packet_format(packet_format, false);
+  validate_pointer(native_packets_ptr, 16, "native_packets");
+  validate_pointer(arc_packets_ptr, 16, "arc_packets");
+  check_hip(fk::launch_native_to_arc(reinterpret_cast<const void*>(native_packets_ptr),
+                                     reinterpret_cast<void*>(arc_packets_ptr), n, k, group_size,
+                                     format, reinterpret_cast<hipStream_t>(stream_ptr)),
+            "native_to_arc launch");
+}
+
+void arc_w4a16_forward_native(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
+                              std::uintptr_t output_ptr, std::uintptr_t workspace_ptr,
+                              std::size_t workspace_bytes, int batch, int n, int k, int group_size,
+                              int packet_format, int activation_dtype, int split_k_slices,
+                              std::uintptr_t stream_ptr) {
+  validate_dimensions(batch, n, k, group_size);
+  forward_with_format(activations_ptr, packets_ptr, output_ptr, workspace_ptr, workspace_bytes,
+                      batch, n, k, group_size, to_packet_format(packet_format, true),
+                      activation_dtype, split_k_slices, stream_ptr);
 }
 
 }  // namespace fast_kernels::decode_quant_linear

@@ -124,6 +124,43 @@ int fk_arc_w4a16_forward_ex(const void* activations, const void* packets, void* 
                             int group_size, int packet_stride_bytes, int activation_dtype,
                             int split_k_slices, void* stream);
 
+/* Native packet formats for gfx950. They keep the reference packet's code words and alpha and
+ * drop its fp16 beta, which for int4 quantisation is always half_rn(-alpha * zp):
+ *   FK_PACKET_NATIVE_SYM   zp = 8 for every group; 64*G + 256 bytes per packet
+ *   FK_PACKET_NATIVE_ASYM  128 int4 zero points after alpha (column c in byte c/2, bits 0-3 for
+ *                          even c); 64*G + 320 bytes per packet
+ * (FK_PACKET_ARC is the reference layout above, 64*G + 512 bytes.) Results of the forward over
+ * native packets equal those over the reference packets they were converted from. */
+#define FK_PACKET_ARC 0
+#define FK_PACKET_NATIVE_SYM 1
+#define FK_PACKET_NATIVE_ASYM 2
+
+/* Bytes per packet of a format (group_size 64 or 128); -1 on invalid arguments. */
+int fk_packet_stride_bytes(int group_size, int packet_format);
+
+/* Native packets from q_u8 [N, K/2], alpha fp16 [N, K/G] and, for FK_PACKET_NATIVE_ASYM,
+ * zero_points uint8 [N, K/G] holding 0..15 (zero_points may be NULL for the symmetric format). */
+int fk_pack_native_w4a16_packets(const void* q, const void* alpha, const void* zero_points,
+                                 void* packets, int n, int k, int group_size, int packet_format,
+                                 void* stream);
+
+/* Reference packets -> native packets. FK_ERR_INVALID_ARGUMENT when some beta is not
+ * half_rn(-alpha * zp) for an integer zp in 0..15 (zp = 8 for the symmetric format). Synchronises
+ * the stream to read the check's flag back, so it is a load-time call, not a graph node. */
+int fk_convert_arc_to_native_packets(const void* arc_packets, void* native_packets, int n, int k,
+                                     int group_size, int packet_format, void* stream);
+
+/* Native packets -> reference packets, bit for bit the inverse of the conversion above. */
+int fk_convert_native_to_arc_packets(const void* native_packets, void* arc_packets, int n, int k,
+                                     int group_size, int packet_format, void* stream);
+
+/* fk_arc_w4a16_forward_ex over packets of any FK_PACKET_* format: same plan, workspace contract,
+ * graph-capture behaviour and results. */
+int fk_arc_w4a16_forward_native(const void* activations, const void* packets, void* output,
+                                void* workspace, size_t workspace_bytes, int batch, int n, int k,
+                                int group_size, int packet_format, int activation_dtype,
+                                int split_k_slices, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -158,6 +158,11 @@ def test_pybind_module_mirrors_reference_names() -> None:
         "cublaslt_fp16_after_dequant",
         "arc_w4a16_forward_ex",
         "arc_w4a16_plan",
+        "packet_stride_bytes",
+        "pack_native_w4a16_packets",
+        "convert_arc_to_native_packets",
+        "convert_native_to_arc_packets",
+        "arc_w4a16_forward_native",
     ]:
         assert hasattr(m, name), name
     info = native_build_info()
@@ -167,3 +172,36 @@ def test_pybind_module_mirrors_reference_names() -> None:
             activations_ptr=0, packets_ptr=0, group_sums_ptr=0, output_ptr=0, batch=1, n=128,
             k=256, group_size=64, packet_stride_bytes=1, stream_ptr=0,
         )
+
+
+@pytest.mark.parametrize("group_size", [64, 128])
+def test_packet_format_strides(lib: ctypes.CDLL, group_size: int) -> None:
+    """Reference packets: codes (64*G) + alpha + beta (256 + 256); native symmetric drops beta,
+    native asymmetric replaces it with 128 int4 zero points (64 bytes)."""
+    from fast_kernels.ops import packet_stride_bytes
+
+    want = {0: 64 * group_size + 512, 1: 64 * group_size + 256, 2: 64 * group_size + 320}
+    for fmt, stride in want.items():
+        assert lib.fk_packet_stride_bytes(group_size, fmt) == stride
+        assert packet_stride_bytes(group_size, fmt) == stride
+    assert packet_stride_bytes(group_size, "native_sym") == want[1]
+    assert lib.fk_packet_stride_bytes(group_size, 3) == -1
+    assert lib.fk_packet_stride_bytes(96, 1) == -1
+    with pytest.raises(ValueError):
+        packet_stride_bytes(group_size, "native")
+
+
+def test_native_format_validation_without_gpu(lib: ctypes.CDLL) -> None:
+    lib.fk_last_error.restype = ctypes.c_char_p
+    rc = lib.fk_pack_native_w4a16_packets(None, None, None, None, 128, 256, 128, 0, None)
+    assert rc == 1 and b"packet_format" in lib.fk_last_error()
+    rc = lib.fk_pack_native_w4a16_packets(None, None, None, None, 128, 256, 128, 2, None)
+    assert rc == 1 and b"must not be null" in lib.fk_last_error()
+    rc = lib.fk_convert_arc_to_native_packets(None, None, 100, 256, 128, 1, None)
+    assert rc == 1
+    rc = lib.fk_convert_native_to_arc_packets(None, None, 128, 256, 128, 7, None)
+    assert rc == 1 and b"packet_format" in lib.fk_last_error()
+    rc = lib.fk_arc_w4a16_forward_native(None, None, None, None, 0, 1, 128, 256, 128, 5, 0, 0, None)
+    assert rc == 1 and b"packet_format" in lib.fk_last_error()
+    rc = lib.fk_arc_w4a16_forward_native(None, None, None, None, 0, 1, 128, 256, 128, 1, 0, 0, None)
+    assert rc == 1 and b"must not be null" in lib.fk_last_error()
