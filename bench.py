@@ -277,6 +277,7 @@ def measure(torch, native, args, act, g, shapes, packets):
             "rotations": R,
             "groups_per_workgroup": b.plan["groups_per_workgroup"],
             "workgroups": b.plan["workgroups"],
+            "slice_cols": b.plan["slice_cols"],
         }
 
     # Whole step: R_max steps captured, each step = all shapes with that step's rotation.

@@ -133,6 +133,32 @@ def traffic(
     return {"read_scale_bytes_per_kib": rs, "write_scale_bytes_per_kib": ws, "kernels": rows}
 
 
+def _shape_row(rows: dict, threads: int, slice_cols: int | None) -> tuple[str, dict] | None:
+    """The kernel row of one bench shape: same grid, and (when given) the slice width, which the
+    GEMV kernel's template arguments carry as ", <cols>, (PacketFormat)"."""
+    hits = [
+        (k, v) for k, v in rows.items()
+        if k.endswith(f" grid={threads}")
+        and (slice_cols is None or f", {slice_cols}, (PacketFormat)" in k)
+    ]
+    return hits[0] if len(hits) == 1 else None
+
+
+def traffic_by_shape(result: dict, bench: dict) -> dict:
+    """traffic() rows keyed by the bench line's shape names (per_shape workgroups x 256 threads,
+    slice_cols), with the algorithmic bytes beside them."""
+    out = {}
+    for name, shape in bench["per_shape"].items():
+        hit = _shape_row(result["kernels"], int(shape["workgroups"]) * 256, shape.get("slice_cols"))
+        if hit is None:
+            continue
+        kernel, row = hit
+        out[name] = dict(row, kernel=kernel, grid_threads=int(shape["workgroups"]) * 256,
+                         algorithmic_bytes=int(shape["bytes"]),
+                         traffic_over_algorithmic=round(row["hbm_bytes_per_launch"] / shape["bytes"], 4))
+    return out
+
+
 def _markdown_trace(rows: list[dict]) -> str:
     lines = [
         "| kernel | grid threads | workgroups | calls | avg us | median us | min us | max us |",
@@ -159,16 +185,21 @@ def main(argv: list[str] | None = None) -> int:
     c.add_argument("--copy-write", required=True)
     c.add_argument("--copy-bytes", type=int, default=COPY_CALIBRATION_BYTES)
     c.add_argument("--filter", default="w4a16")
+    c.add_argument("--bench-json", help="bench.py line of the profiled run: key rows by shape")
     args = p.parse_args(argv)
     if args.cmd == "trace":
         print(_markdown_trace(kernel_trace_by_grid(args.directory, args.filter)))
     else:
-        print(
-            json.dumps(
-                traffic(args.fetch, args.write, args.copy_fetch, args.copy_write, args.copy_bytes, args.filter),
-                indent=1,
-            )
-        )
+        result = traffic(args.fetch, args.write, args.copy_fetch, args.copy_write, args.copy_bytes,
+                         args.filter)
+        if args.bench_json:
+            bench = json.loads(Path(args.bench_json).read_text().strip().splitlines()[-1])
+            result = {
+                "read_scale_bytes_per_kib": result["read_scale_bytes_per_kib"],
+                "write_scale_bytes_per_kib": result["write_scale_bytes_per_kib"],
+                bench["config"]["workload"]: traffic_by_shape(result, bench),
+            }
+        print(json.dumps(result, indent=1))
     return 0
 
 
