@@ -4,17 +4,18 @@ Workload (benchmark configuration 2): one Llama-70B-class layer's four M=1 decod
 group size 128, symmetric int4 (zp = 8), bf16 activations and outputs:
     qkv 10240x8192, o 8192x8192, gate_up 57344x8192, down 8192x28672.
 A "step" is one pass over the four GEMVs. Weights are random int4 codes (synthetic, seeded on the
-device), packed once into the reference packet layout (--packets arc, the default) or converted
-from it to the native symmetric packets (--packets native_sym: the same codes and alpha without
-the fp16 beta, which zp = 8 fixes); the other format is measured too and reported under
-"other_packets". Each shape has R rotated weight copies
+device), packed into the reference packet layout and, for the headline (--packets native_sym, the
+default), converted on the GPU to the native symmetric slabs: the same code words (8 codes along K
+per uint32, the reference's packing) and alphas, laid out slice-major for contiguous streaming,
+without the fp16 offsets that zp = 8 fixes. The other format (--packets arc: the reference packets
+as the drop-in entry points take them) is measured too and reported under "other_packets". Each shape has R rotated weight copies
 whose total exceeds twice the 256 MiB Infinity Cache, and consecutive steps use different copies,
 so every launch streams its weights from HBM.
 
 Timing: the launches of R steps are captured once into a HIP graph (torch.cuda.CUDAGraph) and
 replayed; HIP events on the capture stream bracket the K timed steps. value = algorithmic bytes
-per step / time per step (int4 codes + fp16 scales + activations + outputs; the packets' fp16
-beta is read but not credited).
+per step / time per step (int4 codes + fp16 scales + activations + outputs; the reference
+packets' fp16 beta, when measured, is read but not credited).
 
 Also reported: per-shape us/call and GB/s (each shape's own graph, events over >= 200 launches),
 a roofline object for the dominant kernel (gate_up), and the CPU oracle timed on the host cores
@@ -73,9 +74,9 @@ def parse_args() -> argparse.Namespace:
     p.add_argument(
         "--packets",
         choices=["arc", "native_sym"],
-        default="arc",
-        help="packet format of the headline value: the reference's (arc) or the native symmetric "
-        "one (codes and alpha only)",
+        default="native_sym",
+        help="packet format of the headline value: the native symmetric slabs (default) or the "
+        "reference packets (arc)",
     )
     p.add_argument(
         "--no-other-packets",
@@ -131,7 +132,7 @@ class ShapeBuffers:
             )
             if self.format != PACKET_FORMATS["arc"]:
                 arc = pk
-                pk = torch.empty(((n // 128) * ng, self.native_stride), device=dev, dtype=torch.uint8)
+                pk = torch.empty(((n // 32) * ng, self.native_stride), device=dev, dtype=torch.uint8)
                 native.convert_arc_to_native_packets(
                     arc.data_ptr(), pk.data_ptr(), n, k, g, self.format,
                     torch.cuda.current_stream().cuda_stream,
@@ -141,7 +142,9 @@ class ShapeBuffers:
             del q, alpha, beta
         self.x = torch.randn((batch, k), device=dev, generator=gen).to(dtype)
         self.out = torch.empty((batch, n), device=dev, dtype=dtype)
-        self.plan = dict(native.arc_w4a16_plan(batch, n, k, g, self.act_code, split_k, 0))
+        self.plan = dict(
+            native.arc_w4a16_plan(batch, n, k, g, self.act_code, split_k, 0, self.format)
+        )
         self.split_k = split_k
         self.bytes = algorithmic_bytes(batch, n, k, g)
 
@@ -196,7 +199,7 @@ def time_events(torch, run, reps: int) -> float:
     return float(start.elapsed_time(end))
 
 
-def measured_traffic(workload: str, shape: str):
+def measured_traffic(workload: str, shape: str, packets: str = "native_sym"):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 PMC summary
     (profiles/w4a16_gemv_traffic.json, FETCH_SIZE + WRITE_SIZE scaled by a plain copy of known
     size), or None when no measurement for this workload and shape is committed."""
@@ -205,7 +208,7 @@ def measured_traffic(workload: str, shape: str):
         return None
     try:
         data = json.loads(path.read_text())
-        entry = data[workload][shape]
+        entry = data[packets][workload][shape]
         return int(entry["hbm_bytes_per_launch"])
     except (KeyError, ValueError, TypeError):
         return None
@@ -368,12 +371,13 @@ def main() -> int:
         "per_shape": per_shape,
         "roofline": {
             "bound": "hbm",
-            "kernel": f"w4a16_gemv_kernel ({dominant.name} {dominant.n}x{dominant.k})",
+            "kernel": ("w4a16_gemv_native_kernel" if args.packets != "arc" else "w4a16_gemv_kernel")
+            + f" ({dominant.name} {dominant.n}x{dominant.k})",
             "achieved": achieved,
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": measured_traffic(args.workload, dominant.name),
+            "traffic": measured_traffic(args.workload, dominant.name, args.packets),
         },
     }
     if other is not None:

@@ -203,10 +203,10 @@ PYBIND11_MODULE(_native, m) {
   m.def(
       "arc_w4a16_plan",
       [](int batch, int n, int k, int group_size, int activation_dtype, int split_k_slices,
-         int cu_count) {
+         int cu_count, int packet_format) {
         fk_arc_w4a16_plan plan{};
-        check(fk_arc_w4a16_plan_for(batch, n, k, group_size, activation_dtype, split_k_slices,
-                                    cu_count, &plan));
+        check(fk_w4a16_plan_for_format(batch, n, k, group_size, activation_dtype, split_k_slices,
+                                       cu_count, packet_format, &plan));
         py::dict d;
         d["m_tile"] = plan.m_tile;
         d["workgroups"] = plan.workgroups;
@@ -218,7 +218,7 @@ PYBIND11_MODULE(_native, m) {
       },
       py::arg("batch"), py::arg("n"), py::arg("k"), py::arg("group_size"),
       py::arg("activation_dtype") = FK_ACT_F16, py::arg("split_k_slices") = 0,
-      py::arg("cu_count") = 0);
+      py::arg("cu_count") = 0, py::arg("packet_format") = FK_PACKET_ARC);
   m.def(
       "arc_w4a16_forward_ex",
       [](std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::uintptr_t output_ptr,

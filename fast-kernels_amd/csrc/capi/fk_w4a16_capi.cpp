@@ -135,23 +135,44 @@ int fk_hipblaslt_fp16_after_dequant(const void* activations, const void* q, cons
   });
 }
 
+namespace {
+
+void copy_plan(const ops::ArcW4A16Plan& p, fk_arc_w4a16_plan* plan) {
+  plan->m_tile = p.m_tile;
+  plan->workgroups = p.workgroups;
+  plan->groups_per_workgroup = p.groups_per_workgroup;
+  plan->max_tile_contributors = p.max_tile_contributors;
+  plan->workspace_bytes = p.workspace_bytes;
+  plan->slice_cols = p.slice_cols;
+}
+
+}  // namespace
+
 int fk_arc_w4a16_plan_for(int batch, int n, int k, int group_size, int activation_dtype,
                           int split_k_slices, int cu_count, fk_arc_w4a16_plan* plan) {
   return guarded([&] {
     if (plan == nullptr) {
       throw std::invalid_argument("plan must not be null");
     }
-    const ops::ArcW4A16Plan p =
-        cu_count > 0 ? ops::plan_arc_w4a16_for_cu_count(batch, n, k, group_size, activation_dtype,
-                                                        split_k_slices, cu_count)
-                     : ops::plan_arc_w4a16(batch, n, k, group_size, activation_dtype,
-                                           split_k_slices);
-    plan->m_tile = p.m_tile;
-    plan->workgroups = p.workgroups;
-    plan->groups_per_workgroup = p.groups_per_workgroup;
-    plan->max_tile_contributors = p.max_tile_contributors;
-    plan->workspace_bytes = p.workspace_bytes;
-    plan->slice_cols = p.slice_cols;
+    copy_plan(cu_count > 0 ? ops::plan_arc_w4a16_for_cu_count(batch, n, k, group_size,
+                                                              activation_dtype, split_k_slices,
+                                                              cu_count)
+                           : ops::plan_arc_w4a16(batch, n, k, group_size, activation_dtype,
+                                                 split_k_slices),
+              plan);
+  });
+}
+
+int fk_w4a16_plan_for_format(int batch, int n, int k, int group_size, int activation_dtype,
+                             int split_k_slices, int cu_count, int packet_format,
+                             fk_arc_w4a16_plan* plan) {
+  return guarded([&] {
+    if (plan == nullptr) {
+      throw std::invalid_argument("plan must not be null");
+    }
+    copy_plan(ops::plan_w4a16_for_format(batch, n, k, group_size, activation_dtype,
+                                         split_k_slices, cu_count, packet_format),
+              plan);
   });
 }
 

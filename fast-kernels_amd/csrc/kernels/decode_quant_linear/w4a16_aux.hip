@@ -152,10 +152,52 @@ unsigned int blocks_for(size_t n, int threads) {
 }
 
 
-// Native packets (PacketFormat in w4a16_device.h) from q_u8 / alpha / zero points: the code words
-// and alpha exactly as in pack_packets_kernel, then (kNativeAsym) the 128 zero points as nibbles,
-// column c in byte c/2 (even c low). zero_points is uint8 [N, NG] (values 0..15), unused for
-// kNativeSym.
+// Where column c (0..127) of tile `tile`, group g lives in the native slabs (PacketFormat in
+// w4a16_device.h): its slab and its column 16*i + n inside the slab.
+struct NativeSlot {
+  uint8_t* slab;
+  int i;
+  int n;
+};
+
+template <int G, PacketFormat F>
+__device__ __forceinline__ NativeSlot native_slot(uint8_t* packets, int tile, int g, int c,
+                                                  int num_groups) {
+  const size_t slab = (static_cast<size_t>(tile) * kSlicesPerTile + c / kSliceCols) * num_groups + g;
+  const int cs = c % kSliceCols;
+  return {packets + slab * static_cast<size_t>(format_packet_stride(G, F)), cs / 16, cs % 16};
+}
+
+// Code word w (codes k = 8w .. 8w+7 of the group) of the slot's column.
+template <int G>
+__device__ __forceinline__ uint32_t* slab_word(NativeSlot s, int w) {
+  constexpr int U = native_unit_words(G);
+  return reinterpret_cast<uint32_t*>(s.slab + native_word_offset(G, s.i, w / U, s.n, w % U));
+}
+
+template <int G>
+__device__ __forceinline__ uint16_t* slab_alpha(NativeSlot s) {
+  return reinterpret_cast<uint16_t*>(s.slab + native_alpha_offset(G)) + 2 * s.n + s.i;
+}
+
+template <int G>
+__device__ __forceinline__ uint8_t* slab_zp_byte(NativeSlot s) {
+  return s.slab + native_zp_offset(G) + s.n;
+}
+
+// Writes the zero point of this thread's column. Columns n and n + 16 of a slab share a byte;
+// they are the threads c and c + 16 of one wave.
+template <int G>
+__device__ __forceinline__ void store_zp_pair(NativeSlot s, uint32_t zp) {
+  const int lane = static_cast<int>(threadIdx.x) % 64;
+  const uint32_t hi = static_cast<uint32_t>(__shfl(static_cast<int>(zp), min(lane + 16, 63)));
+  if (s.i == 0) {
+    *slab_zp_byte<G>(s) = static_cast<uint8_t>((zp & 0xFu) | ((hi & 0xFu) << 4));
+  }
+}
+
+// Native slabs from q_u8 / alpha / zero points (uint8 [N, NG], values 0..15, unused for
+// kNativeSym). One thread per column of a (tile, group).
 template <int G, PacketFormat F>
 __global__ void __launch_bounds__(kTileCols)
 pack_native_kernel(const uint8_t* __restrict__ q, const uint16_t* __restrict__ alpha,
@@ -163,35 +205,28 @@ pack_native_kernel(const uint8_t* __restrict__ q, const uint16_t* __restrict__ a
                    int num_groups) {
   constexpr int kGroupBytes = G / 2;
   constexpr int kVecs = kGroupBytes / 16;
-  constexpr int QB = kTileCols * kGroupBytes;
   const int tile = static_cast<int>(blockIdx.x);
   const int g = static_cast<int>(blockIdx.y);
   const int c = static_cast<int>(threadIdx.x);
   const size_t row = static_cast<size_t>(tile) * kTileCols + c;
-  const size_t stride = static_cast<size_t>(format_packet_stride(G, F));
-  uint8_t* packet = packets + (static_cast<size_t>(tile) * num_groups + g) * stride;
+  const NativeSlot s = native_slot<G, F>(packets, tile, g, c, num_groups);
   const uint4* src = reinterpret_cast<const uint4*>(q + row * (k / 2) + static_cast<size_t>(g) * kGroupBytes);
-  uint32_t* words = reinterpret_cast<uint32_t*>(packet);
 #pragma unroll
   for (int v = 0; v < kVecs; ++v) {
     const uint4 d = src[v];
-    words[(4 * v + 0) * kTileCols + c] = d.x;
-    words[(4 * v + 1) * kTileCols + c] = d.y;
-    words[(4 * v + 2) * kTileCols + c] = d.z;
-    words[(4 * v + 3) * kTileCols + c] = d.w;
+    *slab_word<G>(s, 4 * v + 0) = d.x;
+    *slab_word<G>(s, 4 * v + 1) = d.y;
+    *slab_word<G>(s, 4 * v + 2) = d.z;
+    *slab_word<G>(s, 4 * v + 3) = d.w;
   }
-  reinterpret_cast<uint16_t*>(packet + QB)[c] = alpha[row * num_groups + g];
+  *slab_alpha<G>(s) = alpha[row * num_groups + g];
   if constexpr (F == PacketFormat::kNativeAsym) {
-    if ((c & 1) == 0) {
-      const uint32_t lo = zero_points[row * num_groups + g] & 0xFu;
-      const uint32_t hi = zero_points[(row + 1) * num_groups + g] & 0xFu;
-      packet[QB + kTileCols * 2 + c / 2] = static_cast<uint8_t>(lo | (hi << 4));
-    }
+    store_zp_pair<G>(s, zero_points[row * num_groups + g]);
   }
 }
 
-// Reference packets -> native packets. The zero point of a (column, group) is the integer
-// zp in 0..15 with half_rn(-alpha * zp) == beta (bit for bit); kNativeSym requires zp = 8.
+// Reference packets -> native slabs. The zero point of a (column, group) is the integer zp in
+// 0..15 with half_rn(-alpha * zp) == beta (bit for bit); kNativeSym requires zp = 8.
 // (column, group)s with no such zp raise *bad, and the caller rejects the conversion.
 template <int G, PacketFormat F>
 __global__ void __launch_bounds__(kTileCols)
@@ -203,16 +238,15 @@ arc_to_native_kernel(const uint8_t* __restrict__ arc, uint8_t* __restrict__ nati
   const int c = static_cast<int>(threadIdx.x);
   const size_t unit = static_cast<size_t>(tile) * num_groups + g;
   const uint8_t* src = arc + unit * static_cast<size_t>(packet_stride_bytes(G));
-  uint8_t* dst = native + unit * static_cast<size_t>(format_packet_stride(G, F));
+  const NativeSlot s = native_slot<G, F>(native, tile, g, c, num_groups);
   const uint32_t* sw = reinterpret_cast<const uint32_t*>(src);
-  uint32_t* dw = reinterpret_cast<uint32_t*>(dst);
 #pragma unroll
   for (int w = 0; w < G / 8; ++w) {
-    dw[w * kTileCols + c] = sw[w * kTileCols + c];
+    *slab_word<G>(s, w) = sw[w * kTileCols + c];
   }
   const uint16_t a_bits = reinterpret_cast<const uint16_t*>(src + QB)[c];
   const uint16_t b_bits = reinterpret_cast<const uint16_t*>(src + QB)[kTileCols + c];
-  reinterpret_cast<uint16_t*>(dst + QB)[c] = a_bits;
+  *slab_alpha<G>(s) = a_bits;
   int zp = -1;
   if constexpr (F == PacketFormat::kNativeSym) {
     zp = neg_alpha_zp_bits(a_bits, 8) == b_bits ? 8 : -1;
@@ -228,14 +262,11 @@ arc_to_native_kernel(const uint8_t* __restrict__ arc, uint8_t* __restrict__ nati
     zp = 0;
   }
   if constexpr (F == PacketFormat::kNativeAsym) {
-    const int other = __shfl_xor(zp, 1);
-    if ((c & 1) == 0) {
-      dst[QB + kTileCols * 2 + c / 2] = static_cast<uint8_t>(zp | (other << 4));
-    }
+    store_zp_pair<G>(s, static_cast<uint32_t>(zp));
   }
 }
 
-// Native packets -> reference packets: the same codes and alpha, beta = half_rn(-alpha * zp).
+// Native slabs -> reference packets: the same codes and alpha, beta = half_rn(-alpha * zp).
 template <int G, PacketFormat F>
 __global__ void __launch_bounds__(kTileCols)
 native_to_arc_kernel(const uint8_t* __restrict__ native, uint8_t* __restrict__ arc, int num_groups) {
@@ -244,18 +275,18 @@ native_to_arc_kernel(const uint8_t* __restrict__ native, uint8_t* __restrict__ a
   const int g = static_cast<int>(blockIdx.y);
   const int c = static_cast<int>(threadIdx.x);
   const size_t unit = static_cast<size_t>(tile) * num_groups + g;
-  const uint8_t* src = native + unit * static_cast<size_t>(format_packet_stride(G, F));
+  // The slab is only read here; native_slot takes a non-const pointer for the writers.
+  const NativeSlot s = native_slot<G, F>(const_cast<uint8_t*>(native), tile, g, c, num_groups);
   uint8_t* dst = arc + unit * static_cast<size_t>(packet_stride_bytes(G));
-  const uint32_t* sw = reinterpret_cast<const uint32_t*>(src);
   uint32_t* dw = reinterpret_cast<uint32_t*>(dst);
 #pragma unroll
   for (int w = 0; w < G / 8; ++w) {
-    dw[w * kTileCols + c] = sw[w * kTileCols + c];
+    dw[w * kTileCols + c] = *slab_word<G>(s, w);
   }
-  const uint16_t a_bits = reinterpret_cast<const uint16_t*>(src + QB)[c];
+  const uint16_t a_bits = *slab_alpha<G>(s);
   uint32_t zp = 8;
   if constexpr (F == PacketFormat::kNativeAsym) {
-    zp = (src[QB + kTileCols * 2 + c / 2] >> (4 * (c & 1))) & 0xFu;
+    zp = (*slab_zp_byte<G>(s) >> (4 * s.i)) & 0xFu;
   }
   reinterpret_cast<uint16_t*>(dst + QB)[c] = a_bits;
   reinterpret_cast<uint16_t*>(dst + QB)[kTileCols + c] = neg_alpha_zp_bits(a_bits, zp);

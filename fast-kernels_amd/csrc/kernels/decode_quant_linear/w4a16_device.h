@@ -31,17 +31,54 @@ __host__ __device__ constexpr int packet_stride_bytes(int group_size) {
   return kTileCols * (group_size / 2) + 2 * kTileCols * 2;
 }
 
-// Packet formats. kArc: the reference's (codes, alpha[128], beta[128] fp16). The native formats
-// keep the codes and alpha and drop the fp16 offsets, which the kernels rebuild exactly:
-// kNativeSym (zero point 8 for every group: beta = half_rn(-8 alpha)) stores nothing more;
-// kNativeAsym stores the 128 int4 zero points (column c in byte c/2, even c in the low nibble)
-// and beta = half_rn(-alpha * zp), the reference recipe's definition of beta.
+// Packet formats.
+//  kArc: the reference's packet (arc_w4a16.cu:87-122), one per (128-column tile, group): G/8 word
+//    rows of 512 bytes (word w of column c at byte (w*128 + c)*4), alpha[128], beta[128] fp16.
+//  kNativeSym / kNativeAsym: slabs, one per (tile, 32-column slice, group), laid out
+//    [tile][slice][group] so that the groups of a slice are one contiguous byte range. A slab
+//    holds the slice's code words in "quarter" order, then its alphas, then (kNativeAsym) its
+//    zero points. Quarter order: slice column c = 16*i + n (i = 0, 1; n < 16) has W = G/8 words,
+//    cut into four quarters of U = W/4 consecutive words; lane l = 16*t + n of a wave owns
+//    quarter t of columns n and n + 16. G = 128 (U = 4): the words of column 16*i + n, quarter t
+//    are the 16 bytes at i*1024 + l*16, so each 64-lane dwordx4 load reads 1 KB contiguous.
+//    G = 64 (U = 2): both of the lane's units share the 16 bytes at l*16 (column n first). The
+//    32 alphas follow as pairs (alpha[n], alpha[n + 16]) at 4*n; kNativeAsym adds 16 bytes of zero
+//    points, byte n = zp[n] | zp[n + 16] << 4. The fp16 offsets are not stored: the kernels rebuild
+//    beta = half_rn(-alpha * zp) exactly (zp = 8 for kNativeSym), the reference recipe's
+//    definition of beta. A lane thus applies each group's scale to two columns, and the same
+//    layout feeds the matrix cores (w4a16_gemm_mfma.hip).
 enum class PacketFormat : int { kArc = 0, kNativeSym = 1, kNativeAsym = 2 };
 
+constexpr int kSliceCols = 32;  // native formats: columns per slab
+constexpr int kSlicesPerTile = kTileCols / kSliceCols;
+
+// Native slab offsets (see above). Unit = the U words of one (column, quarter).
+__host__ __device__ constexpr int native_unit_words(int group_size) { return group_size / 32; }
+
+// Byte offset, in a slab, of word j of the unit of column 16*i + n, quarter t.
+__host__ __device__ constexpr int native_word_offset(int group_size, int i, int t, int n, int j) {
+  return group_size == 128 ? i * 1024 + (16 * t + n) * 16 + 4 * j
+                           : (16 * t + n) * 16 + i * 8 + 4 * j;
+}
+
+__host__ __device__ constexpr int native_alpha_offset(int group_size) {
+  return kSliceCols * group_size / 2;
+}
+
+__host__ __device__ constexpr int native_zp_offset(int group_size) {
+  return kSliceCols * group_size / 2 + kSliceCols * 2;
+}
+
+__host__ __device__ constexpr bool is_native(PacketFormat format) {
+  return format != PacketFormat::kArc;
+}
+
+// Bytes per packet (kArc) or per slab (native formats).
 __host__ __device__ constexpr int format_packet_stride(int group_size, PacketFormat format) {
-  return kTileCols * (group_size / 2) + kTileCols * 2 +
-         (format == PacketFormat::kArc ? kTileCols * 2
-                                       : (format == PacketFormat::kNativeAsym ? kTileCols / 2 : 0));
+  return format == PacketFormat::kArc
+             ? packet_stride_bytes(group_size)
+             : kSliceCols * (group_size / 2) + kSliceCols * 2 +
+                   (format == PacketFormat::kNativeAsym ? kSliceCols / 2 : 0);
 }
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t bits) {
@@ -190,10 +227,14 @@ __device__ __forceinline__ uint32_t move(uint32_t v) {
 
 template <int N>
 __device__ __forceinline__ float group_sum(float v) {
-  static_assert(N == 8 || N == 16, "group of 8 or 16 lanes");
+  static_assert(N == 2 || N == 4 || N == 8 || N == 16, "group of 2, 4, 8 or 16 lanes");
   v += dpp::move<dpp::kQuadXor1>(v);
-  v += dpp::move<dpp::kQuadXor2>(v);
-  v += dpp::move<dpp::kRowHalfMirror>(v);
+  if constexpr (N >= 4) {
+    v += dpp::move<dpp::kQuadXor2>(v);
+  }
+  if constexpr (N >= 8) {
+    v += dpp::move<dpp::kRowHalfMirror>(v);
+  }
   if constexpr (N == 16) {
     v += dpp::move<dpp::kRowMirror>(v);
   }

@@ -1,6 +1,6 @@
 // W4A16 small-batch GEMM (8-16 activation rows) on the gfx950 matrix cores.
 //
-// Same math and packet layout as w4a16_gemv.hip; with 8 or more rows the dot2 loop there is bound
+// Same math and packet formats as w4a16_gemv.hip; with 8 or more rows the dot2 loop there is bound
 // by VALU issue (four v_dot2 per code word per row), so here the products run on
 // v_mfma_f32_16x16x32_f16 and the VALU only unpacks nibbles:
 //
@@ -133,25 +133,51 @@ struct MfmaGroupLoad {
   static constexpr int KB = G / 32;  // MFMA k-blocks per group
   uint4 w[2][KB];                    // [half of the tile][k-block]
   uint2 alpha[2];
-  uint2 beta[2];  // kArc: 4 fp16 offsets; kNativeAsym: 4 int4 zero points in beta[h].x
+  uint2 beta[2];  // kArc: 4 fp16 offsets; kNativeAsym: the zero-point bytes of slabs 2h, 2h+1 in beta[h].x
 };
 
+// packet: the group's reference packet (kArc), or its slab of slice 0 (native formats: the slab
+// of slice s is slice_step bytes further on).
 template <int G, PacketFormat F>
-__device__ __forceinline__ void mfma_load_group(MfmaGroupLoad<G>& gl, const uint8_t* packet, int lane) {
-  constexpr int QB = kTileCols * G / 2;
+__device__ __forceinline__ void mfma_load_group(MfmaGroupLoad<G>& gl, const uint8_t* packet,
+                                                size_t slice_step, int lane) {
   const int col4 = 4 * (lane % 16);
-  const int code = (lane / 16) * kWordRowBytes + col4 * 4;
+  if constexpr (is_native(F)) {
+    // Slab s (slice s of the tile) gives this lane the quarter t = lane / 16 of its columns
+    // n = lane % 16 and n + 16: G = 128 two 16-byte units (w[s/2][2*(s%2) + i]), G = 64 one
+    // 16-byte vector holding both units (w[s/2][s%2]).
+    (void)col4;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    gl.alpha[h] = *reinterpret_cast<const uint2*>(packet + QB + (h * 64 + col4) * 2);
-    if constexpr (F == PacketFormat::kArc) {
-      gl.beta[h] = *reinterpret_cast<const uint2*>(packet + QB + kTileCols * 2 + (h * 64 + col4) * 2);
-    } else if constexpr (F == PacketFormat::kNativeAsym) {
-      gl.beta[h].x = *reinterpret_cast<const uint16_t*>(packet + QB + kTileCols * 2 + (h * 64 + col4) / 2);
+    for (int s = 0; s < kSlicesPerTile; ++s) {
+      const uint8_t* slab = packet + static_cast<size_t>(s) * slice_step;
+      const uint32_t pair = *reinterpret_cast<const uint32_t*>(slab + native_alpha_offset(G) + 4 * (lane % 16));
+      if (s % 2 == 0) {
+        gl.alpha[s / 2].x = pair;
+      } else {
+        gl.alpha[s / 2].y = pair;
+      }
+      if constexpr (F == PacketFormat::kNativeAsym) {
+        const uint32_t zb = *(slab + native_zp_offset(G) + lane % 16);
+        gl.beta[s / 2].x = (s % 2 == 0) ? zb : (gl.beta[s / 2].x | (zb << 8));
+      }
+      if constexpr (G == 128) {
+        gl.w[s / 2][2 * (s % 2)] = *reinterpret_cast<const uint4*>(slab + lane * 16);
+        gl.w[s / 2][2 * (s % 2) + 1] = *reinterpret_cast<const uint4*>(slab + 1024 + lane * 16);
+      } else {
+        gl.w[s / 2][s % 2] = *reinterpret_cast<const uint4*>(slab + lane * 16);
+      }
     }
+  } else {
+    constexpr int QB = kTileCols * G / 2;
+    const int code = (lane / 16) * kWordRowBytes + col4 * 4;
 #pragma unroll
-    for (int kb = 0; kb < MfmaGroupLoad<G>::KB; ++kb) {
-      gl.w[h][kb] = *reinterpret_cast<const uint4*>(packet + code + kb * 4 * kWordRowBytes + h * 256);
+    for (int h = 0; h < 2; ++h) {
+      gl.alpha[h] = *reinterpret_cast<const uint2*>(packet + QB + (h * 64 + col4) * 2);
+      gl.beta[h] = *reinterpret_cast<const uint2*>(packet + QB + kTileCols * 2 + (h * 64 + col4) * 2);
+#pragma unroll
+      for (int kb = 0; kb < MfmaGroupLoad<G>::KB; ++kb) {
+        gl.w[h][kb] = *reinterpret_cast<const uint4*>(packet + code + kb * 4 * kWordRowBytes + h * 256);
+      }
     }
   }
 }
@@ -173,11 +199,6 @@ __device__ __forceinline__ void mfma_compute_group(const MfmaSmem<G>& sm, const 
                                                    int gl, int lane, uint32_t mask,
                                                    float (&y)[2][4][4]) {
   constexpr int KB = MfmaGroupLoad<G>::KB;
-  half8_t a[KB];
-#pragma unroll
-  for (int kb = 0; kb < KB; ++kb) {
-    a[kb] = __builtin_bit_cast(half8_t, sm.xs[gl][kb * 4 + lane / 16][lane % 16]);
-  }
   const int r0 = 4 * (lane / 16);  // output rows r0 .. r0+3 of this lane
   const float4 s4 = *reinterpret_cast<const float4*>(&sm.sums[gl][r0]);
   float4 sc4 = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
@@ -186,6 +207,58 @@ __device__ __forceinline__ void mfma_compute_group(const MfmaSmem<G>& sm, const 
   }
   const float s[4] = {s4.x, s4.y, s4.z, s4.w};
   const float sc[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
+  if constexpr (is_native(F)) {
+    // Block (slab s, half i) = columns 32 s + 16 i + (lane % 16); its U MFMAs j multiply the
+    // lane's unit word j (k-chunk lane / 16 of the window {j, U + j, 2U + j, 3U + j}) by the
+    // activations of word U * (lane / 16) + j, all into one accumulator.
+    constexpr int U = native_unit_words(G);
+    half8_t a[U];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      a[j] = __builtin_bit_cast(half8_t, sm.xs[gl][U * (lane / 16) + j][lane % 16]);
+    }
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk) {
+      const int sl = blk / 2;  // slab
+      const int i = blk % 2;   // half of the slab
+      uint32_t words[U];
+      if constexpr (G == 128) {
+        const uint4 v = ld.w[sl / 2][2 * (sl % 2) + i];
+        words[0] = v.x;
+        words[1] = v.y;
+        words[2] = v.z;
+        words[3] = v.w;
+      } else {
+        const uint4 v = ld.w[sl / 2][sl % 2];
+        words[0] = i == 0 ? v.x : v.z;
+        words[1] = i == 0 ? v.y : v.w;
+      }
+      float4_t d = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < U; ++j) {
+        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j], unpack_word(words[j], mask), d, 0, 0, 0);
+      }
+      const uint32_t pair = (sl % 2 == 0) ? ld.alpha[sl / 2].x : ld.alpha[sl / 2].y;
+      const float alpha = half_bits_to_float(static_cast<uint16_t>(pair >> (16 * i)));
+      const uint32_t zp_byte = (ld.beta[sl / 2].x >> (8 * (sl % 2))) & 0xFFu;
+      const float beta = group_offset<F>(alpha, 0, (zp_byte >> (4 * i)) & 0xFu);
+      const float c = fmaf(-1024.0f, alpha, beta);  // beta - 1024 alpha
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float t = fmaf(alpha, d[r], c * s[r]);
+        if constexpr (A == Act::kBF16) {
+          t *= sc[r];
+        }
+        y[blk / 4][blk % 4][r] += t;
+      }
+    }
+    return;
+  }
+  half8_t a[KB];
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    a[kb] = __builtin_bit_cast(half8_t, sm.xs[gl][kb * 4 + lane / 16][lane % 16]);
+  }
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     float4_t d[4];
@@ -244,9 +317,10 @@ __device__ __forceinline__ void mfma_stream_groups(MfmaSmem<G>& sm, const MfmaPa
     const int gl_base = n_w > 0 ? wave : n_chunk - 1;
     const uint8_t* gp = tile_packets + static_cast<size_t>(g0 + gl_base) * stride;
     const size_t step = static_cast<size_t>(kWaves) * stride;
+    const size_t slice_step = static_cast<size_t>(p.NG) * stride;  // native formats
     MfmaGroupLoad<G> buf[2];
-    mfma_load_group<G, F>(buf[0], gp, lane);
-    mfma_load_group<G, F>(buf[1], gp + static_cast<size_t>(min(1, t_last)) * step, lane);
+    mfma_load_group<G, F>(buf[0], gp, slice_step, lane);
+    mfma_load_group<G, F>(buf[1], gp + static_cast<size_t>(min(1, t_last)) * step, slice_step, lane);
     __builtin_amdgcn_sched_barrier(0);
     mfma_stage_store<G, A>(sm, st, n_chunk);
     lds_barrier();
@@ -256,7 +330,8 @@ __device__ __forceinline__ void mfma_stream_groups(MfmaSmem<G>& sm, const MfmaPa
 #pragma unroll
       for (int d = 0; d < 2; ++d) {
         mfma_compute_group<G, A, F>(sm, buf[d], wave + (t0 + d) * kWaves, lane, mask, y);
-        mfma_load_group<G, F>(buf[d], gp + static_cast<size_t>(min(t0 + 2 + d, t_last)) * step, lane);
+        mfma_load_group<G, F>(buf[d], gp + static_cast<size_t>(min(t0 + 2 + d, t_last)) * step,
+                              slice_step, lane);
       }
     }
 #pragma unroll
@@ -294,15 +369,27 @@ __global__ void __launch_bounds__(kThreads, 1) w4a16_gemm_mfma_kernel(MfmaParams
     const int row0 = (T / p.tiles) * kRows;
     const int col_base = tile * kTileCols;
     float y[2][4][4] = {};
-    const uint8_t* tile_packets = p.packets + static_cast<size_t>(tile) * p.NG * stride;
+    const uint8_t* tile_packets =
+        p.packets + static_cast<size_t>(tile) * (is_native(F) ? kSlicesPerTile : 1) * p.NG * stride;
     mfma_stream_groups<G, A, F>(sm, p, tile_packets, row0, g_lo, g_hi, lane, wave, mask, y);
-    // Lane l holds rows 4*(l/16)+r and columns h*64 + 4*(l%16) + j.
+    if constexpr (is_native(F)) {
+      // Lane l holds rows 4*(l/16)+r of column 32*s + 16*i + l%16 in y[s/2][2*(s%2)+i].
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+      for (int blk = 0; blk < 8; ++blk) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        *reinterpret_cast<float4*>(&sm.red[wave][4 * (lane / 16) + r][h * 64 + 4 * (lane % 16)]) =
-            make_float4(y[h][0][r], y[h][1][r], y[h][2][r], y[h][3][r]);
+        for (int r = 0; r < 4; ++r) {
+          sm.red[wave][4 * (lane / 16) + r][16 * blk + lane % 16] = y[blk / 4][blk % 4][r];
+        }
+      }
+    } else {
+      // Lane l holds rows 4*(l/16)+r and columns h*64 + 4*(l%16) + j.
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          *reinterpret_cast<float4*>(&sm.red[wave][4 * (lane / 16) + r][h * 64 + 4 * (lane % 16)]) =
+              make_float4(y[h][0][r], y[h][1][r], y[h][2][r], y[h][3][r]);
+        }
       }
     }
     __syncthreads();

@@ -1,6 +1,6 @@
-// W4A16 GEMV / small-batch GEMM kernels (dot2 path), hand-written for gfx950. Templates only:
-// w4a16_gemv.hip instantiates them for the reference packet format, w4a16_gemv_native.hip for
-// the native formats (PacketFormat in w4a16_device.h), so the two compile in parallel.
+// W4A16 GEMV / small-batch GEMM kernels (dot2 path) over the reference packets, hand-written for
+// gfx950. Templates: w4a16_gemv.hip instantiates them; the native slab formats have their own
+// kernel (w4a16_gemv_native.hip), which shares the staging, the work split and the fix-up here.
 //
 // Computes y[m,n] = round( sum_g sum_{k in g} (alpha[n,g]*q[n,k] + beta[n,g]) * x[m,k] ), fp32
 // accumulation, output in the activation dtype (fp16 or bf16). Follows the math of the reference
@@ -202,14 +202,13 @@ struct GroupLoad {
   static constexpr int NL = Slice<G, CW>::kLoads;
   uint4 w[NL];
   uint2 alpha;
-  uint2 beta;  // kArc: 4 fp16 offsets; kNativeAsym: 4 int4 zero points in beta.x; else unused
+  uint2 beta;  // 4 fp16 offsets
 };
 
 // Per-lane constant parts of a group's addresses inside its packet.
 struct LaneAddr {
   int code;   // byte offset of the lane's first 16 B of codes
-  int scale;  // byte offset of the lane's 4 alphas (kArc: the betas follow 256 bytes later)
-  int zp;     // kNativeAsym: byte offset of the lane's 4 zero points (2 bytes)
+  int scale;  // byte offset of the lane's 4 alphas (the betas follow 256 bytes later)
 };
 
 template <int G, int CW>
@@ -219,20 +218,16 @@ __device__ __forceinline__ LaneAddr lane_addr(int lane, int slice) {
   LaneAddr a;
   a.code = (lane / LPR) * kWordRowBytes + col * 4;
   a.scale = kTileCols * G / 2 + col * 2;
-  a.zp = kTileCols * G / 2 + kTileCols * 2 + col / 2;
   return a;
 }
 
 template <int G, int CW, PacketFormat F>
 __device__ __forceinline__ void load_group(GroupLoad<G, CW, F>& gl, const uint8_t* packet,
                                            LaneAddr la) {
+  static_assert(F == PacketFormat::kArc, "native slabs are read by w4a16_gemv_native.hip");
   constexpr int R = Slice<G, CW>::kRowsPerLoad;
   gl.alpha = *reinterpret_cast<const uint2*>(packet + la.scale);
-  if constexpr (F == PacketFormat::kArc) {
-    gl.beta = *reinterpret_cast<const uint2*>(packet + la.scale + kTileCols * 2);
-  } else if constexpr (F == PacketFormat::kNativeAsym) {
-    gl.beta.x = *reinterpret_cast<const uint16_t*>(packet + la.zp);
-  }
+  gl.beta = *reinterpret_cast<const uint2*>(packet + la.scale + kTileCols * 2);
 #pragma unroll
   for (int i = 0; i < GroupLoad<G, CW, F>::NL; ++i) {
     gl.w[i] = *reinterpret_cast<const uint4*>(packet + la.code + i * R * kWordRowBytes);
@@ -412,6 +407,68 @@ __device__ __forceinline__ float red_sum(const Smem<G, MT, CW>& sm, int m, int c
   return v;
 }
 
+// Writes the totals of one run of slice T (value(m, c) for row row0 + m, column col_base + c).
+// A run that covers the whole slice writes them directly. Otherwise the slice's contributors hand
+// off through the workspace without cache-wide maintenance: partials and the arrival counter are
+// accessed only through agent-scope relaxed atomics, which the gfx950 memory model serves
+// coherently across XCDs (their L2s are not coherent with each other) without the whole-L2
+// write-back / invalidate an agent-scope fence costs; ordering between a contributor's partial
+// stores and its counter increment comes from waiting for the stores to complete (vmcnt(0))
+// before the workgroup barrier that precedes the increment. The last contributor to arrive adds
+// the partials in contributor order (deterministic) and resets the counter. `last` is an LDS
+// flag. Ends with a workgroup barrier, so LDS used by value() can be reused afterwards.
+template <Act A, int MT, int CW, class Value>
+__device__ __forceinline__ void finish_run(const GemvParams& p, int T, int b, int row0, int col_base,
+                                           int& last, Value value) {
+  constexpr int kOut = MT * CW;
+  const int tid = static_cast<int>(threadIdx.x);
+  const long long slice_u0 = static_cast<long long>(T) * p.NG;
+  const int first_wg = static_cast<int>(slice_u0 / p.per);
+  const int last_wg = static_cast<int>((slice_u0 + p.NG - 1) / p.per);
+  if (first_wg == last_wg) {
+    for (int idx = tid; idx < kOut; idx += kThreads) {
+      const int m = idx / CW;
+      const int c = idx % CW;
+      if (row0 + m < p.M) {
+        p.out[static_cast<size_t>(row0 + m) * p.N + col_base + c] = float_to_act_bits<A>(value(m, c));
+      }
+    }
+  } else {
+    const int contributors = last_wg - first_wg + 1;
+    float* ws = p.partials + static_cast<size_t>(T) * p.max_contrib * kOut;
+    for (int idx = tid; idx < kOut; idx += kThreads) {
+      __hip_atomic_store(&ws[static_cast<size_t>(b - first_wg) * kOut + idx], value(idx / CW, idx % CW),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t prev = __hip_atomic_fetch_add(&p.counters[T], 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+      last = (prev == static_cast<uint32_t>(contributors - 1)) ? 1 : 0;
+    }
+    __syncthreads();
+    if (last) {
+      constexpr int kPer = (kOut + kThreads - 1) / kThreads;
+      float acc[kPer];
+      sum_tile_partials<kPer, kThreads>(ws, kOut, contributors, tid, acc);
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int idx = tid + i * kThreads;
+        const int m = idx / CW;
+        const int c = idx % CW;
+        if (idx < kOut && row0 + m < p.M) {
+          p.out[static_cast<size_t>(row0 + m) * p.N + col_base + c] = float_to_act_bits<A>(acc[i]);
+        }
+      }
+      if (tid == 0) {
+        __hip_atomic_store(&p.counters[T], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  __syncthreads();
+}
+
 // Work decomposition. A "slice" is CW columns of a 128-column tile for one m-tile of rows; the
 // slices laid end to end (slices of a tile, then tiles, then m-tiles) form a line of T*NG group
 // units. Workgroup b owns units [b*per, (b+1)*per): "stream-K", every workgroup gets the same
@@ -486,60 +543,8 @@ w4a16_gemv_kernel(GemvParams p) {
                                      g_lo, g_hi, wave, sub, mask_lo, mask_hi, y);
       reduce_to_lds<G, MT, CW>(sm, y, lane, wave);
 
-      const long long slice_u0 = static_cast<long long>(T) * p.NG;
-      const int first = static_cast<int>(slice_u0 / p.per);
-      const int last = static_cast<int>((slice_u0 + p.NG - 1) / p.per);
-      if (first == last) {
-        for (int idx = tid; idx < kOut; idx += kThreads) {
-          const int m = idx / CW;
-          const int c = idx % CW;
-          if (row0 + m < p.M) {
-            p.out[static_cast<size_t>(row0 + m) * p.N + col_base + c] =
-                float_to_act_bits<A>(red_sum(sm, m, c));
-          }
-        }
-      } else {
-        // Cross-workgroup hand-off without cache-wide maintenance: the partials and the counter
-        // are accessed only through agent-scope relaxed atomics, which the gfx950 memory model
-        // serves coherently across XCDs (their L2s are not coherent with each other) without
-        // the whole-L2 write-back / invalidate an agent-scope fence costs. Ordering between the
-        // partial stores and the counter increment comes from waiting for the stores to
-        // complete (vmcnt(0)) before the workgroup barrier that precedes the increment.
-        const int contributors = last - first + 1;
-        float* ws = p.partials + static_cast<size_t>(T) * p.max_contrib * kOut;
-        for (int idx = tid; idx < kOut; idx += kThreads) {
-          const int m = idx / CW;
-          const int c = idx % CW;
-          __hip_atomic_store(&ws[static_cast<size_t>(b - first) * kOut + idx], red_sum(sm, m, c),
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-        __syncthreads();
-        if (tid == 0) {
-          const uint32_t prev = __hip_atomic_fetch_add(&p.counters[T], 1u, __ATOMIC_RELAXED,
-                                                       __HIP_MEMORY_SCOPE_AGENT);
-          sm.last = (prev == static_cast<uint32_t>(contributors - 1)) ? 1 : 0;
-        }
-        __syncthreads();
-        if (sm.last) {
-          constexpr int kPer = (kOut + kThreads - 1) / kThreads;
-          float acc[kPer];
-          sum_tile_partials<kPer, kThreads>(ws, kOut, contributors, tid, acc);
-#pragma unroll
-          for (int i = 0; i < kPer; ++i) {
-            const int idx = tid + i * kThreads;
-            const int m = idx / CW;
-            const int c = idx % CW;
-            if (idx < kOut && row0 + m < p.M) {
-              p.out[static_cast<size_t>(row0 + m) * p.N + col_base + c] = float_to_act_bits<A>(acc[i]);
-            }
-          }
-          if (tid == 0) {
-            __hip_atomic_store(&p.counters[T], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-        }
-      }
-      __syncthreads();  // sm.red / sm.last are reused by the next segment
+      finish_run<A, MT, CW>(p, T, b, row0, col_base, sm.last,
+                            [&](int m, int c) { return red_sum(sm, m, c); });
       u += g_hi - g_lo;
     }
   }
@@ -579,11 +584,7 @@ hipError_t launch_t(const GemvLaunch& l, hipStream_t stream) {
 template <int G, Act A, int MT, PacketFormat F>
 hipError_t dispatch_cw(const GemvLaunch& l, hipStream_t stream) {
   if (l.mode == GemvMode::kPartials) {
-    if constexpr (F == PacketFormat::kArc) {
-      return launch_t<G, A, MT, GemvMode::kPartials, kTileCols, F>(l, stream);
-    } else {
-      return hipErrorInvalidValue;  // the reference split-K protocol reads reference packets
-    }
+    return launch_t<G, A, MT, GemvMode::kPartials, kTileCols, F>(l, stream);
   }
   // Narrow slices serve the small-N shapes of decode (one or two activation rows); with more rows
   // a tile's registers per lane grow with MT and the narrow-slice buffers would spill.

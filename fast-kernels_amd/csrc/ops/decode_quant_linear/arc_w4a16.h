@@ -66,10 +66,11 @@ void cublaslt_fp16_after_dequant(std::uintptr_t activations_ptr, std::uintptr_t 
 
 enum ActivationDtype : int { kActivationF16 = 0, kActivationBF16 = 1 };
 
-// Packet formats: the reference's (codes, alpha, beta) and the native gfx950 packets, which keep
-// the reference's code and alpha layout and drop the fp16 beta: symmetric (zero point 8, nothing
-// more) or asymmetric (128 int4 zero points after alpha). Strides: 64*G + 512, 64*G + 256,
-// 64*G + 320 bytes per packet.
+// Packet formats: the reference's packets (codes, alpha, beta per 128-column tile and group,
+// 64*G + 512 bytes) and the native gfx950 slabs, one per (tile, 32-column slice, group) in
+// [tile][slice][group] order, holding the slice's code words and alpha and, instead of the fp16
+// beta, nothing (symmetric, zero point 8: 16*G + 64 bytes) or 32 int4 zero points (asymmetric:
+// 16*G + 80 bytes). A native buffer is [(N/32) * K/G, slab bytes].
 enum PacketFormatCode : int { kPacketArc = 0, kPacketNativeSym = 1, kPacketNativeAsym = 2 };
 
 struct ArcW4A16Plan {
@@ -98,6 +99,12 @@ void arc_w4a16_forward_ex(std::uintptr_t activations_ptr, std::uintptr_t packets
                           std::size_t workspace_bytes, int batch, int n, int k, int group_size,
                           int packet_stride_bytes, int activation_dtype, int split_k_slices,
                           std::uintptr_t stream_ptr);
+
+// Launch plan of arc_w4a16_forward_native for packets of the given format (kPacket*): the
+// reference-format plan for kPacketArc and for the matrix-core batches, 32-column slices
+// otherwise. cu_count = 0 queries the current device.
+ArcW4A16Plan plan_w4a16_for_format(int batch, int n, int k, int group_size, int activation_dtype,
+                                   int split_k_slices, int cu_count, int packet_format);
 
 // Bytes per packet of a format.
 int packet_format_stride_bytes(int group_size, int packet_format);

@@ -121,6 +121,49 @@ constexpr int kMaxRunGroups = 64;
 // Narrowest column slice (the GEMV kernel serves 128, 64 and 32 columns per workgroup).
 constexpr int kMaxSlicesPerTile = 4;
 
+// Grid, run length and fix-up workspace of a stream-K plan over tiles x slices x num_groups units.
+void finish_plan(ArcW4A16Plan& plan, long long tiles, long long slices, int num_groups,
+                 long long per, int n, int batch) {
+  plan.slice_cols = static_cast<int>(fk::kTileCols / slices);
+  const long long units = tiles * slices * num_groups;
+  const long long workgroups = (units + per - 1) / per;
+  if (workgroups > 0x7fffffffLL || per > 0x7fffffffLL) {
+    throw_invalid("shape too large for one launch");
+  }
+  plan.workgroups = static_cast<int>(workgroups);
+  plan.groups_per_workgroup = static_cast<int>(per);
+  const bool aligned = per % num_groups == 0;  // every slice lies inside one run
+  plan.max_tile_contributors = aligned ? 1 : static_cast<int>((num_groups + per - 1) / per + 1);
+  if (aligned) {
+    plan.workspace_bytes = 0;
+  } else {
+    if (static_cast<std::size_t>(tiles * slices) > kMaxFixupCounters) {
+      throw_invalid("n * ceil(batch / m_tile) / 128 exceeds the split tile capacity (16384)");
+    }
+    plan.workspace_bytes =
+        kCounterRegionBytes + fk::gemv_streamk_partial_floats(n, batch, plan.m_tile,
+                                                              plan.max_tile_contributors) *
+                                  sizeof(float);
+  }
+}
+
+fk::PacketFormat to_packet_format(int packet_format, bool allow_arc) {
+  switch (packet_format) {
+    case kPacketArc:
+      if (allow_arc) return fk::PacketFormat::kArc;
+      break;
+    case kPacketNativeSym: return fk::PacketFormat::kNativeSym;
+    case kPacketNativeAsym: return fk::PacketFormat::kNativeAsym;
+    default: break;
+  }
+  throw_invalid(allow_arc ? "packet_format must be 0 (reference), 1 (native symmetric) or 2 "
+                            "(native asymmetric)"
+                          : "packet_format must be 1 (native symmetric) or 2 (native asymmetric)");
+}
+
+// Native slabs: shortest K run worth splitting a slice across workgroups.
+constexpr int kMinNativeRunGroups = 32;
+
 }  // namespace
 
 ArcW4A16Plan plan_arc_w4a16_for_cu_count(int batch, int n, int k, int group_size,
@@ -169,27 +212,43 @@ ArcW4A16Plan plan_arc_w4a16_for_cu_count(int batch, int n, int k, int group_size
     }
     per = (num_groups + s_split - 1) / s_split;
   }
-  plan.slice_cols = static_cast<int>(fk::kTileCols / slices);
-  const long long units = tiles * slices * num_groups;
-  const long long workgroups = (units + per - 1) / per;
-  if (workgroups > 0x7fffffffLL || per > 0x7fffffffLL) {
-    throw_invalid("shape too large for one launch");
+  finish_plan(plan, tiles, slices, num_groups, per, n, batch);
+  return plan;
+}
+
+ArcW4A16Plan plan_w4a16_for_format(int batch, int n, int k, int group_size, int activation_dtype,
+                                   int split_k_slices, int cu_count, int packet_format) {
+  const fk::PacketFormat format = to_packet_format(packet_format, true);
+  validate_dimensions(batch, n, k, group_size);
+  if (cu_count == 0) {
+    cu_count = device_cu_count();
   }
-  plan.workgroups = static_cast<int>(workgroups);
-  plan.groups_per_workgroup = static_cast<int>(per);
-  const bool aligned = per % num_groups == 0;  // every slice lies inside one run
-  plan.max_tile_contributors = aligned ? 1 : static_cast<int>((num_groups + per - 1) / per + 1);
-  if (aligned) {
-    plan.workspace_bytes = 0;
+  ArcW4A16Plan plan = plan_arc_w4a16_for_cu_count(batch, n, k, group_size, activation_dtype,
+                                                  split_k_slices, cu_count);
+  if (format == fk::PacketFormat::kArc || plan.m_tile == fk::kMfmaRows) {
+    return plan;  // the matrix-core kernel reads whole tiles in every format
+  }
+  // Native slabs: stream-K over 32-column slices, whose groups are contiguous in memory. Measured
+  // on MI355X over the Llama-7B/8B/70B decode shapes: a workgroup per whole slice, over all of K,
+  // whatever the slice count (more slices than resident workgroups simply run in later rounds).
+  // Only when the slices leave at least half the CUs idle and K is long is K split (power of two),
+  // keeping runs of at least kMinNativeRunGroups groups, since the fix-up of a split slice costs
+  // about as much as streaming 30 groups.
+  const int num_groups = k / group_size;
+  const long long slices = static_cast<long long>(fk::gemv_tiles(n, batch, plan.m_tile)) * fk::kSlicesPerTile;
+  long long per = 0;
+  if (split_k_slices > 0) {
+    const int s_req = std::min(split_k_slices, num_groups);
+    per = (num_groups + s_req - 1) / s_req;
   } else {
-    if (static_cast<std::size_t>(tiles * slices) > kMaxFixupCounters) {
-      throw_invalid("n * ceil(batch / m_tile) / 128 exceeds the split tile capacity (16384)");
+    long long s_split = 1;
+    while (slices * s_split * 2 <= cu_count && num_groups / (s_split * 2) >= kMinNativeRunGroups) {
+      s_split *= 2;
     }
-    plan.workspace_bytes =
-        kCounterRegionBytes + fk::gemv_streamk_partial_floats(n, batch, plan.m_tile,
-                                                              plan.max_tile_contributors) *
-                                  sizeof(float);
+    per = (num_groups + s_split - 1) / s_split;
   }
+  finish_plan(plan, fk::gemv_tiles(n, batch, plan.m_tile), fk::kSlicesPerTile, num_groups, per, n,
+              batch);
   return plan;
 }
 
@@ -524,20 +583,6 @@ ArcW4A16Plan plan_arc_w4a16(int batch, int n, int k, int group_size, int activat
 
 namespace {
 
-fk::PacketFormat to_packet_format(int packet_format, bool allow_arc) {
-  switch (packet_format) {
-    case kPacketArc:
-      if (allow_arc) return fk::PacketFormat::kArc;
-      break;
-    case kPacketNativeSym: return fk::PacketFormat::kNativeSym;
-    case kPacketNativeAsym: return fk::PacketFormat::kNativeAsym;
-    default: break;
-  }
-  throw_invalid(allow_arc ? "packet_format must be 0 (reference), 1 (native symmetric) or 2 "
-                            "(native asymmetric)"
-                          : "packet_format must be 1 (native symmetric) or 2 (native asymmetric)");
-}
-
 void forward_with_format(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
                          std::uintptr_t output_ptr, std::uintptr_t workspace_ptr,
                          std::size_t workspace_bytes, int batch, int n, int k, int group_size,
@@ -548,8 +593,9 @@ void forward_with_format(std::uintptr_t activations_ptr, std::uintptr_t packets_
   if (split_k_slices < 0) {
     throw_invalid("split_k_slices must be >= 0 (0 = automatic)");
   }
-  const ArcW4A16Plan plan = plan_arc_w4a16_for_cu_count(batch, n, k, group_size, activation_dtype,
-                                                        split_k_slices, device_cu_count());
+  const ArcW4A16Plan plan =
+      plan_w4a16_for_format(batch, n, k, group_size, activation_dtype, split_k_slices,
+                            device_cu_count(), static_cast<int>(format));
   if (plan.workspace_bytes > 0) {
     validate_pointer(workspace_ptr, kCounterRegionAlign, "workspace");
     if (workspace_bytes < plan.workspace_bytes) {

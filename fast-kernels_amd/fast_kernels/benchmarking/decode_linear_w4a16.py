@@ -199,7 +199,10 @@ def run_decode_linear_w4a16_suite(suite: BenchmarkSuite) -> tuple[list[Benchmark
     if not torch.cuda.is_available():
         return _all_skipped(suite, "torch.cuda.is_available() is false on this machine."), notes
     device = torch.device("cuda")
-    notes.append(f"GPU: {torch.cuda.get_device_name(device)}")
+    props = torch.cuda.get_device_properties(device)
+    arch = getattr(props, "gcnArchName", "").split(":")[0]
+    notes.append(f"GPU: {torch.cuda.get_device_name(device)} ({arch}, {props.multi_processor_count} CUs, "
+                 f"{props.total_memory / 2**30:.0f} GiB)")
     cases: list[BenchmarkCase] = []
     for dtype in suite.dtypes:
         for layout in suite.layouts:
@@ -340,7 +343,8 @@ def _run_shape(torch: Any, device: Any, suite: BenchmarkSuite, dtype: str, layou
         impl = kernels[kernel_id].impl
         if impl is not None and impl not in supported:
             out.append(_case("kernel", kernel_id, dtype, layout, name, dims, "skipped",
-                             reason=f"{kernel_id} is not supported on {torch.cuda.get_device_name(device)}"))
+                             reason=f"{kernel_id} is not supported on "
+                                    f"{getattr(torch.cuda.get_device_properties(device), 'gcnArchName', 'this GPU').split(':')[0]}"))
             continue
         if impl == "tc" and act != "f16":
             out.append(_case("kernel", kernel_id, dtype, layout, name, dims, "skipped",

@@ -134,13 +134,13 @@ def traffic(
 
 
 def _shape_row(rows: dict, threads: int, slice_cols: int | None) -> tuple[str, dict] | None:
-    """The kernel row of one bench shape: same grid, and (when given) the slice width, which the
-    GEMV kernel's template arguments carry as ", <cols>, (PacketFormat)"."""
-    hits = [
-        (k, v) for k, v in rows.items()
-        if k.endswith(f" grid={threads}")
-        and (slice_cols is None or f", {slice_cols}, (PacketFormat)" in k)
-    ]
+    """The kernel row of one bench shape: same grid and, when several kernels share the grid, the
+    slice width, which the reference-packet kernel's template arguments carry as
+    ", <cols>, (PacketFormat)" (the native-slab kernel always uses 32-column slices)."""
+    hits = [(k, v) for k, v in rows.items() if k.endswith(f" grid={threads}")]
+    if len(hits) > 1 and slice_cols is not None:
+        hits = [(k, v) for k, v in hits
+                if f", {slice_cols}, (PacketFormat)" in k or ("native" in k and slice_cols == 32)]
     return hits[0] if len(hits) == 1 else None
 
 

@@ -82,9 +82,10 @@ def _rocm_smi() -> dict[str, str] | None:
         if not isinstance(value, dict):
             continue
         if key.startswith("card") and "name" not in info:
-            name = value.get("Card Series") or value.get("Card series") or value.get("Card Model")
+            names = [value.get(k) for k in ("Card Series", "Card series", "Card Model", "Card SKU")]
+            name = next((str(n) for n in names if n and str(n).strip() not in {"N/A", "0x0"}), None)
             if name:
-                info["name"] = str(name)
+                info["name"] = name
             gfx = value.get("GFX Version")
             if gfx:
                 info["gfx_version"] = str(gfx)

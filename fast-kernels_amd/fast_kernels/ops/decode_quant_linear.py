@@ -154,13 +154,16 @@ def arc_w4a16_plan(
     activation_dtype: Any = None,
     split_k_slices: int = 0,
     cu_count: int = 0,
+    packet_format: int = 0,
 ) -> dict[str, int]:
     """Launch plan: m_tile, workgroups, groups_per_workgroup, max_tile_contributors,
-    workspace_bytes and slice_cols (columns of a tile per workgroup)."""
+    workspace_bytes and slice_cols (columns of a tile per workgroup), for reference packets
+    (packet_format 0) or the native formats (1 symmetric, 2 asymmetric)."""
     native = native_module()
     return dict(
         native.arc_w4a16_plan(
-            batch, n, k, group_size, _act_code(activation_dtype), split_k_slices, cu_count
+            batch, n, k, group_size, _act_code(activation_dtype), split_k_slices, cu_count,
+            packet_format,
         )
     )
 

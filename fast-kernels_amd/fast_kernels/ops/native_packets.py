@@ -1,20 +1,25 @@
 """Native gfx950 packet formats of the W4A16 decode linear, and the forward over them.
 
-The reference packet (csrc/kernels/decode_quant_linear/arc_w4a16.cu:92-122) stores per group and
-128-column tile the int4 code words, 128 fp16 alphas and 128 fp16 betas. For int4 quantisation
-beta is always half_rn(-alpha * zp) with an integer zero point zp in 0..15, so the betas carry at
-most four bits of information each. The native formats keep the reference's code words and
-alphas unchanged and drop the fp16 betas:
+The reference packet (csrc/kernels/decode_quant_linear/arc_w4a16.cu:92-122) stores, per
+128-column tile and group, the int4 code words of the 128 columns interleaved word row by word
+row (512 bytes per row), then 128 fp16 alphas and 128 fp16 betas. Two things cost bandwidth on
+MI355X: a workgroup that owns fewer than 128 columns (how the small decode shapes fill 256 CUs)
+reads 128 bytes out of every 512, which HBM serves far below its streaming rate; and for int4
+quantisation beta is always half_rn(-alpha * zp) with an integer zp in 0..15, so its 16 bits
+carry at most 4.
 
-  * "native_sym":  zp = 8 for every group (the symmetric recipe); 64*G + 256 bytes per packet,
-    20% (G=128) or 33% (G=64) fewer bytes than the reference's 64*G + 512;
-  * "native_asym": 128 int4 zero points after the alphas (column c in byte c/2, low nibble for
-    even c); 64*G + 320 bytes per packet.
+The native formats store one slab per (tile, 32-column slice, group), in [tile][slice][group]
+order, so the groups of a slice are one contiguous range:
 
-The kernels rebuild beta = half_rn(-alpha * zp) bit for bit, so a forward over native packets
-returns exactly what the same launch over the reference packets they came from returns. Packets
-convert both ways on the GPU; converting reference packets whose betas are not of that form
-raises ValueError instead of silently changing the weights.
+  * code words: G/8 rows of 32 uint32 (the reference's word packing, 8 codes along K per word);
+  * alpha: 32 fp16;
+  * "native_asym" only: 32 int4 zero points (column c in byte c/2, low nibble for even c).
+
+"native_sym" (zp = 8) slabs are 16*G + 64 bytes, "native_asym" slabs 16*G + 80; a buffer is
+[(N/32) * K/G, slab bytes]. The kernels rebuild beta = half_rn(-alpha * zp) bit for bit, so a
+forward over native slabs returns exactly what the same launch over the reference packets they
+came from returns. Slabs convert both ways on the GPU; converting reference packets whose betas
+are not of that form raises ValueError instead of silently changing the weights.
 """
 
 from __future__ import annotations
@@ -58,14 +63,14 @@ def packet_format_code(packet_format: str | int) -> int:
 
 
 def packet_stride_bytes(group_size: int, packet_format: str | int) -> int:
-    """Bytes per packet: code words (64*G), alphas (256), then betas (256, reference format),
-    nothing (native_sym) or 128 int4 zero points (64, native_asym)."""
+    """Bytes per reference packet (code words 64*G, alphas 256, betas 256) or native slab (code
+    words 16*G, alphas 64, and for native_asym 16 bytes of zero points)."""
     code = packet_format_code(packet_format)
     if code == PACKET_ARC:
         return arc_packet_stride_bytes(group_size)
     if group_size not in {64, 128}:
         raise ValueError("group_size must be 64 or 128")
-    return 64 * group_size + (256 if code == PACKET_NATIVE_SYM else 320)
+    return 16 * group_size + (64 if code == PACKET_NATIVE_SYM else 80)
 
 
 def _native_code(packet_format: str | int) -> int:
@@ -80,7 +85,8 @@ def _packet_shape(n: int, k: int, group_size: int, code: int) -> tuple[int, int]
         raise ValueError("k must be divisible by group_size")
     if n % 128 != 0:
         raise ValueError("n must be divisible by 128")
-    return ((n // 128) * (k // group_size), packet_stride_bytes(group_size, code))
+    rows_per_group = n // 128 if code == PACKET_ARC else n // 32
+    return (rows_per_group * (k // group_size), packet_stride_bytes(group_size, code))
 
 
 def _out_packets(packets: Any, shape: tuple[int, int], like: Any) -> Any:
@@ -228,7 +234,7 @@ def arc_w4a16_forward_native(
         raise ValueError("split_k_slices must be positive")
     requested = 0 if split_k_slices is None else int(split_k_slices)
     act = _act_code(activations.dtype)
-    plan = native.arc_w4a16_plan(batch, n, k, group_size, act, requested, 0)
+    plan = native.arc_w4a16_plan(batch, n, k, group_size, act, requested, 0, code)
     ws_ptr, ws_bytes = 0, int(plan["workspace_bytes"])
     if ws_bytes > 0:
         ws = arc_workspace(activations.device, ws_bytes)

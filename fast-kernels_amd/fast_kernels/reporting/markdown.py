@@ -16,7 +16,8 @@ def _fmt(value: float | None, digits: int = 1) -> str:
 def render_summary_markdown(bundle: ResultBundle) -> str:
     meta = bundle.metadata
     status_counts = Counter(case.status for case in bundle.cases)
-    gpu = (meta.rocm_smi or {}).get("name") or (meta.nvidia_smi or {}).get("name") or "none"
+    smi = meta.rocm_smi or {}
+    gpu = smi.get("name") or smi.get("gfx_version") or (meta.nvidia_smi or {}).get("name") or "none"
     lines = [
         f"# {meta.suite_id}",
         "",

@@ -124,18 +124,24 @@ int fk_arc_w4a16_forward_ex(const void* activations, const void* packets, void* 
                             int group_size, int packet_stride_bytes, int activation_dtype,
                             int split_k_slices, void* stream);
 
-/* Native packet formats for gfx950. They keep the reference packet's code words and alpha and
- * drop its fp16 beta, which for int4 quantisation is always half_rn(-alpha * zp):
- *   FK_PACKET_NATIVE_SYM   zp = 8 for every group; 64*G + 256 bytes per packet
- *   FK_PACKET_NATIVE_ASYM  128 int4 zero points after alpha (column c in byte c/2, bits 0-3 for
- *                          even c); 64*G + 320 bytes per packet
- * (FK_PACKET_ARC is the reference layout above, 64*G + 512 bytes.) Results of the forward over
- * native packets equal those over the reference packets they were converted from. */
+/* Native packet formats for gfx950. The reference packet interleaves the 128 columns of a tile
+ * word row by word row, so a workgroup that owns fewer than 128 columns reads 128 bytes out of
+ * every 512; and it stores an fp16 beta that int4 quantisation always fixes as
+ * half_rn(-alpha * zp). The native formats store one slab per (128-column tile, 32-column slice,
+ * group), in [tile][slice][group] order, so the groups of a slice are one contiguous byte range:
+ *   code words  G/8 rows of 32 uint32, word w of slice column c at byte (w*32 + c)*4
+ *   alpha       32 fp16
+ *   zero points (FK_PACKET_NATIVE_ASYM only) 32 int4, column c in byte c/2, even c low nibble
+ * FK_PACKET_NATIVE_SYM slabs are 16*G + 64 bytes (zp = 8 for every group), FK_PACKET_NATIVE_ASYM
+ * slabs 16*G + 80 bytes; a buffer holds (N/32) * (K/G) slabs. (FK_PACKET_ARC is the reference
+ * layout above, 64*G + 512 bytes per packet.) The forward over native slabs returns, bit for
+ * bit, what it returns over the reference packets they were converted from. */
 #define FK_PACKET_ARC 0
 #define FK_PACKET_NATIVE_SYM 1
 #define FK_PACKET_NATIVE_ASYM 2
 
-/* Bytes per packet of a format (group_size 64 or 128); -1 on invalid arguments. */
+/* Bytes per packet (FK_PACKET_ARC) or slab (native formats) for group_size 64 or 128; -1 on
+ * invalid arguments. */
 int fk_packet_stride_bytes(int group_size, int packet_format);
 
 /* Native packets from q_u8 [N, K/2], alpha fp16 [N, K/G] and, for FK_PACKET_NATIVE_ASYM,
@@ -154,8 +160,14 @@ int fk_convert_arc_to_native_packets(const void* arc_packets, void* native_packe
 int fk_convert_native_to_arc_packets(const void* native_packets, void* arc_packets, int n, int k,
                                      int group_size, int packet_format, void* stream);
 
-/* fk_arc_w4a16_forward_ex over packets of any FK_PACKET_* format: same plan, workspace contract,
- * graph-capture behaviour and results. */
+/* Launch plan of fk_arc_w4a16_forward_native for a packet format (arguments as
+ * fk_arc_w4a16_plan_for); slice_cols is 32 for the native formats below 16 activation rows. */
+int fk_w4a16_plan_for_format(int batch, int n, int k, int group_size, int activation_dtype,
+                             int split_k_slices, int cu_count, int packet_format,
+                             fk_arc_w4a16_plan* plan);
+
+/* fk_arc_w4a16_forward_ex over packets of any FK_PACKET_* format: same workspace contract
+ * (workspace_bytes from fk_w4a16_plan_for_format), graph-capture behaviour and results. */
 int fk_arc_w4a16_forward_native(const void* activations, const void* packets, void* output,
                                 void* workspace, size_t workspace_bytes, int batch, int n, int k,
                                 int group_size, int packet_format, int activation_dtype,

@@ -176,11 +176,11 @@ def test_pybind_module_mirrors_reference_names() -> None:
 
 @pytest.mark.parametrize("group_size", [64, 128])
 def test_packet_format_strides(lib: ctypes.CDLL, group_size: int) -> None:
-    """Reference packets: codes (64*G) + alpha + beta (256 + 256); native symmetric drops beta,
-    native asymmetric replaces it with 128 int4 zero points (64 bytes)."""
+    """Reference packets: codes (64*G) + alpha + beta (256 + 256) per 128 columns; native slabs:
+    codes (16*G) + alpha (64) per 32 columns, plus 32 int4 zero points (16) when asymmetric."""
     from fast_kernels.ops import packet_stride_bytes
 
-    want = {0: 64 * group_size + 512, 1: 64 * group_size + 256, 2: 64 * group_size + 320}
+    want = {0: 64 * group_size + 512, 1: 16 * group_size + 64, 2: 16 * group_size + 80}
     for fmt, stride in want.items():
         assert lib.fk_packet_stride_bytes(group_size, fmt) == stride
         assert packet_stride_bytes(group_size, fmt) == stride
@@ -205,3 +205,30 @@ def test_native_format_validation_without_gpu(lib: ctypes.CDLL) -> None:
     assert rc == 1 and b"packet_format" in lib.fk_last_error()
     rc = lib.fk_arc_w4a16_forward_native(None, None, None, None, 0, 1, 128, 256, 128, 1, 0, 0, None)
     assert rc == 1 and b"must not be null" in lib.fk_last_error()
+
+
+@pytest.mark.parametrize(
+    "shape,want",
+    [
+        # (batch, n, k, G) -> (slice_cols, groups per workgroup, workgroups) on 256 CUs
+        ((1, 8192, 8192, 128), (32, 64, 256)),      # 256 slices, each over all of K
+        ((1, 10240, 8192, 128), (32, 64, 320)),
+        ((1, 57344, 8192, 128), (32, 64, 1792)),    # more slices than resident workgroups
+        ((1, 8192, 28672, 128), (32, 224, 256)),
+        ((1, 4096, 4096, 128), (32, 32, 128)),      # half the CUs idle, but K is short
+        ((1, 4096, 14336, 128), (32, 56, 256)),     # 128 slices, 112 groups: two runs of 56
+        ((4, 14336, 4096, 64), (32, 64, 448)),      # four rows share a slice's runs
+        ((16, 14336, 4096, 64), (128, 16, 448)),    # matrix cores: the reference-format plan
+    ],
+)
+def test_native_plan_policy_without_gpu(lib: ctypes.CDLL, shape, want) -> None:
+    batch, n, k, g = shape
+    p = Plan()
+    assert lib.fk_w4a16_plan_for_format(batch, n, k, g, 0, 0, 256, 1, ctypes.byref(p)) == 0
+    assert (p.slice_cols, p.groups_per_workgroup, p.workgroups) == want
+    arc = Plan()
+    assert lib.fk_w4a16_plan_for_format(batch, n, k, g, 0, 0, 256, 0, ctypes.byref(arc)) == 0
+    rc, ref = _plan(lib, batch, n, k, g)
+    assert rc == 0 and (arc.slice_cols, arc.workgroups) == (ref.slice_cols, ref.workgroups)
+    # a fix-up needs a workspace exactly when runs do not cover whole slices
+    assert (p.workspace_bytes > 0) == (p.groups_per_workgroup % (k // g) != 0)

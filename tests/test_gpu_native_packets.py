@@ -1,14 +1,14 @@
 """GPU tests of the native packet formats (symmetric: no beta; asymmetric: int4 zero points).
 
 Pins:
-  * layout: a native packet is the oracle's reference packet (oracle.pack_packets) with its 256
-    beta bytes dropped (symmetric) or replaced by the 128 zero points, two per byte, low nibble
-    for the even column (asymmetric);
+  * layout: native slabs are the oracle's reference packets (oracle.pack_packets) cut into
+    32-column slices, ordered [tile][slice][group], code words in quarter order, alphas in column
+    pairs, betas dropped (symmetric) or replaced by the slice's 32 zero points (asymmetric);
   * conversions: reference -> native -> reference reproduces oracle.pack_packets byte for byte;
     reference packets whose betas are not half_rn(-alpha * zp) are rejected;
-  * forward: over native packets the output equals, bit for bit, the same launch over the
-    reference packets, and is within the GEMV bar of the oracle (rel 1e-2,
-    abs 1e-2 * sqrt(K) * max|alpha|).
+  * forward: over native slabs the output is within the GEMV bar of the oracle (rel 1e-2,
+    abs 1e-2 * sqrt(K) * max|alpha|), like the forward over the reference packets the slabs came
+    from (the two launches differ in slice width and K split, so in fp32 summation order only).
 """
 
 from __future__ import annotations
@@ -46,16 +46,43 @@ def _fmt(asym: bool) -> str:
     return "native_asym" if asym else "native_sym"
 
 
+def _native_word_offset(g: int, i: int, t: int, n: int, j: int) -> int:
+    """Byte offset in a slab of word j of the unit (column 16 i + n, quarter t)."""
+    return i * 1024 + (16 * t + n) * 16 + 4 * j if g == 128 else (16 * t + n) * 16 + i * 8 + 4 * j
+
+
 def _expected_native(case, asym: bool) -> np.ndarray:
-    ref = oracle.pack_packets(case.q_u8, case.alpha, case.beta, case.group_size)
-    head = 64 * case.group_size + 256  # code words and alpha
-    if not asym:
-        return np.ascontiguousarray(ref[:, :head])
-    ng = case.k // case.group_size
-    # zero points in packet order: packet (tile t, group g), column c -> zp[t*128 + c, g]
-    zp = case.zero_points.reshape(case.n // 128, 128, ng).transpose(0, 2, 1).reshape(-1, 128)
-    nibbles = (zp[:, 0::2] | (zp[:, 1::2] << 4)).astype(np.uint8)
-    return np.ascontiguousarray(np.concatenate([ref[:, :head], nibbles], axis=1))
+    """Native slabs rearranged from the oracle's reference packets. Slab (tile, slice, group):
+    the slice's code words in quarter order (column 16 i + n has G/8 words in four quarters of
+    U = G/32; lane 16 t + n of a wave owns quarter t of columns n and n + 16), then the alphas as
+    pairs (alpha[n], alpha[n + 16]), then (asymmetric) the zero points, byte n = zp[n] | zp[n+16] << 4."""
+    g = case.group_size
+    ng = case.k // g
+    tiles = case.n // 128
+    u = g // 32
+    ref = oracle.pack_packets(case.q_u8, case.alpha, case.beta, g).reshape(tiles, ng, -1)
+    words = ref[:, :, : 64 * g].copy().view(np.uint32).reshape(tiles, ng, g // 8, 128)
+    alpha = ref[:, :, 64 * g : 64 * g + 256].copy().view(np.uint16).reshape(tiles, ng, 128)
+    stride = 16 * g + 64 + (16 if asym else 0)
+    out = np.zeros((tiles, 4, ng, stride), dtype=np.uint8)
+    codes = np.zeros((tiles, 4, ng, 4 * g), dtype=np.uint32)  # 16 g bytes per slab
+    for i in range(2):
+        for t in range(4):
+            for n in range(16):
+                for j in range(u):
+                    dst = _native_word_offset(g, i, t, n, j) // 4
+                    col = np.arange(4) * 32 + 16 * i + n  # this column in each of the 4 slices
+                    codes[:, :, :, dst] = words[:, :, t * u + j, col].transpose(0, 2, 1)
+    out[..., : 16 * g] = codes.view(np.uint8).reshape(tiles, 4, ng, 16 * g)
+    pairs = np.zeros((tiles, 4, ng, 32), dtype=np.uint16)
+    for i in range(2):
+        for n in range(16):
+            pairs[..., 2 * n + i] = alpha[:, :, np.arange(4) * 32 + 16 * i + n].transpose(0, 2, 1)
+    out[..., 16 * g : 16 * g + 64] = pairs.view(np.uint8).reshape(tiles, 4, ng, 64)
+    if asym:
+        zp = case.zero_points.reshape(tiles, 4, 32, ng).transpose(0, 1, 3, 2)  # [t, s, g, col]
+        out[..., 16 * g + 64 :] = (zp[..., :16] | (zp[..., 16:] << 4)).astype(np.uint8)
+    return out.reshape(tiles * 4 * ng, stride)
 
 
 @pytest.mark.parametrize("asym", [False, True])
@@ -130,45 +157,67 @@ def test_forward_native_matches_reference_packets(asym, group_size, batch, act) 
     case = make_case(batch, 512, 16 * group_size, group_size, act=act, asymmetric=asym,
                      seed=1000 + batch + group_size)
     y_nat, y_arc = _forward_pair(case, asym)
-    np.testing.assert_array_equal(y_nat, y_arc)
     ref, _ = oracle.gemv(case.x, case.q_u8, case.alpha, case.beta, group_size, act)
     _assert_gemv_close(y_nat, ref, case, f"{_fmt(asym)} {act} G={group_size} M={batch}")
+    _assert_gemv_close(y_arc, ref, case, f"arc {act} G={group_size} M={batch}")
 
 
 @pytest.mark.parametrize(
     "shape,act,asym",
     [
-        ((1, 1024, 2048, 128), "f16", False),    # 32-column slices
-        ((1, 10240, 4096, 128), "f16", True),    # 64-column slices
-        ((1, 4096, 14336, 128), "bf16", False),  # narrow slices + K split (fix-up)
-        ((1, 8192, 8192, 128), "f16", False),    # Llama-70B o, whole tiles + K split
-        ((2, 4096, 4096, 64), "f16", True),      # two rows, K runs per tile
-        ((16, 4096, 4096, 64), "bf16", True),    # matrix-core tile
+        ((1, 1024, 2048, 128), "f16", False),    # 32 slices, one per workgroup
+        ((1, 10240, 4096, 128), "f16", True),    # 320 slices, two workgroups per CU
+        ((1, 4096, 14336, 128), "bf16", False),  # 128 slices, K split in two (fix-up)
+        ((1, 57344, 8192, 128), "bf16", False),  # Llama-70B gate_up, four slices per workgroup
+        ((2, 4096, 4096, 64), "f16", True),      # two rows
+        ((8, 4096, 4096, 64), "bf16", True),     # eight rows (half-depth pipeline)
+        ((16, 4096, 4096, 64), "bf16", True),    # matrix-core tile over four slabs per group
     ],
 )
 def test_forward_native_plans_match_oracle(shape, act, asym) -> None:
     batch, n, k, g = shape
     plan = arc_w4a16_plan(batch=batch, n=n, k=k, group_size=g,
-                          activation_dtype=torch.float16 if act == "f16" else torch.bfloat16)
+                          activation_dtype=torch.float16 if act == "f16" else torch.bfloat16,
+                          packet_format=2 if asym else 1)
+    assert plan["slice_cols"] == (128 if batch >= 8 else 32)
     case = make_case(batch, n, k, g, act=act, asymmetric=asym)
-    y_nat, y_arc = _forward_pair(case, asym)
-    np.testing.assert_array_equal(y_nat, y_arc)
+    y_nat, _ = _forward_pair(case, asym)
+    if n > 8192:  # the oracle checks a spread subset of rows of the large shape
+        rows = np.unique(np.linspace(0, n - 1, 512).astype(int))
+        ref, _ = oracle.gemv(case.x, np.ascontiguousarray(case.q_u8[rows]),
+                             np.ascontiguousarray(case.alpha[rows]),
+                             np.ascontiguousarray(case.beta[rows]), g, act)
+        _assert_gemv_close(y_nat[:, rows], ref, case, f"{shape} {act} plan={plan}")
+        return
     ref, _ = oracle.gemv(case.x, case.q_u8, case.alpha, case.beta, g, act)
     _assert_gemv_close(y_nat, ref, case, f"{shape} {act} plan={plan}")
 
 
-@pytest.mark.parametrize("split", [3, 7])
+@pytest.mark.parametrize("split", [1, 3, 7])
 def test_forward_native_forced_split(split: int) -> None:
+    """Forced K runs of ceil(64/split) groups over 32-column slices; 3 and 7 give runs that
+    straddle slices, so a slice is finished from the partials of up to 3 workgroups."""
     case = make_case(1, 1024, 64 * 128, 128, asymmetric=True, seed=99)
-    y_nat, y_arc = _forward_pair(case, True, split_k_slices=1)
-    np.testing.assert_array_equal(y_nat, y_arc)
     x, q, a, b = _upload(case)
     arc = pack_arc_w4a16_packets(q, a, b, group_size=128)
     native = convert_arc_to_native_packets(arc, n=1024, k=64 * 128, group_size=128,
                                            packet_format="native_asym")
-    # the native forward with a Stream-K run length the automatic plan would not pick
+    plan = arc_w4a16_plan(batch=1, n=1024, k=64 * 128, group_size=128, split_k_slices=split,
+                          packet_format=2)
+    assert plan["groups_per_workgroup"] == -(-64 // split) and plan["slice_cols"] == 32
     y = arc_w4a16_forward_native(x, native, n=1024, k=64 * 128, group_size=128,
                                  packet_format="native_asym", split_k_slices=split)
     torch.cuda.synchronize()
     ref, _ = oracle.gemv(case.x, case.q_u8, case.alpha, case.beta, 128)
     _assert_gemv_close(_bits(y), ref, case, f"native split={split}")
+
+
+def test_forward_native_deterministic() -> None:
+    case = make_case(1, 4096, 14336, 128, seed=5)  # K split in two: the fix-up path
+    x, q, a, b = _upload(case)
+    native = convert_arc_to_native_packets(pack_arc_w4a16_packets(q, a, b, group_size=128),
+                                           n=4096, k=14336, group_size=128)
+    ys = [_bits(arc_w4a16_forward_native(x, native, n=4096, k=14336, group_size=128))
+          for _ in range(3)]
+    for y in ys[1:]:
+        np.testing.assert_array_equal(y, ys[0])
