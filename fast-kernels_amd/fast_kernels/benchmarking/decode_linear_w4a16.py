@@ -38,6 +38,7 @@ PEAK_HBM_GBS = 8000.0
 SubjectKind = Literal["kernel", "baseline"]
 VENDOR_BASELINES = ("vendor/cublaslt_fp16_after_dequant", "vendor/hipblaslt_fp16_after_dequant")
 REFERENCE_BASELINE = "torch/reference_w4a16_linear"
+NATIVE_IMPL = "native"  # kernel impl: the forward over native slabs
 _DTYPES = {"fp16": "f16", "bf16": "bf16"}
 
 
@@ -215,8 +216,11 @@ def run_decode_linear_w4a16_suite(suite: BenchmarkSuite) -> tuple[list[Benchmark
 def _run_shape(torch: Any, device: Any, suite: BenchmarkSuite, dtype: str, layout: str, shape: Any,
                recipe: str, asymmetric: bool, launches: int) -> list[BenchmarkCase]:
     from fast_kernels.ops import (
+        PACKET_FORMATS,
         arc_w4a16_forward,
+        arc_w4a16_forward_native,
         arc_w4a16_plan,
+        convert_arc_to_native_packets,
         arc_w4a16_supported_impls,
         cublaslt_fp16_after_dequant,
         dequant_w4a16_to_fp16,
@@ -252,12 +256,17 @@ def _run_shape(torch: Any, device: Any, suite: BenchmarkSuite, dtype: str, layou
     batch = shape.batch
     act = _DTYPES[dtype]
     atol, rtol = suite.tolerances.atol, suite.tolerances.rtol
-    supported = set(arc_w4a16_supported_impls(device))
+    supported = set(arc_w4a16_supported_impls(device)) | {NATIVE_IMPL}
+    native_format = "native_asym" if asymmetric else "native_sym"
     out: list[BenchmarkCase] = []
     try:
         case = make_case(batch, n, k, group_size, act=act, asymmetric=asymmetric, recipe=recipe)
         x, q, a, b = _upload(torch, case, device)
         packets = pack_arc_w4a16_packets(q, a, b, group_size=group_size)
+        slabs = None
+        if any(kernels[kid].impl == NATIVE_IMPL for kid in suite.kernels.ids):
+            slabs = convert_arc_to_native_packets(packets, n=n, k=k, group_size=group_size,
+                                                  packet_format=native_format)
         explicit = _explicit_reference(torch, x, q, a, b, group_size)
         ref_weight = torch.empty((n, k), device=device, dtype=torch.float16)
         ref_out = torch.empty((batch, n), device=device, dtype=x.dtype)
@@ -278,7 +287,12 @@ def _run_shape(torch: Any, device: Any, suite: BenchmarkSuite, dtype: str, layou
             impl = kernels[kernel_id].impl
             if impl is not None and (impl not in supported or (impl == "tc" and act != "f16")):
                 continue
-            arc_w4a16_forward(x, packets, n=n, k=k, group_size=group_size, output=kernel_out, impl=impl)
+            if impl == NATIVE_IMPL:
+                arc_w4a16_forward_native(x, slabs, n=n, k=k, group_size=group_size,
+                                         packet_format=native_format, output=kernel_out)
+            else:
+                arc_w4a16_forward(x, packets, n=n, k=k, group_size=group_size, output=kernel_out,
+                                  impl=impl)
             _check_close(kernel_out, ref_out, atol, rtol, f"{kernel_id} output")
             checked[kernel_id] = _max_err(kernel_out, explicit)
         vendor_out = torch.empty((batch, n), device=device, dtype=torch.float16)
@@ -297,6 +311,7 @@ def _run_shape(torch: Any, device: Any, suite: BenchmarkSuite, dtype: str, layou
     packet_bytes = packets.numel()
     rotations = max(2, math.ceil(CACHE_BUST_BYTES / max(packet_bytes, 1)))
     packet_rot = [packets] + [packets.clone() for _ in range(rotations - 1)]
+    slab_rot = [] if slabs is None else [slabs] + [slabs.clone() for _ in range(rotations - 1)]
     qab_rot = [(q, a, b)] + [(q.clone(), a.clone(), b.clone()) for _ in range(rotations - 1)]
     alg_bytes = algorithmic_bytes(batch, n, k, group_size, asymmetric=asymmetric)
     latencies: dict[str, float] = {}
@@ -351,16 +366,24 @@ def _run_shape(torch: Any, device: Any, suite: BenchmarkSuite, dtype: str, layou
                              reason="the tc (hipBLASLt) path takes fp16 activations only"))
             continue
 
-        def run_kernel(p: Any = packets, impl: str | None = impl) -> Any:
-            return arc_w4a16_forward(x, p, n=n, k=k, group_size=group_size, output=kernel_out,
-                                     impl=impl)
+        if impl == NATIVE_IMPL:
+            def run_kernel(p: Any = slabs, impl: str | None = impl) -> Any:
+                return arc_w4a16_forward_native(x, p, n=n, k=k, group_size=group_size,
+                                                packet_format=native_format, output=kernel_out)
+            rot = slab_rot
+        else:
+            def run_kernel(p: Any = packets, impl: str | None = impl) -> Any:
+                return arc_w4a16_forward(x, p, n=n, k=k, group_size=group_size, output=kernel_out,
+                                         impl=impl)
+            rot = packet_rot
 
         extra = {"max_abs_err": checked.get(kernel_id, float("nan"))}
-        if impl in (None, "scalar"):
+        if impl in (None, "scalar", NATIVE_IMPL):
             plan = arc_w4a16_plan(batch=batch, n=n, k=k, group_size=group_size,
-                                  activation_dtype=x.dtype)
+                                  activation_dtype=x.dtype,
+                                  packet_format=PACKET_FORMATS[native_format] if impl == NATIVE_IMPL else 0)
             extra.update({f"plan_{key}": float(val) for key, val in plan.items()})
-        out.append(timed("kernel", kernel_id, run_kernel, lambda r, f=run_kernel: f(packet_rot[r]), extra))
+        out.append(timed("kernel", kernel_id, run_kernel, lambda r, f=run_kernel, rot=rot: f(rot[r]), extra))
     if vendor_id is not None and vendor_id in latencies:
         for c in out:
             if c.status == "ok" and c.subject_id != vendor_id and c.device_latency_us_median:

@@ -6,7 +6,9 @@ GEMVs of one decode step (layers x projections) are captured in one HIP graph an
 step's weights (3.6 GB for the 32-layer 8B stack) exceed every cache, so each replay streams them
 from HBM. Reported per suite shape: device microseconds per GEMV (a graph of that projection
 over all layers) and, as the extra shape "decode_step", microseconds per whole step and aggregate
-effective HBM GB/s. The torch reference baseline (dequantize + matmul per GEMV) is timed eagerly.
+effective HBM GB/s. When the suite lists the native-slab kernel id, the same stack is converted to
+native symmetric slabs and timed the same way. The torch reference baseline (dequantize + matmul
+per GEMV) is timed eagerly.
 
 Correctness: after the timed replays, the outputs of the first and the last layer are compared
 with the explicit fp32 formula (alpha*q + beta weights, fp32 matmul) within the suite tolerances.
@@ -78,10 +80,13 @@ def run_decode_step_w4a16_suite(suite: BenchmarkSuite) -> tuple[list[BenchmarkCa
 def _run_stack(torch: Any, suite: BenchmarkSuite, dtype: str, layout: str, layers: int) -> list[BenchmarkCase]:
     from fast_kernels.ops import (
         arc_w4a16_forward,
+        arc_w4a16_forward_native,
+        convert_arc_to_native_packets,
         dequant_w4a16_to_fp16,
         group_size_for_layout,
         pack_arc_w4a16_packets,
     )
+    from fast_kernels.registry import kernel_registry
 
     act_dtype = {"fp16": torch.float16, "bf16": torch.bfloat16}.get(dtype)
     if act_dtype is None:
@@ -92,6 +97,9 @@ def _run_stack(torch: Any, suite: BenchmarkSuite, dtype: str, layout: str, layer
     atol, rtol = suite.tolerances.atol, suite.tolerances.rtol
     shapes = [(s.name, s.require_dimension("n"), s.require_dimension("k"), s.dimensions())
               for s in suite.shapes]
+    registry = kernel_registry()
+    native_id = next((kid for kid in suite.kernels.ids if registry[kid].impl == "native"), None)
+    slabs: dict[tuple[int, str], Any] = {}
     try:
         weights: dict[tuple[int, str], tuple[Any, Any, Any, Any]] = {}
         keep_raw = {0, layers - 1}
@@ -105,6 +113,9 @@ def _run_stack(torch: Any, suite: BenchmarkSuite, dtype: str, layout: str, layer
                 beta = (alpha.float() * -8.0).half()
                 packets = pack_arc_w4a16_packets(q, alpha, beta, group_size=group_size)
                 weights[(layer, name)] = (packets, q, alpha, beta) if layer in keep_raw else (packets, None, None, None)
+                if native_id is not None:
+                    slabs[(layer, name)] = convert_arc_to_native_packets(
+                        packets, n=n, k=k, group_size=group_size, packet_format="native_sym")
         gen = torch.Generator(device=device)
         gen.manual_seed(12345)
         xs = {k: torch.randn((1, k), device=device, generator=gen).to(act_dtype)
@@ -113,20 +124,26 @@ def _run_stack(torch: Any, suite: BenchmarkSuite, dtype: str, layout: str, layer
                 for layer in range(layers) for name, n, _, _ in shapes}
         stream = torch.cuda.Stream()
 
-        def launch(selection: list[str]) -> None:
+        def launch(selection: list[str], native: bool = False) -> None:
             for layer in range(layers):
                 for name, n, k, _ in shapes:
-                    if name in selection:
+                    if name not in selection:
+                        continue
+                    if native:
+                        arc_w4a16_forward_native(xs[k], slabs[(layer, name)], n=n, k=k,
+                                                 group_size=group_size, packet_format="native_sym",
+                                                 output=outs[(layer, name)])
+                    else:
                         arc_w4a16_forward(xs[k], weights[(layer, name)][0], n=n, k=k,
                                           group_size=group_size, output=outs[(layer, name)])
 
-        def graph_for(selection: list[str]) -> Any:
+        def graph_for(selection: list[str], native: bool = False) -> Any:
             with torch.cuda.stream(stream):
-                launch(selection)  # warm-up: plans and the library workspace exist before capture
+                launch(selection, native)  # warm-up: plans and the workspace exist before capture
             torch.cuda.synchronize()
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, stream=stream):
-                launch(selection)
+                launch(selection, native)
             return graph
 
         def time_graph(graph: Any) -> tuple[float, float]:
@@ -159,39 +176,63 @@ def _run_stack(torch: Any, suite: BenchmarkSuite, dtype: str, layout: str, layer
         per_shape = {}
         for name, _, _, _ in shapes:
             per_shape[name] = time_graph(graph_for([name]))
+        native_results: dict[str, tuple[float, float]] = {}
+        native_errors: dict[str, float] = {}
+        if native_id is not None:
+            all_names = [name for name, _, _, _ in shapes]
+            native_results[STEP_SHAPE] = time_graph(graph_for(all_names, native=True))
+            for layer in sorted(keep_raw):
+                for name, n, k, _ in shapes:
+                    _, q, alpha, beta = weights[(layer, name)]
+                    ref = _explicit_reference(torch, xs[k], q, alpha, beta, group_size)
+                    _check_close(outs[(layer, name)], ref, atol, rtol, f"native layer {layer} {name}")
+                    native_errors[name] = max(native_errors.get(name, 0.0),
+                                              _max_err(outs[(layer, name)], ref))
+            for name in all_names:
+                native_results[name] = time_graph(graph_for([name], native=True))
     except Exception as exc:  # noqa: BLE001 - reported as failed cases
         return [c.model_copy(update={"status": "failed", "reason": str(exc)})
                 for c in _all(suite, "failed", "") if c.dtype == dtype and c.layout == layout]
 
     cases: list[BenchmarkCase] = []
-    kernel_id = suite.kernels.ids[0]
-    step_bytes = 0
-    for name, n, k, dims in shapes:
-        med, p95 = per_shape[name]
-        alg = algorithmic_bytes(1, n, k, group_size)
-        step_bytes += alg * layers
-        us = med / layers
-        cases.append(_case("kernel", kernel_id, dtype, layout, name, dims, "ok",
-                           latency_us_median=us, latency_us_p95=p95 / layers,
-                           device_latency_us_median=us, device_latency_us_p95=p95 / layers,
-                           throughput=1e6 / us, decode_tokens_per_second=1e6 / us,
-                           metrics={"hbm_gbs": alg / us / 1e3,
-                                    "pct_hbm_peak": 100 * alg / us / 1e3 / PEAK_HBM_GBS,
-                                    "algorithmic_bytes": float(alg), "layers": float(layers),
-                                    "max_abs_err": errors.get(name, math.nan)}))
-    cases.append(_case("kernel", kernel_id, dtype, layout, STEP_SHAPE,
-                       {"batch": 1, "layers": layers, "gemvs": layers * len(shapes)}, "ok",
-                       latency_us_median=step_med, latency_us_p95=step_p95,
-                       device_latency_us_median=step_med, device_latency_us_p95=step_p95,
-                       throughput=1e6 / step_med, decode_tokens_per_second=1e6 / step_med,
-                       metrics={"hbm_gbs": step_bytes / step_med / 1e3,
-                                "pct_hbm_peak": 100 * step_bytes / step_med / 1e3 / PEAK_HBM_GBS,
-                                "algorithmic_bytes": float(step_bytes),
-                                "us_per_step": step_med}))
-    for kid in suite.kernels.ids[1:]:
-        cases += [_case("kernel", kid, dtype, layout, name, dims, "not_implemented",
-                        reason="the decode-step stream times the automatic dispatch only")
-                  for name, _, _, dims in shapes]
+    step_bytes = sum(algorithmic_bytes(1, n, k, group_size) * layers for _, n, k, _ in shapes)
+
+    def emit(kernel_id: str, results: dict[str, tuple[float, float]], errs: dict[str, float]) -> None:
+        for name, n, k, dims in shapes:
+            med, p95 = results[name]
+            alg = algorithmic_bytes(1, n, k, group_size)
+            us = med / layers
+            cases.append(_case("kernel", kernel_id, dtype, layout, name, dims, "ok",
+                               latency_us_median=us, latency_us_p95=p95 / layers,
+                               device_latency_us_median=us, device_latency_us_p95=p95 / layers,
+                               throughput=1e6 / us, decode_tokens_per_second=1e6 / us,
+                               metrics={"hbm_gbs": alg / us / 1e3,
+                                        "pct_hbm_peak": 100 * alg / us / 1e3 / PEAK_HBM_GBS,
+                                        "algorithmic_bytes": float(alg), "layers": float(layers),
+                                        "max_abs_err": errs.get(name, math.nan)}))
+        s_med, s_p95 = results[STEP_SHAPE]
+        cases.append(_case("kernel", kernel_id, dtype, layout, STEP_SHAPE,
+                           {"batch": 1, "layers": layers, "gemvs": layers * len(shapes)}, "ok",
+                           latency_us_median=s_med, latency_us_p95=s_p95,
+                           device_latency_us_median=s_med, device_latency_us_p95=s_p95,
+                           throughput=1e6 / s_med, decode_tokens_per_second=1e6 / s_med,
+                           metrics={"hbm_gbs": step_bytes / s_med / 1e3,
+                                    "pct_hbm_peak": 100 * step_bytes / s_med / 1e3 / PEAK_HBM_GBS,
+                                    "algorithmic_bytes": float(step_bytes),
+                                    "us_per_step": s_med}))
+
+    arc_id = next((kid for kid in suite.kernels.ids if kid != native_id), None)
+    if arc_id is not None:
+        emit(arc_id, dict(per_shape, **{STEP_SHAPE: (step_med, step_p95)}), errors)
+    if native_id is not None:
+        emit(native_id, native_results, native_errors)
+    timed_ids = {arc_id, native_id}
+    for kid in suite.kernels.ids:
+        if kid not in timed_ids:
+            cases += [_case("kernel", kid, dtype, layout, name, dims, "not_implemented",
+                            reason="the decode-step stream times the automatic dispatch and the "
+                                   "native slabs only")
+                      for name, _, _, dims in shapes]
 
     # torch reference: dequantize + matmul for every GEMV of one step, eager, a few steps.
     for baseline_id in suite.baselines.ids:

@@ -16,7 +16,8 @@ class KernelSpec:
     family: str
     description: str
     maturity: str
-    impl: str | None = None  # arc_w4a16_forward impl name; None = automatic dispatch
+    impl: str | None = None  # arc_w4a16_forward impl name; None = automatic dispatch;
+    # "native" = arc_w4a16_forward_native over slabs converted from the packets
 
 
 def kernel_registry() -> dict[str, KernelSpec]:
@@ -35,6 +36,14 @@ def kernel_registry() -> dict[str, KernelSpec]:
             "accumulation, in-kernel activation sums and split-K fix-up (gfx950 HIP).",
             "experimental",
             "scalar",
+        ),
+        KernelSpec(
+            "decode/w4a16_linear_native",
+            "decode_quant_linear",
+            "The same GEMV over native gfx950 slabs (slice-major, no fp16 offsets), converted once "
+            "from the ARC packets; symmetric or asymmetric slabs follow the case's zero points.",
+            "experimental",
+            "native",
         ),
         KernelSpec(
             "decode/w4a16_linear_tc",
