@@ -240,9 +240,15 @@ __device__ __forceinline__ void mfma_compute_group(const MfmaSmem<G>& sm, const 
       }
       const uint32_t pair = (sl % 2 == 0) ? ld.alpha[sl / 2].x : ld.alpha[sl / 2].y;
       const float alpha = half_bits_to_float(static_cast<uint16_t>(pair >> (16 * i)));
-      const uint32_t zp_byte = (ld.beta[sl / 2].x >> (8 * (sl % 2))) & 0xFFu;
-      const float beta = group_offset<F>(alpha, 0, (zp_byte >> (4 * i)) & 0xFu);
-      const float c = fmaf(-1024.0f, alpha, beta);  // beta - 1024 alpha
+      float c = -1032.0f * alpha;  // kNativeSym: beta - 1024 alpha with beta = -8 alpha exactly
+      if constexpr (F == PacketFormat::kNativeAsym) {
+        // beta = half_rn(-alpha * zp): fp16 0x6400 | z is 1024 + z, 1024 - that is -z exactly.
+        const uint32_t zp_byte = (ld.beta[sl / 2].x >> (8 * (sl % 2))) & 0xFFu;
+        const uint32_t z = (zp_byte >> (4 * i)) & 0xFu;
+        const _Float16 neg_z = static_cast<_Float16>(1024.0f) - __builtin_bit_cast(_Float16, static_cast<uint16_t>(z | 0x6400u));
+        const _Float16 beta = __builtin_bit_cast(_Float16, static_cast<uint16_t>(pair >> (16 * i))) * neg_z;
+        c = fmaf(-1024.0f, alpha, static_cast<float>(beta));
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         float t = fmaf(alpha, d[r], c * s[r]);

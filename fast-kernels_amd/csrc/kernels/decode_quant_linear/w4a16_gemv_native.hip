@@ -8,11 +8,12 @@
 //  * Lane l = 16t + n owns quarter t (U = G/32 consecutive code words, 8U values of k) of columns
 //    n and n + 16. Per group it therefore applies scales to two columns, not four, and reads U
 //    16-byte activation vectors per row (broadcast: the 16 lanes of a quarter read the same one).
-//  * kNativeSym: beta = half_rn(-8 alpha) = -8 alpha exactly, so the unpack bias and the offset
-//    fold into one per-(row, group, quarter) constant, C = -1032 S_even - 72 S_odd, which seeds
-//    the even-k accumulator: y += alpha * (acc_e + acc_o / 16) with acc_e starting at C.
-//    kNativeAsym rebuilds beta = half_rn(-alpha * zp) from the stored zero point and applies
-//    y += alpha * (acc_e + acc_o / 16) + (beta - 1024 alpha) S_even + (beta - 64 alpha) S_odd.
+//  * The unpack bias and the offsets fold into per-(row, group, quarter) constants formed while
+//    staging, so the epilogue is short. kNativeSym: beta = half_rn(-8 alpha) = -8 alpha exactly,
+//    so y += alpha * (acc_e + acc_o / 16) with acc_e seeded by C = -1032 S_even - 72 S_odd.
+//    kNativeAsym: acc_e is seeded by -1024 S_even - 64 S_odd and
+//    y += alpha * (acc_e + acc_o / 16) + beta * (S_even + S_odd), beta = half_rn(-alpha * zp)
+//    rebuilt from the stored zero point (both columns in one packed fp16 multiply).
 //  * The four quarters of a column are summed across lanes (xor 16, xor 32) once per run, then
 //    across waves in LDS.
 #include "w4a16_gemv_kernels.h"
@@ -27,7 +28,7 @@ struct NativeSmem {
   static constexpr int kChunk = chunk_groups<MT, kCW>();
   static constexpr int kWordRows = G / 8;
   uint4 xs[MT][kChunk][kWordRows];  // re-paired fp16 activations, 16 B per word row
-  float2 sums[MT][kChunk][4];       // {even, odd} activation sums per quarter of the group
+  float2 sums[MT][kChunk][4];       // offset terms per quarter of the group (native_stage_store)
   float scale[MT][kChunk];          // power of two undoing the bf16 staging scale
   float red[kWaves][MT][kCW];       // cross-wave reduction
   int last;                         // this workgroup finishes the slice
@@ -68,7 +69,7 @@ __device__ __forceinline__ uint32_t unit_word(const NativeLoad<G>& ld, int i, in
 // Activations of one chunk into LDS: the staged, re-paired values as in the reference-packet
 // kernel, and the {even, odd} sums over each quarter (U consecutive word rows, U consecutive
 // lanes here).
-template <int G, Act A, int MT>
+template <int G, Act A, int MT, PacketFormat F>
 __device__ __forceinline__ void native_stage_store(NativeSmem<G, MT>& sm, StageRegs<G, MT, kCW>& st,
                                                    int n_chunk) {
   constexpr int WR = G / 8;
@@ -108,7 +109,12 @@ __device__ __forceinline__ void native_stage_store(NativeSmem<G, MT>& sm, StageR
     if (u < StageRegs<G, MT, kCW>::kUnits && gl < n_chunk) {
       sm.xs[m][gl][w] = pair_activations(r);
       if (w % U == 0) {
-        sm.sums[m][gl][w / U] = make_float2(se, so);
+        // The offset terms of the epilogue divided by alpha, per (row, group, quarter):
+        // kNativeSym (beta = -8 alpha): -1032 S_e - 72 S_o; kNativeAsym: -1024 S_e - 64 S_o,
+        // plus S_e + S_o for the beta * S term.
+        sm.sums[m][gl][w / U] = F == PacketFormat::kNativeSym
+                                    ? make_float2(fmaf(-1032.0f, se, -72.0f * so), 0.0f)
+                                    : make_float2(fmaf(-1024.0f, se, -64.0f * so), se + so);
       }
       if (w == 0) {
         sm.scale[m][gl] = undo;
@@ -128,10 +134,8 @@ __device__ __forceinline__ void native_compute_group(const NativeSmem<G, MT>& sm
   float acc_o[MT][2];
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
-    const float2 s = sm.sums[m][gl][t];
-    // kNativeSym: the whole offset term, C = (beta - 1024 alpha) S_e + (beta - 64 alpha) S_o
-    // divided by alpha (beta = -8 alpha), seeds the even accumulator.
-    const float seed = F == PacketFormat::kNativeSym ? fmaf(-1032.0f, s.x, -72.0f * s.y) : 0.0f;
+    // The offset term divided by alpha seeds the even accumulator (see native_stage_store).
+    const float seed = sm.sums[m][gl][t].x;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       acc_e[m][i] = seed;
@@ -162,22 +166,24 @@ __device__ __forceinline__ void native_compute_group(const NativeSmem<G, MT>& sm
       }
     }
   }
+  // kNativeAsym: beta = half_rn(-alpha * zp) for both columns with one packed fp16 multiply
+  // (fp16 0x6400 | z is 1024 + z, so 1024 - that is -z exactly).
+  uint32_t beta_pair = 0;
+  if constexpr (F == PacketFormat::kNativeAsym) {
+    const uint32_t z = (ld.zp & 0xFu) | ((ld.zp & 0xF0u) << 12);
+    const half2_t neg_z = __builtin_bit_cast(half2_t, 0x64006400u) -
+                          __builtin_bit_cast(half2_t, z | 0x64006400u);
+    beta_pair = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, ld.alpha) * neg_z);
+  }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const float a = half_bits_to_float(static_cast<uint16_t>(ld.alpha >> (16 * i)));
-    float ce = 0.0f;
-    float co = 0.0f;
-    if constexpr (F == PacketFormat::kNativeAsym) {
-      const float b = group_offset<F>(a, 0, (ld.zp >> (4 * i)) & 0xFu);
-      ce = fmaf(-1024.0f, a, b);  // beta - 1024 alpha
-      co = fmaf(-64.0f, a, b);    // beta - 64 alpha
-    }
+    const float b = half_bits_to_float(static_cast<uint16_t>(beta_pair >> (16 * i)));
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       float t_sum = a * fmaf(0.0625f, acc_o[m][i], acc_e[m][i]);
       if constexpr (F == PacketFormat::kNativeAsym) {
-        const float2 s = sm.sums[m][gl][t];
-        t_sum = fmaf(co, s.y, fmaf(ce, s.x, t_sum));
+        t_sum = fmaf(b, sm.sums[m][gl][t].y, t_sum);
       }
       if constexpr (A == Act::kBF16) {
         t_sum *= sm.scale[m][gl];
@@ -220,7 +226,7 @@ __device__ __forceinline__ void native_stream_groups(NativeSmem<G, MT>& sm, cons
       native_load<G, F>(buf[d], gp + static_cast<size_t>(min(d, t_last)) * step, lane);
     }
     __builtin_amdgcn_sched_barrier(0);  // keep every load above the first use of the activations
-    native_stage_store<G, A, MT>(sm, st, n_chunk);
+    native_stage_store<G, A, MT, F>(sm, st, n_chunk);
     lds_barrier();
     const int n_blocks = (n_w + D - 1) / D;
     int t0 = 0;
