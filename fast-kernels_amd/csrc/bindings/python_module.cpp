@@ -302,4 +302,57 @@ PYBIND11_MODULE(_native, m) {
       py::arg("workspace_ptr"), py::arg("workspace_bytes"), py::arg("batch"), py::arg("n"),
       py::arg("k"), py::arg("group_size"), py::arg("packet_format"), py::arg("activation_dtype"),
       py::arg("split_k_slices"), py::arg("stream_ptr"));
+  m.def(
+      "w4a16_plan_rmsnorm",
+      [](int batch, int n, int k, int group_size, int activation_dtype, int split_k_slices,
+         int cu_count, int packet_format) {
+        fk_arc_w4a16_plan plan{};
+        check(fk_w4a16_plan_rmsnorm(batch, n, k, group_size, activation_dtype, split_k_slices,
+                                    cu_count, packet_format, &plan));
+        py::dict d;
+        d["m_tile"] = plan.m_tile;
+        d["workgroups"] = plan.workgroups;
+        d["groups_per_workgroup"] = plan.groups_per_workgroup;
+        d["max_tile_contributors"] = plan.max_tile_contributors;
+        d["workspace_bytes"] = plan.workspace_bytes;
+        d["slice_cols"] = plan.slice_cols;
+        return d;
+      },
+      py::arg("batch"), py::arg("n"), py::arg("k"), py::arg("group_size"),
+      py::arg("activation_dtype"), py::arg("split_k_slices"), py::arg("cu_count"),
+      py::arg("packet_format"));
+  m.def(
+      "w4a16_forward_rmsnorm",
+      [](std::uintptr_t activations_ptr, std::uintptr_t norm_weight_ptr, float eps,
+         std::uintptr_t packets_ptr, std::uintptr_t output_ptr, std::uintptr_t workspace_ptr,
+         std::size_t workspace_bytes, int batch, int n, int k, int group_size, int packet_format,
+         int activation_dtype, int split_k_slices, std::uintptr_t stream_ptr) {
+        call([&] {
+          return fk_w4a16_forward_rmsnorm(cp(activations_ptr), cp(norm_weight_ptr), eps,
+                                          cp(packets_ptr), mp(output_ptr), mp(workspace_ptr),
+                                          workspace_bytes, batch, n, k, group_size, packet_format,
+                                          activation_dtype, split_k_slices, mp(stream_ptr));
+        });
+      },
+      py::arg("activations_ptr"), py::arg("norm_weight_ptr"), py::arg("eps"),
+      py::arg("packets_ptr"), py::arg("output_ptr"), py::arg("workspace_ptr"),
+      py::arg("workspace_bytes"), py::arg("batch"), py::arg("n"), py::arg("k"),
+      py::arg("group_size"), py::arg("packet_format"), py::arg("activation_dtype"),
+      py::arg("split_k_slices"), py::arg("stream_ptr"));
+  m.def(
+      "w4a16_forward_silu_mul",
+      [](std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::uintptr_t output_ptr,
+         int batch, int n, int k, int group_size, int packet_format, int activation_dtype,
+         std::uintptr_t norm_weight_ptr, float eps, std::uintptr_t stream_ptr) {
+        call([&] {
+          return fk_w4a16_forward_silu_mul(cp(activations_ptr), cp(packets_ptr), mp(output_ptr),
+                                           batch, n, k, group_size, packet_format,
+                                           activation_dtype, cp(norm_weight_ptr), eps,
+                                           mp(stream_ptr));
+        });
+      },
+      py::arg("activations_ptr"), py::arg("packets_ptr"), py::arg("output_ptr"), py::arg("batch"),
+      py::arg("n"), py::arg("k"), py::arg("group_size"), py::arg("packet_format"),
+      py::arg("activation_dtype"), py::arg("norm_weight_ptr"), py::arg("eps"),
+      py::arg("stream_ptr"));
 }

@@ -230,4 +230,40 @@ int fk_arc_w4a16_forward_native(const void* activations, const void* packets, vo
   });
 }
 
+int fk_w4a16_plan_rmsnorm(int batch, int n, int k, int group_size, int activation_dtype,
+                          int split_k_slices, int cu_count, int packet_format,
+                          fk_arc_w4a16_plan* plan) {
+  return guarded([&] {
+    if (plan == nullptr) {
+      throw std::invalid_argument("plan must not be null");
+    }
+    copy_plan(ops::plan_w4a16_rmsnorm(batch, n, k, group_size, activation_dtype, split_k_slices,
+                                      cu_count, packet_format),
+              plan);
+  });
+}
+
+int fk_w4a16_forward_rmsnorm(const void* activations, const void* norm_weight, float eps,
+                             const void* packets, void* output, void* workspace,
+                             size_t workspace_bytes, int batch, int n, int k, int group_size,
+                             int packet_format, int activation_dtype, int split_k_slices,
+                             void* stream) {
+  return guarded([&] {
+    ops::arc_w4a16_forward_rmsnorm(P(activations), P(norm_weight), eps, P(packets), P(output),
+                                   P(workspace), workspace_bytes, batch, n, k, group_size,
+                                   packet_format, activation_dtype, split_k_slices, P(stream));
+  });
+}
+
+int fk_w4a16_forward_silu_mul(const void* activations, const void* packets, void* output,
+                              int batch, int n, int k, int group_size, int packet_format,
+                              int activation_dtype, const void* norm_weight, float eps,
+                              void* stream) {
+  return guarded([&] {
+    ops::arc_w4a16_forward_silu_mul(P(activations), P(packets), P(output), batch, n, k,
+                                    group_size, packet_format, activation_dtype, P(stream),
+                                    P(norm_weight), eps);
+  });
+}
+
 }  // extern "C"

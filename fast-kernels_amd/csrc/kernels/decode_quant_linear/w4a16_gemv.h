@@ -12,6 +12,14 @@ enum class GemvMode : int {
   kPartials = 1,  // fixed split-K, writes fp32 partials [S_k, M, N] (reference layout)
 };
 
+// Decode-step neighbours fused into the native-slab GEMV (w4a16_gemv_fused.hip):
+//  kRmsNorm: y = W . rmsnorm(x), rmsnorm(x) = gamma * round(x * rsqrt(mean(x^2) + eps)), rounded
+//            to the activation dtype after each product as the unfused pipeline does.
+//  kSiluMul: W = [W_gate; W_up] stacked along N; out[M, N/2] = silu(g) * u in the activation
+//            dtype, g and u rounded to it first.
+//  kRmsNormSiluMul: both (the gate_up projection of a Llama block with its input norm).
+enum class GemvFuse : int { kNone = 0, kRmsNorm = 1, kSiluMul = 2, kRmsNormSiluMul = 3 };
+
 struct GemvLaunch {
   const void* x = nullptr;
   const void* packets = nullptr;
@@ -29,6 +37,9 @@ struct GemvLaunch {
   int max_contributors = 0;     // kStreamK: partial slots per slice in the scratch
   int slice_cols = kTileCols;   // kStreamK: columns per workgroup slice (128, 64 or 32)
   PacketFormat format = PacketFormat::kArc;  // kStreamK: packet format of `packets`
+  GemvFuse fuse = GemvFuse::kNone;           // native formats: fused decode-step neighbour
+  const void* norm_weight = nullptr;         // GemvFuse::kRmsNorm: gamma [K], activation dtype
+  float eps = 0.0f;                          // GemvFuse::kRmsNorm: epsilon
 };
 
 // Activation rows per m-tile for a batch: 1, 2, 4, 8 on the dot2 GEMV kernel, kMfmaRows (from
@@ -38,6 +49,7 @@ constexpr int kMfmaMinBatch = 8;
 int gemv_m_tile_for_batch(int batch);
 // m-tile of the reference split-K protocol (kPartials), served by the dot2 kernel only.
 int gemv_partials_m_tile_for_batch(int batch);
+hipError_t launch_w4a16_gemv_fused(const GemvLaunch& l, hipStream_t stream);
 
 // Tiles (128 columns x m_tile rows) of a launch; the stream-K scratch holds one counter per slice
 // (tiles x 128 / slice_cols) and max_contributors fp32 partial slots of m_tile x 128 floats per

@@ -19,6 +19,9 @@ int gemv_partials_m_tile_for_batch(int batch) {
 }
 
 hipError_t launch_w4a16_gemv(const GemvLaunch& l, hipStream_t stream) {
+  if (l.fuse != GemvFuse::kNone) {
+    return launch_w4a16_gemv_fused(l, stream);
+  }
   if (l.m_tile == kMfmaRows) {
     return launch_w4a16_gemm_mfma(l, stream);
   }

@@ -94,6 +94,8 @@ struct GemvParams {
   int per;                          // stream-K: group units per workgroup
   int max_contrib;                  // stream-K: partial slots per slice in the scratch
   int xcd_remap;
+  const uint16_t* norm_weight;      // RMSNorm prologue: gamma [K] (activation dtype), else null
+  float eps;                        // RMSNorm prologue: epsilon
 };
 
 template <int G, int MT, int CW>

@@ -1,340 +1,15 @@
-// W4A16 GEMV / small-batch GEMM (dot2 path) over the native slab formats (PacketFormat in
-// w4a16_device.h): kNativeSym and kNativeAsym, 1-8 activation rows. Same math, staging, stream-K
-// work split and fix-up as the reference-packet kernel (w4a16_gemv_kernels.h), with a lane mapping
-// that follows the slab's quarter order:
-//
-//  * A workgroup streams runs of one 32-column slice; the slice's groups are one contiguous byte
-//    range, and every wave-wide load reads 1 KB (G = 128: two loads per group; G = 64: one).
-//  * Lane l = 16t + n owns quarter t (U = G/32 consecutive code words, 8U values of k) of columns
-//    n and n + 16. Per group it therefore applies scales to two columns, not four, and reads U
-//    16-byte activation vectors per row (broadcast: the 16 lanes of a quarter read the same one).
-//  * The unpack bias and the offsets fold into per-(row, group, quarter) constants formed while
-//    staging, so the epilogue is short. kNativeSym: beta = half_rn(-8 alpha) = -8 alpha exactly,
-//    so y += alpha * (acc_e + acc_o / 16) with acc_e seeded by C = -1032 S_even - 72 S_odd.
-//    kNativeAsym: acc_e is seeded by -1024 S_even - 64 S_odd and
-//    y += alpha * (acc_e + acc_o / 16) + beta * (S_even + S_odd), beta = half_rn(-alpha * zp)
-//    rebuilt from the stored zero point (both columns in one packed fp16 multiply).
-//  * The four quarters of a column are summed across lanes (xor 16, xor 32) once per run, then
-//    across waves in LDS.
-#include "w4a16_gemv_kernels.h"
+// W4A16 GEMV over the native slab formats: the plain forward (kernel, launch and dispatch). The
+// layout, lane mapping and device building blocks are described in w4a16_gemv_native.h.
+#include "w4a16_gemv_native.h"
 
 namespace fk {
 namespace {
 
-constexpr int kCW = kSliceCols;
-
-template <int G, int MT>
-struct NativeSmem {
-  static constexpr int kChunk = chunk_groups<MT, kCW>();
-  static constexpr int kWordRows = G / 8;
-  uint4 xs[MT][kChunk][kWordRows];  // re-paired fp16 activations, 16 B per word row
-  float2 sums[MT][kChunk][4];       // offset terms per quarter of the group (native_stage_store)
-  float scale[MT][kChunk];          // power of two undoing the bf16 staging scale
-  float red[kWaves][MT][kCW];       // cross-wave reduction
-  int last;                         // this workgroup finishes the slice
-};
-
-template <int G>
-struct NativeLoad {
-  static constexpr int kVecs = G == 128 ? 2 : 1;
-  uint4 w[kVecs];
-  uint32_t alpha;  // alpha of columns n (bits 0-15) and n + 16
-  uint32_t zp;     // kNativeAsym: zero points of columns n (bits 0-3) and n + 16 (bits 4-7)
-};
-
-template <int G, PacketFormat F>
-__device__ __forceinline__ void native_load(NativeLoad<G>& ld, const uint8_t* slab, int lane) {
-#pragma unroll
-  for (int v = 0; v < NativeLoad<G>::kVecs; ++v) {
-    ld.w[v] = *reinterpret_cast<const uint4*>(slab + v * 1024 + lane * 16);
-  }
-  ld.alpha = *reinterpret_cast<const uint32_t*>(slab + native_alpha_offset(G) + 4 * (lane % 16));
-  if constexpr (F == PacketFormat::kNativeAsym) {
-    ld.zp = *(slab + native_zp_offset(G) + lane % 16);
-  }
-}
-
-// Word j of the lane's unit of column n + 16 i.
-template <int G>
-__device__ __forceinline__ uint32_t unit_word(const NativeLoad<G>& ld, int i, int j) {
-  if constexpr (G == 128) {
-    const uint4 v = ld.w[i];
-    return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
-  } else {
-    const uint4 v = ld.w[0];
-    return i == 0 ? (j == 0 ? v.x : v.y) : (j == 0 ? v.z : v.w);
-  }
-}
-
-// Activations of one chunk into LDS: the staged, re-paired values as in the reference-packet
-// kernel, and the {even, odd} sums over each quarter (U consecutive word rows, U consecutive
-// lanes here).
-template <int G, Act A, int MT, PacketFormat F>
-__device__ __forceinline__ void native_stage_store(NativeSmem<G, MT>& sm, StageRegs<G, MT, kCW>& st,
-                                                   int n_chunk) {
-  constexpr int WR = G / 8;
-  constexpr int U = native_unit_words(G);
-  constexpr int kChunk = NativeSmem<G, MT>::kChunk;
-  const int tid = static_cast<int>(threadIdx.x);
-#pragma unroll
-  for (int it = 0; it < StageRegs<G, MT, kCW>::kPerThread; ++it) {
-    const int u = it * kThreads + tid;
-    const int w = u % WR;
-    const int gl = (u / WR) % kChunk;
-    const int m = u / (WR * kChunk);
-    uint4 r = st.raw[it];
-    float undo = 1.0f;
-    if constexpr (A == Act::kBF16) {
-      const uint32_t e = group_max<WR>(
-          max(max(bf16_exp(r.x), bf16_exp(r.y)), max(bf16_exp(r.z), bf16_exp(r.w))));
-      const int shift = max(0, static_cast<int>(e) - kMaxFp16SafeBf16Exp);
-      const float s = __builtin_bit_cast(float, static_cast<uint32_t>(127 - shift) << 23);
-      undo = __builtin_bit_cast(float, static_cast<uint32_t>(127 + shift) << 23);
-      r.x = bf16_pair_to_half_pair(r.x, s);
-      r.y = bf16_pair_to_half_pair(r.y, s);
-      r.z = bf16_pair_to_half_pair(r.z, s);
-      r.w = bf16_pair_to_half_pair(r.w, s);
-    }
-    // even k: x0 x2 x4 x6 (low halves), odd k: x1 x3 x5 x7 (high halves)
-    float se = half_bits_to_float(static_cast<uint16_t>(r.x)) +
-               half_bits_to_float(static_cast<uint16_t>(r.y)) +
-               half_bits_to_float(static_cast<uint16_t>(r.z)) +
-               half_bits_to_float(static_cast<uint16_t>(r.w));
-    float so = half_bits_to_float(static_cast<uint16_t>(r.x >> 16)) +
-               half_bits_to_float(static_cast<uint16_t>(r.y >> 16)) +
-               half_bits_to_float(static_cast<uint16_t>(r.z >> 16)) +
-               half_bits_to_float(static_cast<uint16_t>(r.w >> 16));
-    se = group_sum<U>(se);
-    so = group_sum<U>(so);
-    if (u < StageRegs<G, MT, kCW>::kUnits && gl < n_chunk) {
-      sm.xs[m][gl][w] = pair_activations(r);
-      if (w % U == 0) {
-        // The offset terms of the epilogue divided by alpha, per (row, group, quarter):
-        // kNativeSym (beta = -8 alpha): -1032 S_e - 72 S_o; kNativeAsym: -1024 S_e - 64 S_o,
-        // plus S_e + S_o for the beta * S term.
-        sm.sums[m][gl][w / U] = F == PacketFormat::kNativeSym
-                                    ? make_float2(fmaf(-1032.0f, se, -72.0f * so), 0.0f)
-                                    : make_float2(fmaf(-1024.0f, se, -64.0f * so), se + so);
-      }
-      if (w == 0) {
-        sm.scale[m][gl] = undo;
-      }
-    }
-  }
-}
-
-template <int G, Act A, int MT, PacketFormat F>
-__device__ __forceinline__ void native_compute_group(const NativeSmem<G, MT>& sm,
-                                                     const NativeLoad<G>& ld, int gl, int t,
-                                                     uint32_t mask_lo, uint32_t mask_hi,
-                                                     float (&y)[MT][2]) {
-  constexpr int U = native_unit_words(G);
-  constexpr uint32_t kBias = 0x64006400u;  // fp16 1024.0 pair
-  float acc_e[MT][2];
-  float acc_o[MT][2];
-#pragma unroll
-  for (int m = 0; m < MT; ++m) {
-    // The offset term divided by alpha seeds the even accumulator (see native_stage_store).
-    const float seed = sm.sums[m][gl][t].x;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      acc_e[m][i] = seed;
-      acc_o[m][i] = 0.0f;
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < U; ++j) {
-    uint32_t e0[2], o0[2], e1[2], o1[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t wv = unit_word<G>(ld, i, j);
-      const uint32_t w8 = wv >> 8;
-      e0[i] = (wv & mask_lo) | kBias;  // 1024+q for k0,k4
-      o0[i] = (wv & mask_hi) | kBias;  // 1024+16q for k1,k5
-      e1[i] = (w8 & mask_lo) | kBias;  // k2,k6
-      o1[i] = (w8 & mask_hi) | kBias;  // k3,k7
-    }
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const uint4 xp = sm.xs[m][gl][U * t + j];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        acc_e[m][i] = dot2<Act::kF16>(e0[i], xp.x, acc_e[m][i]);
-        acc_o[m][i] = dot2<Act::kF16>(o0[i], xp.y, acc_o[m][i]);
-        acc_e[m][i] = dot2<Act::kF16>(e1[i], xp.z, acc_e[m][i]);
-        acc_o[m][i] = dot2<Act::kF16>(o1[i], xp.w, acc_o[m][i]);
-      }
-    }
-  }
-  // kNativeAsym: beta = half_rn(-alpha * zp) for both columns with one packed fp16 multiply
-  // (fp16 0x6400 | z is 1024 + z, so 1024 - that is -z exactly).
-  uint32_t beta_pair = 0;
-  if constexpr (F == PacketFormat::kNativeAsym) {
-    const uint32_t z = (ld.zp & 0xFu) | ((ld.zp & 0xF0u) << 12);
-    const half2_t neg_z = __builtin_bit_cast(half2_t, 0x64006400u) -
-                          __builtin_bit_cast(half2_t, z | 0x64006400u);
-    beta_pair = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, ld.alpha) * neg_z);
-  }
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const float a = half_bits_to_float(static_cast<uint16_t>(ld.alpha >> (16 * i)));
-    const float b = half_bits_to_float(static_cast<uint16_t>(beta_pair >> (16 * i)));
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      float t_sum = a * fmaf(0.0625f, acc_o[m][i], acc_e[m][i]);
-      if constexpr (F == PacketFormat::kNativeAsym) {
-        t_sum = fmaf(b, sm.sums[m][gl][t].y, t_sum);
-      }
-      if constexpr (A == Act::kBF16) {
-        t_sum *= sm.scale[m][gl];
-      }
-      y[m][i] += t_sum;
-    }
-  }
-}
-
-// Groups [g_lo, g_hi) of one slice: stage the activations of up to kChunk groups in LDS, then
-// each wave streams groups g_lo + wave, g_lo + wave + 4, ... through D register buffers (as the
-// reference-packet kernel's stream_groups).
-template <int G, Act A, int MT, PacketFormat F>
-__device__ __forceinline__ void native_stream_groups(NativeSmem<G, MT>& sm, const GemvParams& p,
-                                                     const uint8_t* slabs, int row0, int g_lo,
-                                                     int g_hi, int lane, int wave,
-                                                     uint32_t mask_lo, uint32_t mask_hi,
-                                                     float (&y)[MT][2]) {
-  constexpr int kChunk = NativeSmem<G, MT>::kChunk;
-  // 8 KB of weights in flight per wave (4 groups at G = 128, 8 at G = 64): measured on MI355X,
-  // deeper pipelines (8 or 16 KB per wave) lower the achieved HBM bandwidth of every decode shape.
-  constexpr int D = 8 / NativeLoad<G>::kVecs / (MT >= 8 ? 2 : 1);
-  const size_t stride = static_cast<size_t>(format_packet_stride(G, F));
-  const int t = lane / 16;
-  for (int g0 = g_lo; g0 < g_hi; g0 += kChunk) {
-    const int n_chunk = min(kChunk, g_hi - g0);
-    if (g0 != g_lo) {
-      lds_barrier();  // previous chunk's readers are done with xs / sums
-    }
-    StageRegs<G, MT, kCW> st;
-    stage_load<G, MT, kCW>(st, p, row0, g0, n_chunk);
-    const int n_w = n_chunk > wave ? (n_chunk - wave + kWaves - 1) / kWaves : 0;
-    const int t_last = max(n_w - 1, 0);
-    const int gl_base = n_w > 0 ? wave : n_chunk - 1;
-    const uint8_t* gp = slabs + static_cast<size_t>(g0 + gl_base) * stride;
-    const size_t step = static_cast<size_t>(kWaves) * stride;
-    NativeLoad<G> buf[D];
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      native_load<G, F>(buf[d], gp + static_cast<size_t>(min(d, t_last)) * step, lane);
-    }
-    __builtin_amdgcn_sched_barrier(0);  // keep every load above the first use of the activations
-    native_stage_store<G, A, MT, F>(sm, st, n_chunk);
-    lds_barrier();
-    const int n_blocks = (n_w + D - 1) / D;
-    int t0 = 0;
-    for (int blk = 0; blk + 1 < n_blocks; ++blk, t0 += D) {
-#pragma unroll
-      for (int d = 0; d < D; ++d) {
-        native_compute_group<G, A, MT, F>(sm, buf[d], wave + (t0 + d) * kWaves, t, mask_lo,
-                                          mask_hi, y);
-        native_load<G, F>(buf[d], gp + static_cast<size_t>(min(t0 + D + d, t_last)) * step, lane);
-      }
-    }
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      if (t0 + d < n_w) {
-        native_compute_group<G, A, MT, F>(sm, buf[d], wave + (t0 + d) * kWaves, t, mask_lo,
-                                          mask_hi, y);
-      }
-    }
-  }
-}
-
-// Stream-K over (m-tile, tile, slice, group) units, as the reference-packet kernel with 32-column
-// slices: workgroup b owns units [b*per, (b+1)*per); slices split between workgroups are finished
-// by finish_run.
-template <int G, Act A, int MT, PacketFormat F>
-__global__ void __launch_bounds__(kThreads, min_waves_per_eu<MT>())
-w4a16_gemv_native_kernel(GemvParams p) {
-  __shared__ NativeSmem<G, MT> sm;
-  const int tid = static_cast<int>(threadIdx.x);
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t mask_lo = vgpr_constant(0x000f000fu);
-  const uint32_t mask_hi = vgpr_constant(0x00f000f0u);
-  const size_t stride = static_cast<size_t>(format_packet_stride(G, F));
-  const int grid = static_cast<int>(gridDim.x);
-  int b = static_cast<int>(blockIdx.x);
-  if (p.xcd_remap) {
-    b = (b & 7) * (grid >> 3) + (b >> 3);
-  }
-  const long long total_units =
-      static_cast<long long>(p.tiles) * kSlicesPerTile * p.mtiles * p.NG;
-  const long long u_begin = static_cast<long long>(b) * p.per;
-  const long long u_end = min(total_units, u_begin + p.per);
-  long long u = u_begin;
-  while (u < u_end) {
-    const int T = static_cast<int>(u / p.NG);
-    const int g_lo = static_cast<int>(u - static_cast<long long>(T) * p.NG);
-    const int g_hi = static_cast<int>(min(static_cast<long long>(p.NG), g_lo + (u_end - u)));
-    const int slice = T % kSlicesPerTile;
-    const int tile = (T / kSlicesPerTile) % p.tiles;
-    const int row0 = (T / (kSlicesPerTile * p.tiles)) * MT;
-    const uint8_t* slabs =
-        p.packets + (static_cast<size_t>(tile) * kSlicesPerTile + slice) * p.NG * stride;
-    float y[MT][2] = {};
-    native_stream_groups<G, A, MT, F>(sm, p, slabs, row0, g_lo, g_hi, lane, wave, mask_lo,
-                                      mask_hi, y);
-    // Quarters of a column live in lanes n, n+16, n+32, n+48.
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        y[m][i] += __shfl_xor(y[m][i], 16);
-        y[m][i] += __shfl_xor(y[m][i], 32);
-      }
-    }
-    if (lane < 16) {
-#pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        sm.red[wave][m][lane] = y[m][0];
-        sm.red[wave][m][lane + 16] = y[m][1];
-      }
-    }
-    __syncthreads();
-    finish_run<A, MT, kCW>(p, T, b, row0, tile * kTileCols + slice * kCW, sm.last,
-                           [&](int m, int c) {
-                             float v = sm.red[0][m][c];
-#pragma unroll
-                             for (int w = 1; w < kWaves; ++w) {
-                               v += sm.red[w][m][c];
-                             }
-                             return v;
-                           });
-    u += g_hi - g_lo;
-  }
-}
-
 template <int G, Act A, int MT, PacketFormat F>
 hipError_t launch_native_t(const GemvLaunch& l, hipStream_t stream) {
-  GemvParams p;
-  p.x = static_cast<const uint16_t*>(l.x);
-  p.packets = static_cast<const uint8_t*>(l.packets);
-  p.out = static_cast<uint16_t*>(l.out);
-  p.partials = static_cast<float*>(l.partials);
-  p.counters = static_cast<uint32_t*>(l.counters);
-  p.M = l.M;
-  p.N = l.N;
-  p.K = l.K;
-  p.NG = l.K / G;
-  p.tiles = l.N / kTileCols;
-  p.mtiles = (l.M + MT - 1) / MT;
-  p.splits = 0;
-  p.gps = 0;
-  p.per = l.units_per_workgroup;
-  p.max_contrib = l.max_contributors;
-  const long long total = static_cast<long long>(p.tiles) * kSlicesPerTile * p.mtiles * p.NG;
-  const int grid = static_cast<int>((total + p.per - 1) / p.per);
-  p.xcd_remap = (grid % 8 == 0) ? 1 : 0;
-  hipLaunchKernelGGL((w4a16_gemv_native_kernel<G, A, MT, F>), dim3(grid), dim3(kThreads), 0,
+  int grid = 0;
+  const GemvParams p = native_params<G, MT>(l, &grid);
+  hipLaunchKernelGGL((w4a16_gemv_native_kernel<G, A, MT, F, false>), dim3(grid), dim3(kThreads), 0,
                      stream, p);
   return hipGetLastError();
 }

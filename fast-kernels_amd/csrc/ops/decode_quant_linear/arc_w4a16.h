@@ -106,6 +106,28 @@ void arc_w4a16_forward_ex(std::uintptr_t activations_ptr, std::uintptr_t packets
 ArcW4A16Plan plan_w4a16_for_format(int batch, int n, int k, int group_size, int activation_dtype,
                                    int split_k_slices, int cu_count, int packet_format);
 
+// Fused decode-step neighbours over native slabs (packet_format kPacketNativeSym or
+// kPacketNativeAsym). y = W . rmsnorm(x), rmsnorm(x) = round(gamma * round(x * rsqrt(mean(x^2) +
+// eps))) in the activation dtype, gamma = norm_weight [K]; plan, workspace contract and results
+// otherwise as arc_w4a16_forward_native (the plan keeps 8+ rows on the dot2 kernel).
+void arc_w4a16_forward_rmsnorm(std::uintptr_t activations_ptr, std::uintptr_t norm_weight_ptr,
+                               float eps, std::uintptr_t packets_ptr, std::uintptr_t output_ptr,
+                               std::uintptr_t workspace_ptr, std::size_t workspace_bytes, int batch,
+                               int n, int k, int group_size, int packet_format,
+                               int activation_dtype, int split_k_slices, std::uintptr_t stream_ptr);
+ArcW4A16Plan plan_w4a16_rmsnorm(int batch, int n, int k, int group_size, int activation_dtype,
+                                int split_k_slices, int cu_count, int packet_format);
+
+// The gate_up projection with its SiLU: the slabs hold [W_gate; W_up] stacked along n (n % 256
+// == 0); output [batch, n / 2] = round(round(silu(round(x.W_gate^T))) * round(x.W_up^T)) in the
+// activation dtype. A non-null norm_weight_ptr adds the RMSNorm prologue of
+// arc_w4a16_forward_rmsnorm to x. No workspace.
+void arc_w4a16_forward_silu_mul(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
+                                std::uintptr_t output_ptr, int batch, int n, int k, int group_size,
+                                int packet_format, int activation_dtype,
+                                std::uintptr_t stream_ptr, std::uintptr_t norm_weight_ptr = 0,
+                                float eps = 0.0f);
+
 // Bytes per packet of a format.
 int packet_format_stride_bytes(int group_size, int packet_format);
 

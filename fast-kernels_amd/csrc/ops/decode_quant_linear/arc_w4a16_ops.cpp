@@ -216,8 +216,13 @@ ArcW4A16Plan plan_arc_w4a16_for_cu_count(int batch, int n, int k, int group_size
   return plan;
 }
 
-ArcW4A16Plan plan_w4a16_for_format(int batch, int n, int k, int group_size, int activation_dtype,
-                                   int split_k_slices, int cu_count, int packet_format) {
+namespace {
+
+// plan_w4a16_for_format; dot2_only keeps batches of 8+ rows on the dot2 kernel (m-tiles of at
+// most 8 rows), which the fused kernels need.
+ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int activation_dtype,
+                                  int split_k_slices, int cu_count, int packet_format,
+                                  bool dot2_only) {
   const fk::PacketFormat format = to_packet_format(packet_format, true);
   validate_dimensions(batch, n, k, group_size);
   if (cu_count == 0) {
@@ -225,6 +230,9 @@ ArcW4A16Plan plan_w4a16_for_format(int batch, int n, int k, int group_size, int 
   }
   ArcW4A16Plan plan = plan_arc_w4a16_for_cu_count(batch, n, k, group_size, activation_dtype,
                                                   split_k_slices, cu_count);
+  if (dot2_only) {
+    plan.m_tile = fk::gemv_partials_m_tile_for_batch(batch);
+  }
   if (format == fk::PacketFormat::kArc || plan.m_tile == fk::kMfmaRows) {
     return plan;  // the matrix-core kernel reads whole tiles in every format
   }
@@ -250,6 +258,14 @@ ArcW4A16Plan plan_w4a16_for_format(int batch, int n, int k, int group_size, int 
   finish_plan(plan, fk::gemv_tiles(n, batch, plan.m_tile), fk::kSlicesPerTile, num_groups, per, n,
               batch);
   return plan;
+}
+
+}  // namespace
+
+ArcW4A16Plan plan_w4a16_for_format(int batch, int n, int k, int group_size, int activation_dtype,
+                                   int split_k_slices, int cu_count, int packet_format) {
+  return plan_for_format_impl(batch, n, k, group_size, activation_dtype, split_k_slices, cu_count,
+                              packet_format, false);
 }
 
 namespace {
@@ -290,7 +306,9 @@ void* library_workspace(std::size_t bytes, hipStream_t stream) {
 void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::uintptr_t output_ptr,
               void* workspace, const ArcW4A16Plan& plan, int batch, int n, int k, int group_size,
               int activation_dtype, hipStream_t stream,
-              fk::PacketFormat format = fk::PacketFormat::kArc) {
+              fk::PacketFormat format = fk::PacketFormat::kArc,
+              fk::GemvFuse fuse = fk::GemvFuse::kNone, std::uintptr_t norm_weight_ptr = 0,
+              float eps = 0.0f) {
   fk::GemvLaunch l;
   l.x = reinterpret_cast<const void*>(activations_ptr);
   l.packets = reinterpret_cast<const void*>(packets_ptr);
@@ -306,6 +324,9 @@ void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::u
   l.max_contributors = plan.max_tile_contributors;
   l.slice_cols = plan.slice_cols;
   l.format = format;
+  l.fuse = fuse;
+  l.norm_weight = reinterpret_cast<const void*>(norm_weight_ptr);
+  l.eps = eps;
   if (plan.workspace_bytes > 0) {
     l.counters = workspace;
     l.partials = static_cast<char*>(workspace) + kCounterRegionBytes;
@@ -713,6 +734,76 @@ void arc_w4a16_forward_native(std::uintptr_t activations_ptr, std::uintptr_t pac
   forward_with_format(activations_ptr, packets_ptr, output_ptr, workspace_ptr, workspace_bytes,
                       batch, n, k, group_size, to_packet_format(packet_format, true),
                       activation_dtype, split_k_slices, stream_ptr);
+}
+
+void arc_w4a16_forward_rmsnorm(std::uintptr_t activations_ptr, std::uintptr_t norm_weight_ptr,
+                               float eps, std::uintptr_t packets_ptr, std::uintptr_t output_ptr,
+                               std::uintptr_t workspace_ptr, std::size_t workspace_bytes, int batch,
+                               int n, int k, int group_size, int packet_format,
+                               int activation_dtype, int split_k_slices, std::uintptr_t stream_ptr) {
+  validate_dimensions(batch, n, k, group_size);
+  const fk::PacketFormat format = to_packet_format(packet_format, false);
+  validate_activation_dtype(activation_dtype);
+  validate_forward_buffers(activations_ptr, packets_ptr, output_ptr);
+  validate_pointer(norm_weight_ptr, 16, "norm_weight");
+  if (!(eps >= 0.0f)) {
+    throw_invalid("eps must be >= 0");
+  }
+  if (split_k_slices < 0) {
+    throw_invalid("split_k_slices must be >= 0 (0 = automatic)");
+  }
+  const ArcW4A16Plan plan = plan_w4a16_rmsnorm(batch, n, k, group_size, activation_dtype,
+                                               split_k_slices, 0, packet_format);
+  if (plan.workspace_bytes > 0) {
+    validate_pointer(workspace_ptr, kCounterRegionAlign, "workspace");
+    if (workspace_bytes < plan.workspace_bytes) {
+      std::ostringstream oss;
+      oss << "workspace_bytes=" << workspace_bytes << " is smaller than the " << plan.workspace_bytes
+          << " bytes this launch needs";
+      throw_invalid(oss.str());
+    }
+  }
+  run_gemv(activations_ptr, packets_ptr, output_ptr, reinterpret_cast<void*>(workspace_ptr), plan,
+           batch, n, k, group_size, activation_dtype, reinterpret_cast<hipStream_t>(stream_ptr),
+           format, fk::GemvFuse::kRmsNorm, norm_weight_ptr, eps);
+}
+
+ArcW4A16Plan plan_w4a16_rmsnorm(int batch, int n, int k, int group_size, int activation_dtype,
+                                int split_k_slices, int cu_count, int packet_format) {
+  to_packet_format(packet_format, false);
+  return plan_for_format_impl(batch, n, k, group_size, activation_dtype, split_k_slices, cu_count,
+                              packet_format, true);
+}
+
+void arc_w4a16_forward_silu_mul(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
+                                std::uintptr_t output_ptr, int batch, int n, int k, int group_size,
+                                int packet_format, int activation_dtype,
+                                std::uintptr_t stream_ptr, std::uintptr_t norm_weight_ptr,
+                                float eps) {
+  validate_dimensions(batch, n, k, group_size);
+  if (n % (2 * fk::kTileCols) != 0) {
+    throw_invalid("n (gate and up rows together) must be divisible by 256");
+  }
+  const fk::PacketFormat format = to_packet_format(packet_format, false);
+  validate_activation_dtype(activation_dtype);
+  validate_forward_buffers(activations_ptr, packets_ptr, output_ptr);
+  const bool norm = norm_weight_ptr != 0;
+  if (norm && !(eps >= 0.0f)) {
+    throw_invalid("eps must be >= 0");
+  }
+  if (norm) {
+    validate_pointer(norm_weight_ptr, 16, "norm_weight");
+  }
+  // One workgroup per (gate slice, up slice) pair over all of K: no fix-up, no workspace.
+  ArcW4A16Plan plan{};
+  plan.m_tile = fk::gemv_partials_m_tile_for_batch(batch);
+  plan.slice_cols = fk::kSliceCols;
+  plan.groups_per_workgroup = k / group_size;
+  plan.max_tile_contributors = 1;
+  plan.workspace_bytes = 0;
+  run_gemv(activations_ptr, packets_ptr, output_ptr, nullptr, plan, batch, n, k, group_size,
+           activation_dtype, reinterpret_cast<hipStream_t>(stream_ptr), format,
+           norm ? fk::GemvFuse::kRmsNormSiluMul : fk::GemvFuse::kSiluMul, norm_weight_ptr, eps);
 }
 
 }  // namespace fast_kernels::decode_quant_linear

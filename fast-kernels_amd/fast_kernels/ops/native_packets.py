@@ -244,3 +244,113 @@ def arc_w4a16_forward_native(
         n, k, group_size, code, act, requested, _current_stream_ptr(activations.device),
     )
     return output
+
+
+def arc_w4a16_forward_rmsnorm(
+    activations: torch.Tensor,
+    norm_weight: torch.Tensor,
+    packets: torch.Tensor,
+    *,
+    n: int,
+    k: int,
+    group_size: int,
+    eps: float = 1e-5,
+    packet_format: str | int = "native_sym",
+    output: torch.Tensor | None = None,
+    split_k_slices: int | None = None,
+) -> torch.Tensor:
+    """y = rmsnorm(x) . W^T in one launch over native slabs, with
+    rmsnorm(x) = round(norm_weight * round(x * rsqrt(mean(x^2) + eps))) in the activation dtype
+    (the Llama input norm of the qkv and gate_up projections, rounded as an unfused norm kernel
+    that writes its output would round it). norm_weight: [k], the activation dtype."""
+    torch = _require_torch()
+    native = _require_gpu_backend()
+    code = _native_code(packet_format)
+    _check_gpu_tensor(
+        activations, name="activations", dtype=(torch.float16, torch.bfloat16), ndim=2
+    )
+    _check_gpu_tensor(norm_weight, name="norm_weight", dtype=activations.dtype, ndim=1)
+    _check_gpu_tensor(packets, name="packets", dtype=torch.uint8, ndim=2)
+    batch = activations.shape[0]
+    if activations.shape[1] != k or norm_weight.shape[0] != k:
+        raise ValueError("activations.shape[1] and norm_weight.shape[0] must match k")
+    shape = _packet_shape(n, k, group_size, code)
+    if tuple(packets.shape) != shape:
+        raise ValueError(f"packets must have shape {shape}")
+    if output is None:
+        output = torch.empty((batch, n), device=activations.device, dtype=activations.dtype)
+    else:
+        _check_gpu_tensor(output, name="output", dtype=activations.dtype, ndim=2)
+        if tuple(output.shape) != (batch, n):
+            raise ValueError(f"output must have shape {(batch, n)}")
+    _check_same_device(("activations", activations), ("norm_weight", norm_weight),
+                       ("packets", packets), ("output", output))
+    if split_k_slices is not None and split_k_slices < 1:
+        raise ValueError("split_k_slices must be positive")
+    requested = 0 if split_k_slices is None else int(split_k_slices)
+    act = _act_code(activations.dtype)
+    plan = native.w4a16_plan_rmsnorm(batch, n, k, group_size, act, requested, 0, code)
+    ws_ptr, ws_bytes = 0, int(plan["workspace_bytes"])
+    if ws_bytes > 0:
+        ws = arc_workspace(activations.device, ws_bytes)
+        ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
+    native.w4a16_forward_rmsnorm(
+        activations.data_ptr(), norm_weight.data_ptr(), float(eps), packets.data_ptr(),
+        output.data_ptr(), ws_ptr, ws_bytes, batch, n, k, group_size, code, act, requested,
+        _current_stream_ptr(activations.device),
+    )
+    return output
+
+
+def arc_w4a16_forward_silu_mul(
+    activations: torch.Tensor,
+    packets: torch.Tensor,
+    *,
+    n: int,
+    k: int,
+    group_size: int,
+    packet_format: str | int = "native_sym",
+    output: torch.Tensor | None = None,
+    norm_weight: torch.Tensor | None = None,
+    eps: float = 1e-5,
+) -> torch.Tensor:
+    """silu(x . W_gate^T) * (x . W_up^T) in one launch, for native slabs of [W_gate; W_up]
+    stacked along n (n rows in all, n % 256 == 0). Output [batch, n // 2] in the activation
+    dtype; each GEMV result and the SiLU are rounded to it as the unfused pipeline rounds them.
+    With norm_weight, x is first normalised as in arc_w4a16_forward_rmsnorm (a Llama block's input
+    norm, gate_up projection and activation in one launch)."""
+    torch = _require_torch()
+    native = _require_gpu_backend()
+    code = _native_code(packet_format)
+    _check_gpu_tensor(
+        activations, name="activations", dtype=(torch.float16, torch.bfloat16), ndim=2
+    )
+    _check_gpu_tensor(packets, name="packets", dtype=torch.uint8, ndim=2)
+    batch = activations.shape[0]
+    if activations.shape[1] != k:
+        raise ValueError("activations.shape[1] must match k")
+    if n % 256 != 0:
+        raise ValueError("n (gate and up rows together) must be divisible by 256")
+    shape = _packet_shape(n, k, group_size, code)
+    if tuple(packets.shape) != shape:
+        raise ValueError(f"packets must have shape {shape}")
+    if output is None:
+        output = torch.empty((batch, n // 2), device=activations.device, dtype=activations.dtype)
+    else:
+        _check_gpu_tensor(output, name="output", dtype=activations.dtype, ndim=2)
+        if tuple(output.shape) != (batch, n // 2):
+            raise ValueError(f"output must have shape {(batch, n // 2)}")
+    _check_same_device(("activations", activations), ("packets", packets), ("output", output))
+    norm_ptr = 0
+    if norm_weight is not None:
+        _check_gpu_tensor(norm_weight, name="norm_weight", dtype=activations.dtype, ndim=1)
+        if norm_weight.shape[0] != k:
+            raise ValueError("norm_weight.shape[0] must match k")
+        _check_same_device(("activations", activations), ("norm_weight", norm_weight))
+        norm_ptr = norm_weight.data_ptr()
+    native.w4a16_forward_silu_mul(
+        activations.data_ptr(), packets.data_ptr(), output.data_ptr(), batch, n, k, group_size,
+        code, _act_code(activations.dtype), norm_ptr, float(eps),
+        _current_stream_ptr(activations.device),
+    )
+    return output

@@ -173,6 +173,33 @@ int fk_arc_w4a16_forward_native(const void* activations, const void* packets, vo
                                 int group_size, int packet_format, int activation_dtype,
                                 int split_k_slices, void* stream);
 
+/* Fused decode-step neighbours over native slabs (FK_PACKET_NATIVE_SYM / _ASYM); no counterpart
+ * in the reference, whose decode step runs these as separate launches.
+ *
+ * fk_w4a16_forward_rmsnorm: y = x_n . W^T with x_n = round(gamma * round(x * rsqrt(mean(x^2) +
+ * eps))) in the activation dtype (the Llama input RMSNorm of the qkv / gate_up projections,
+ * rounded as an unfused norm kernel writing x_n would round it); norm_weight = gamma [K] in the
+ * activation dtype. Workspace: at least plan.workspace_bytes from fk_w4a16_plan_rmsnorm, with the
+ * contract of fk_arc_w4a16_forward_ex. */
+int fk_w4a16_plan_rmsnorm(int batch, int n, int k, int group_size, int activation_dtype,
+                          int split_k_slices, int cu_count, int packet_format,
+                          fk_arc_w4a16_plan* plan);
+int fk_w4a16_forward_rmsnorm(const void* activations, const void* norm_weight, float eps,
+                             const void* packets, void* output, void* workspace,
+                             size_t workspace_bytes, int batch, int n, int k, int group_size,
+                             int packet_format, int activation_dtype, int split_k_slices,
+                             void* stream);
+
+/* fk_w4a16_forward_silu_mul: the gate_up projection with its activation. The slabs hold
+ * [W_gate; W_up] stacked along n (n % 256 == 0); output [batch, n/2] =
+ * round(round(silu(round(x . W_gate^T))) * round(x . W_up^T)) in the activation dtype, one
+ * launch, no workspace. A non-NULL norm_weight applies the RMSNorm prologue of
+ * fk_w4a16_forward_rmsnorm to x first (a Llama block's norm, gate_up and SiLU in one launch). */
+int fk_w4a16_forward_silu_mul(const void* activations, const void* packets, void* output,
+                              int batch, int n, int k, int group_size, int packet_format,
+                              int activation_dtype, const void* norm_weight, float eps,
+                              void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -232,3 +232,20 @@ def test_native_plan_policy_without_gpu(lib: ctypes.CDLL, shape, want) -> None:
     assert rc == 0 and (arc.slice_cols, arc.workgroups) == (ref.slice_cols, ref.workgroups)
     # a fix-up needs a workspace exactly when runs do not cover whole slices
     assert (p.workspace_bytes > 0) == (p.groups_per_workgroup % (k // g) != 0)
+
+
+def test_fused_entry_points_validate_without_gpu(lib: ctypes.CDLL) -> None:
+    lib.fk_last_error.restype = ctypes.c_char_p
+    f = ctypes.c_float
+    rc = lib.fk_w4a16_forward_rmsnorm(None, None, f(1e-5), None, None, None, 0, 1, 128, 256, 128,
+                                      0, 0, 0, None)
+    assert rc == 1 and b"packet_format" in lib.fk_last_error()
+    rc = lib.fk_w4a16_forward_rmsnorm(None, None, f(1e-5), None, None, None, 0, 1, 128, 256, 128,
+                                      1, 0, 0, None)
+    assert rc == 1 and b"must not be null" in lib.fk_last_error()
+    rc = lib.fk_w4a16_forward_silu_mul(None, None, None, 1, 384, 256, 128, 1, 0, None, f(0.0), None)
+    assert rc == 1 and b"256" in lib.fk_last_error()
+    p = Plan()
+    assert lib.fk_w4a16_plan_rmsnorm(16, 4096, 4096, 128, 0, 0, 256, 1, ctypes.byref(p)) == 0
+    assert (p.m_tile, p.slice_cols) == (8, 32)
+    assert lib.fk_w4a16_plan_rmsnorm(1, 4096, 4096, 128, 0, 0, 256, 0, ctypes.byref(p)) == 1

@@ -1,0 +1,179 @@
+"""GPU tests of the fused decode-step neighbours over native slabs.
+
+Pins:
+  * SiLU-and-multiply: against the unfused pipeline built from this library's own plain forward
+    over the same slabs (run for run the same fp32 sums, so the gate and up halves match bit for
+    bit) followed by torch's SiLU and product in the activation dtype: equal up to one ulp of the
+    output dtype (the exponential of the two SiLUs may differ in its last fp32 bit); and, within
+    the GEMV bar, against the oracle's gate and up GEMVs combined in float64.
+  * RMSNorm prologue: against the unfused pipeline (torch RMSNorm with the Llama rounding, then
+    the plain forward) and against the oracle GEMV of x normalised in float64 then rounded to the
+    activation dtype, within the GEMV bar (rel 1e-2, abs 1e-2 * sqrt(K) * max|alpha|).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import gpu_available
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not gpu_available(), reason="needs a GPU"),
+]
+
+torch = pytest.importorskip("torch")
+
+from fast_kernels.benchmarking.inputs import bf16_bits_to_f32, f16_bits_to_f32, make_case  # noqa: E402
+from fast_kernels.ops import (  # noqa: E402
+    arc_w4a16_forward_native,
+    arc_w4a16_forward_rmsnorm,
+    arc_w4a16_forward_silu_mul,
+    arc_w4a16_plan,
+    convert_arc_to_native_packets,
+    pack_arc_w4a16_packets,
+)
+from oracle import oracle  # noqa: E402
+from test_gpu_w4a16_parity import _assert_gemv_close, _bits, _upload  # noqa: E402
+
+DEV = "cuda"
+
+
+def _slabs(case, asym: bool):
+    x, q, a, b = _upload(case)
+    packets = pack_arc_w4a16_packets(q, a, b, group_size=case.group_size)
+    fmt = "native_asym" if asym else "native_sym"
+    slabs = convert_arc_to_native_packets(packets, n=case.n, k=case.k, group_size=case.group_size,
+                                          packet_format=fmt)
+    return x, slabs, fmt
+
+
+def _to_f32(bits: np.ndarray, act: str) -> np.ndarray:
+    return f16_bits_to_f32(bits) if act == "f16" else bf16_bits_to_f32(bits)
+
+
+def _round_act(v: np.ndarray, act: str) -> np.ndarray:
+    t = torch.from_numpy(np.ascontiguousarray(v, dtype=np.float32))
+    return t.to(torch.float16 if act == "f16" else torch.bfloat16).float().numpy()
+
+
+@pytest.mark.parametrize("act", ["f16", "bf16"])
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 8, 16])
+@pytest.mark.parametrize("group_size,asym", [(128, False), (64, True)])
+def test_silu_mul_matches_unfused_pipeline(act, batch, group_size, asym) -> None:
+    n, k = 1024, 16 * group_size  # gate 512 rows, up 512 rows
+    case = make_case(batch, n, k, group_size, act=act, asymmetric=asym, seed=500 + batch)
+    x, slabs, fmt = _slabs(case, asym)
+    fused = arc_w4a16_forward_silu_mul(x, slabs, n=n, k=k, group_size=group_size,
+                                       packet_format=fmt)
+    y = arc_w4a16_forward_native(x, slabs, n=n, k=k, group_size=group_size, packet_format=fmt,
+                                 split_k_slices=1)
+    g, u = y[:, : n // 2].float(), y[:, n // 2 :].float()
+    ref = (torch.nn.functional.silu(g).to(x.dtype).float() * u).to(x.dtype)
+    torch.cuda.synchronize()
+    got, want = fused.float(), ref.float()
+    if batch < 8:  # from 8 rows the plain forward runs on the matrix cores, a different sum order
+        ulp = 2.0 ** (-10 if act == "f16" else -7)
+        bound = ulp * want.abs() + 1e-6
+        assert bool(((got - want).abs() <= bound).all()), (
+            f"max |fused - unfused| {float((got - want).abs().max()):.4g}"
+        )
+        assert float((got == want).float().mean()) > 0.99
+
+    # the oracle's gate and up GEMVs, combined in float64
+    ref_bits, _ = oracle.gemv(case.x, case.q_u8, case.alpha, case.beta, group_size, act)
+    yo = _to_f32(ref_bits, act).astype(np.float64)
+    go, uo = yo[:, : n // 2], yo[:, n // 2 :]
+    so = _round_act(go / (1.0 + np.exp(-go)), act).astype(np.float64)
+    want_o = so * uo
+    max_alpha = float(f16_bits_to_f32(case.alpha).max())
+    atol = 1e-2 * np.sqrt(k) * max_alpha * (np.abs(uo).max() + np.abs(so).max() + 1.0)
+    err = np.abs(got.cpu().numpy().astype(np.float64) - want_o)
+    assert np.all(err <= atol + 2e-2 * np.abs(want_o)), f"max err {err.max():.4g} atol {atol:.4g}"
+
+
+def _hf_rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """Llama RMSNorm rounding: round(w * round(x * rsqrt(mean(x^2) + eps)))."""
+    xf = x.float()
+    h = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype)
+    return (w.float() * h.float()).to(x.dtype)
+
+
+@pytest.mark.parametrize("act", ["f16", "bf16"])
+@pytest.mark.parametrize("batch", [1, 2, 5, 8, 16])
+@pytest.mark.parametrize("shape,asym", [((1024, 2048, 128), False), ((512, 4096, 64), True),
+                                        ((4096, 14336, 128), False)])
+def test_rmsnorm_matches_unfused_pipeline_and_oracle(act, batch, shape, asym) -> None:
+    n, k, group_size = shape
+    if k > 8192 and batch > 2:
+        pytest.skip("large-K case runs at one and two rows")
+    case = make_case(batch, n, k, group_size, act=act, asymmetric=asym, seed=900 + batch)
+    x, slabs, fmt = _slabs(case, asym)
+    gen = torch.Generator(device="cpu").manual_seed(7 + batch)
+    w = (0.5 + torch.rand(k, generator=gen)).to(x.dtype).to(DEV)
+    eps = 1e-5
+    fused = arc_w4a16_forward_rmsnorm(x, w, slabs, n=n, k=k, group_size=group_size, eps=eps,
+                                      packet_format=fmt)
+    xn = _hf_rmsnorm(x, w, eps)
+    unfused = arc_w4a16_forward_native(xn, slabs, n=n, k=k, group_size=group_size,
+                                       packet_format=fmt)
+    torch.cuda.synchronize()
+    # the normalised activations agree with torch's up to the last bit of a few elements, so the
+    # two results agree within the GEMV bar
+    _assert_gemv_close(_bits(fused), _bits(unfused), case, f"fused vs unfused {shape} M={batch}")
+
+    # oracle: x normalised in float64, rounded as above, then the oracle GEMV
+    xf = _to_f32(case.x, act).astype(np.float64)
+    inv = 1.0 / np.sqrt((xf * xf).mean(axis=1, keepdims=True) + eps)
+    h = _round_act(xf * inv, act).astype(np.float64)
+    xn_np = _round_act(w.float().cpu().numpy().astype(np.float64) * h, act)
+    xn_bits = torch.from_numpy(xn_np).to(x.dtype).view(torch.int16).numpy().view(np.uint16)
+    ref_bits, _ = oracle.gemv(xn_bits, case.q_u8, case.alpha, case.beta, group_size, act)
+    _assert_gemv_close(_bits(fused), ref_bits, case, f"fused vs oracle {shape} M={batch}")
+
+
+def test_rmsnorm_plan_keeps_rows_on_dot2_kernel() -> None:
+    from fast_kernels.native import native_module
+
+    native = native_module()
+    plan = native.w4a16_plan_rmsnorm(16, 4096, 4096, 128, 0, 0, 0, 1)
+    assert plan["m_tile"] == 8 and plan["slice_cols"] == 32
+    assert arc_w4a16_plan(batch=16, n=4096, k=4096, group_size=128, packet_format=1)["m_tile"] == 16
+
+
+def test_fused_ops_reject_reference_packets_and_bad_shapes() -> None:
+    case = make_case(1, 512, 1024, 128, seed=1)
+    x, q, a, b = _upload(case)
+    packets = pack_arc_w4a16_packets(q, a, b, group_size=128)
+    with pytest.raises(ValueError):
+        arc_w4a16_forward_silu_mul(x, packets, n=512, k=1024, group_size=128, packet_format="arc")
+    slabs = convert_arc_to_native_packets(packets, n=512, k=1024, group_size=128)
+    with pytest.raises(ValueError):  # n must cover whole gate and up tiles
+        arc_w4a16_forward_silu_mul(x, slabs, n=384, k=1024, group_size=128)
+    w = torch.ones(1024, device=DEV, dtype=x.dtype)
+    with pytest.raises(ValueError):
+        arc_w4a16_forward_rmsnorm(x, w, slabs, n=512, k=1024, group_size=128, eps=-1.0)
+
+
+@pytest.mark.parametrize("act", ["f16", "bf16"])
+@pytest.mark.parametrize("batch", [1, 2, 4])
+def test_rmsnorm_silu_mul_matches_unfused_pipeline(act, batch) -> None:
+    """A Llama block's norm, gate_up and SiLU in one launch, against torch RMSNorm followed by the
+    fused SiLU-and-multiply without the prologue, and against the oracle."""
+    n, k, g = 2048, 4096, 128
+    case = make_case(batch, n, k, g, act=act, seed=1300 + batch)
+    x, slabs, fmt = _slabs(case, False)
+    gen = torch.Generator(device="cpu").manual_seed(3)
+    w = (0.5 + torch.rand(k, generator=gen)).to(x.dtype).to(DEV)
+    fused = arc_w4a16_forward_silu_mul(x, slabs, n=n, k=k, group_size=g, norm_weight=w, eps=1e-6)
+    xn = _hf_rmsnorm(x, w, 1e-6)
+    unfused = arc_w4a16_forward_silu_mul(xn, slabs, n=n, k=k, group_size=g)
+    torch.cuda.synchronize()
+    got = fused.float().cpu().numpy().astype(np.float64)
+    want = unfused.float().cpu().numpy().astype(np.float64)
+    max_alpha = float(f16_bits_to_f32(case.alpha).max())
+    atol = 1e-2 * np.sqrt(k) * max_alpha * (np.abs(want).max() + 1.0)
+    err = np.abs(got - want)
+    assert np.all(err <= atol + 2e-2 * np.abs(want)), f"max err {err.max():.4g}"
+    assert np.mean(got == want) > 0.9  # the normalised activations rarely differ in a last bit
