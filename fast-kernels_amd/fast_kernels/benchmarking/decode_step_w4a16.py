@@ -7,7 +7,10 @@ step's weights (3.6 GB for the 32-layer 8B stack) exceed every cache, so each re
 from HBM. Reported per suite shape: device microseconds per GEMV (a graph of that projection
 over all layers) and, as the extra shape "decode_step", microseconds per whole step and aggregate
 effective HBM GB/s. When the suite lists the native-slab kernel id, the same stack is converted to
-native symmetric slabs and timed the same way. The torch reference baseline (dequantize + matmul
+native symmetric slabs and timed the same way, and two more shapes time the layers as a Llama block
+chains them (input RMSNorms and the SiLU-and-multiply included): "decode_step_layers_unfused"
+(torch norm and activation kernels between the GEMVs) and "decode_step_layers_fused" (the norm and
+the activation fused into the GEMV launches). The torch reference baseline (dequantize + matmul
 per GEMV) is timed eagerly.
 
 Correctness: after the timed replays, the outputs of the first and the last layer are compared
@@ -77,6 +80,80 @@ def run_decode_step_w4a16_suite(suite: BenchmarkSuite) -> tuple[list[BenchmarkCa
     return cases, notes
 
 
+LAYER_UNFUSED = "decode_step_layers_unfused"
+LAYER_FUSED = "decode_step_layers_fused"
+
+
+def _time_layer_chain(torch: Any, layers: int, dims: dict, slabs: dict, xs: dict, group_size: int,
+                      act_dtype: Any, stream: Any, time_graph: Any) -> dict[str, tuple[float, float]]:
+    """The layers' projections chained as a Llama block runs them (the attention itself and the
+    residual adds aside), over native slabs, in two versions captured as one graph each:
+    unfused (torch RMSNorm before qkv and gate_up, torch SiLU-and-multiply after gate_up) and
+    fused (the RMSNorm prologue of qkv; gate_up with its norm and activation in one launch)."""
+    from fast_kernels.ops import (
+        arc_w4a16_forward_native,
+        arc_w4a16_forward_rmsnorm,
+        arc_w4a16_forward_silu_mul,
+    )
+
+    hidden = dims["qkv"][1]
+    inter = dims["down"][1]
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4242)
+    x = torch.randn((1, hidden), device=dev, generator=gen).to(act_dtype)
+    w_attn = (0.5 + torch.rand(hidden, device=dev, generator=gen)).to(act_dtype)
+    w_ffn = (0.5 + torch.rand(hidden, device=dev, generator=gen)).to(act_dtype)
+    qkv_out = torch.empty((1, dims["qkv"][0]), device=dev, dtype=act_dtype)
+    o_out = torch.empty((1, dims["o"][0]), device=dev, dtype=act_dtype)
+    gu_out = torch.empty((1, dims["gate_up"][0]), device=dev, dtype=act_dtype)
+    act_out = torch.empty((1, inter), device=dev, dtype=act_dtype)
+    down_out = torch.empty((1, dims["down"][0]), device=dev, dtype=act_dtype)
+    o_in = xs[dims["o"][1]]
+
+    def rmsnorm(v: Any, w: Any) -> Any:
+        vf = v.float()
+        h = (vf * torch.rsqrt(vf.pow(2).mean(-1, keepdim=True) + 1e-5)).to(act_dtype)
+        return (w.float() * h.float()).to(act_dtype)
+
+    def proj(v: Any, layer: int, name: str, out: Any) -> None:
+        n, k = dims[name]
+        arc_w4a16_forward_native(v, slabs[(layer, name)], n=n, k=k, group_size=group_size,
+                                 packet_format="native_sym", output=out)
+
+    def unfused() -> None:
+        for layer in range(layers):
+            proj(rmsnorm(x, w_attn), layer, "qkv", qkv_out)
+            proj(o_in, layer, "o", o_out)
+            proj(rmsnorm(x, w_ffn), layer, "gate_up", gu_out)
+            g, u = gu_out[:, :inter].float(), gu_out[:, inter:].float()
+            act_out.copy_((torch.nn.functional.silu(g).to(act_dtype).float() * u).to(act_dtype))
+            proj(act_out, layer, "down", down_out)
+
+    def fused() -> None:
+        for layer in range(layers):
+            n, k = dims["qkv"]
+            arc_w4a16_forward_rmsnorm(x, w_attn, slabs[(layer, "qkv")], n=n, k=k,
+                                      group_size=group_size, eps=1e-5, output=qkv_out)
+            proj(o_in, layer, "o", o_out)
+            n, k = dims["gate_up"]
+            arc_w4a16_forward_silu_mul(x, slabs[(layer, "gate_up")], n=n, k=k,
+                                       group_size=group_size, output=act_out, norm_weight=w_ffn,
+                                       eps=1e-5)
+            proj(act_out, layer, "down", down_out)
+
+    results = {}
+    for name, fn in ((LAYER_UNFUSED, unfused), (LAYER_FUSED, fused)):
+        with torch.cuda.stream(stream):
+            fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            fn()
+        results[name] = time_graph(graph)
+    return results
+
+
 def _run_stack(torch: Any, suite: BenchmarkSuite, dtype: str, layout: str, layers: int) -> list[BenchmarkCase]:
     from fast_kernels.ops import (
         arc_w4a16_forward,
@@ -97,6 +174,7 @@ def _run_stack(torch: Any, suite: BenchmarkSuite, dtype: str, layout: str, layer
     atol, rtol = suite.tolerances.atol, suite.tolerances.rtol
     shapes = [(s.name, s.require_dimension("n"), s.require_dimension("k"), s.dimensions())
               for s in suite.shapes]
+    layer_results: dict[str, tuple[float, float]] = {}
     registry = kernel_registry()
     native_id = next((kid for kid in suite.kernels.ids if registry[kid].impl == "native"), None)
     slabs: dict[tuple[int, str], Any] = {}
@@ -190,6 +268,10 @@ def _run_stack(torch: Any, suite: BenchmarkSuite, dtype: str, layout: str, layer
                                               _max_err(outs[(layer, name)], ref))
             for name in all_names:
                 native_results[name] = time_graph(graph_for([name], native=True))
+            dims = {name: (n, k) for name, n, k, _ in shapes}
+            if {"qkv", "o", "gate_up", "down"} <= set(dims) and dims["down"][1] * 2 == dims["gate_up"][0]:
+                layer_results = _time_layer_chain(torch, layers, dims, slabs, xs, group_size,
+                                                  act_dtype, stream, time_graph)
     except Exception as exc:  # noqa: BLE001 - reported as failed cases
         return [c.model_copy(update={"status": "failed", "reason": str(exc)})
                 for c in _all(suite, "failed", "") if c.dtype == dtype and c.layout == layout]
@@ -226,6 +308,15 @@ def _run_stack(torch: Any, suite: BenchmarkSuite, dtype: str, layout: str, layer
         emit(arc_id, dict(per_shape, **{STEP_SHAPE: (step_med, step_p95)}), errors)
     if native_id is not None:
         emit(native_id, native_results, native_errors)
+        for shape_name, (med, p95) in layer_results.items():
+            cases.append(_case("kernel", native_id, dtype, layout, shape_name,
+                               {"batch": 1, "layers": layers}, "ok",
+                               latency_us_median=med, latency_us_p95=p95,
+                               device_latency_us_median=med, device_latency_us_p95=p95,
+                               throughput=1e6 / med, decode_tokens_per_second=1e6 / med,
+                               metrics={"hbm_gbs": step_bytes / med / 1e3,
+                                        "pct_hbm_peak": 100 * step_bytes / med / 1e3 / PEAK_HBM_GBS,
+                                        "us_per_step": med}))
     timed_ids = {arc_id, native_id}
     for kid in suite.kernels.ids:
         if kid not in timed_ids:
