@@ -13,8 +13,8 @@
 //    four columns 4*(l % (CW/4)) .. +3 of word row l / (CW/4). Narrow slices give small-N shapes
 //    enough workgroups to fill the chip without splitting K across workgroups.
 //  * A wave streams its own groups of the slice through D register buffers of one group each
-//    (D*G*CW/2048 = 16 dwordx4 loads in flight whatever CW), refilling each buffer as soon as
-//    it is consumed.
+//    (16 dwordx4 loads per lane in flight for whole tiles, 8 for narrower slices), refilling
+//    each buffer as soon as it is consumed.
 //  * Register dequant with no per-element conversion: nibbles are OR-ed into fp16 mantissas
 //    (see w4a16_device.h) and multiplied by v_dot2_f32_f16 (fp32 accumulation) against
 //    activations re-paired once per workgroup in LDS. The constant bias the trick adds (1024 for
@@ -58,7 +58,10 @@ struct Slice {
   static constexpr int kRowsPerLoad = 64 / kLanesPerRow;  // word rows per wave-wide load
   static constexpr int kWordRows = G / 8;                 // word rows per group
   static constexpr int kLoads = kWordRows / kRowsPerLoad;  // dwordx4 loads per group and lane
-  static constexpr int kDepth = 16 / kLoads;              // register buffers (groups in flight)
+  // Register buffers (groups in flight per wave): 16 dwordx4 loads per lane for whole tiles,
+  // 8 for 64- and 32-column slices (measured on MI355X: deeper pipelines over narrow slices
+  // lower the achieved bandwidth, as for the native slabs).
+  static constexpr int kDepth = (CW == kTileCols ? 16 : 8) / kLoads;
   static constexpr int kSlices = kTileCols / CW;
   static_assert(kLoads >= 1 && kWordRows % kRowsPerLoad == 0, "unsupported slice");
 };
