@@ -175,24 +175,27 @@ __device__ __forceinline__ uint32_t* slab_word(NativeSlot s, int w) {
   return reinterpret_cast<uint32_t*>(s.slab + native_word_offset(G, s.i, w / U, s.n, w % U));
 }
 
-template <int G>
+template <int G, PacketFormat F>
 __device__ __forceinline__ uint16_t* slab_alpha(NativeSlot s) {
-  return reinterpret_cast<uint16_t*>(s.slab + native_alpha_offset(G)) + 2 * s.n + s.i;
+  return reinterpret_cast<uint16_t*>(s.slab + native_record_offset(G) + native_record_bytes(F) * s.n) +
+         s.i;
 }
 
+// kNativeAsym: the word after the column pair's alphas (zero points in byte 0, three zero bytes).
 template <int G>
-__device__ __forceinline__ uint8_t* slab_zp_byte(NativeSlot s) {
-  return s.slab + native_zp_offset(G) + s.n;
+__device__ __forceinline__ uint32_t* slab_zp_word(NativeSlot s) {
+  return reinterpret_cast<uint32_t*>(s.slab + native_record_offset(G) +
+                                     native_record_bytes(PacketFormat::kNativeAsym) * s.n + 4);
 }
 
-// Writes the zero point of this thread's column. Columns n and n + 16 of a slab share a byte;
-// they are the threads c and c + 16 of one wave.
+// Writes the zero points of this thread's column pair. Columns n and n + 16 of a slab share a
+// byte; they are the threads c and c + 16 of one wave.
 template <int G>
 __device__ __forceinline__ void store_zp_pair(NativeSlot s, uint32_t zp) {
   const int lane = static_cast<int>(threadIdx.x) % 64;
   const uint32_t hi = static_cast<uint32_t>(__shfl(static_cast<int>(zp), min(lane + 16, 63)));
   if (s.i == 0) {
-    *slab_zp_byte<G>(s) = static_cast<uint8_t>((zp & 0xFu) | ((hi & 0xFu) << 4));
+    *slab_zp_word<G>(s) = (zp & 0xFu) | ((hi & 0xFu) << 4);
   }
 }
 
@@ -219,7 +222,7 @@ pack_native_kernel(const uint8_t* __restrict__ q, const uint16_t* __restrict__ a
     *slab_word<G>(s, 4 * v + 2) = d.z;
     *slab_word<G>(s, 4 * v + 3) = d.w;
   }
-  *slab_alpha<G>(s) = alpha[row * num_groups + g];
+  *slab_alpha<G, F>(s) = alpha[row * num_groups + g];
   if constexpr (F == PacketFormat::kNativeAsym) {
     store_zp_pair<G>(s, zero_points[row * num_groups + g]);
   }
@@ -246,7 +249,7 @@ arc_to_native_kernel(const uint8_t* __restrict__ arc, uint8_t* __restrict__ nati
   }
   const uint16_t a_bits = reinterpret_cast<const uint16_t*>(src + QB)[c];
   const uint16_t b_bits = reinterpret_cast<const uint16_t*>(src + QB)[kTileCols + c];
-  *slab_alpha<G>(s) = a_bits;
+  *slab_alpha<G, F>(s) = a_bits;
   int zp = -1;
   if constexpr (F == PacketFormat::kNativeSym) {
     zp = neg_alpha_zp_bits(a_bits, 8) == b_bits ? 8 : -1;
@@ -283,10 +286,10 @@ native_to_arc_kernel(const uint8_t* __restrict__ native, uint8_t* __restrict__ a
   for (int w = 0; w < G / 8; ++w) {
     dw[w * kTileCols + c] = *slab_word<G>(s, w);
   }
-  const uint16_t a_bits = *slab_alpha<G>(s);
+  const uint16_t a_bits = *slab_alpha<G, F>(s);
   uint32_t zp = 8;
   if constexpr (F == PacketFormat::kNativeAsym) {
-    zp = (*slab_zp_byte<G>(s) >> (4 * s.i)) & 0xFu;
+    zp = (*slab_zp_word<G>(s) >> (4 * s.i)) & 0xFu;
   }
   reinterpret_cast<uint16_t*>(dst + QB)[c] = a_bits;
   reinterpret_cast<uint16_t*>(dst + QB)[kTileCols + c] = neg_alpha_zp_bits(a_bits, zp);

@@ -41,9 +41,10 @@ __host__ __device__ constexpr int packet_stride_bytes(int group_size) {
 //    cut into four quarters of U = W/4 consecutive words; lane l = 16*t + n of a wave owns
 //    quarter t of columns n and n + 16. G = 128 (U = 4): the words of column 16*i + n, quarter t
 //    are the 16 bytes at i*1024 + l*16, so each 64-lane dwordx4 load reads 1 KB contiguous.
-//    G = 64 (U = 2): both of the lane's units share the 16 bytes at l*16 (column n first). The
-//    32 alphas follow as pairs (alpha[n], alpha[n + 16]) at 4*n; kNativeAsym adds 16 bytes of zero
-//    points, byte n = zp[n] | zp[n + 16] << 4. The fp16 offsets are not stored: the kernels rebuild
+//    G = 64 (U = 2): both of the lane's units share the 16 bytes at l*16 (column n first). Then
+//    16 records, one per column pair (n, n + 16): the two alphas, and for kNativeAsym the two
+//    zero points in a byte (zp[n] | zp[n + 16] << 4, padded to 8 bytes). The fp16 offsets are
+//    not stored: the kernels rebuild
 //    beta = half_rn(-alpha * zp) exactly (zp = 8 for kNativeSym), the reference recipe's
 //    definition of beta. A lane thus applies each group's scale to two columns, and the same
 //    layout feeds the matrix cores (w4a16_gemm_mfma.hip).
@@ -61,12 +62,16 @@ __host__ __device__ constexpr int native_word_offset(int group_size, int i, int 
                            : (16 * t + n) * 16 + i * 8 + 4 * j;
 }
 
-__host__ __device__ constexpr int native_alpha_offset(int group_size) {
+// The scales (and zero points) of a slab follow its code words as 16 records, record n for
+// columns n and n + 16: kNativeSym 4 bytes (alpha[n], alpha[n + 16]); kNativeAsym 8 bytes (the
+// two alphas, then zp[n] | zp[n + 16] << 4, then three zero bytes), so a lane reads everything
+// its two columns need with one load.
+__host__ __device__ constexpr int native_record_offset(int group_size) {
   return kSliceCols * group_size / 2;
 }
 
-__host__ __device__ constexpr int native_zp_offset(int group_size) {
-  return kSliceCols * group_size / 2 + kSliceCols * 2;
+__host__ __device__ constexpr int native_record_bytes(PacketFormat format) {
+  return format == PacketFormat::kNativeAsym ? 8 : 4;
 }
 
 __host__ __device__ constexpr bool is_native(PacketFormat format) {
@@ -77,8 +82,7 @@ __host__ __device__ constexpr bool is_native(PacketFormat format) {
 __host__ __device__ constexpr int format_packet_stride(int group_size, PacketFormat format) {
   return format == PacketFormat::kArc
              ? packet_stride_bytes(group_size)
-             : kSliceCols * (group_size / 2) + kSliceCols * 2 +
-                   (format == PacketFormat::kNativeAsym ? kSliceCols / 2 : 0);
+             : kSliceCols * (group_size / 2) + 16 * native_record_bytes(format);
 }
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t bits) {

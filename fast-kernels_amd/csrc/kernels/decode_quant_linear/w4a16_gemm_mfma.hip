@@ -150,15 +150,20 @@ __device__ __forceinline__ void mfma_load_group(MfmaGroupLoad<G>& gl, const uint
 #pragma unroll
     for (int s = 0; s < kSlicesPerTile; ++s) {
       const uint8_t* slab = packet + static_cast<size_t>(s) * slice_step;
-      const uint32_t pair = *reinterpret_cast<const uint32_t*>(slab + native_alpha_offset(G) + 4 * (lane % 16));
+      const uint8_t* record = slab + native_record_offset(G) + native_record_bytes(F) * (lane % 16);
+      uint32_t pair = 0;
+      if constexpr (F == PacketFormat::kNativeAsym) {
+        const uint2 r = *reinterpret_cast<const uint2*>(record);
+        pair = r.x;
+        const uint32_t zb = r.y & 0xFFu;
+        gl.beta[s / 2].x = (s % 2 == 0) ? zb : (gl.beta[s / 2].x | (zb << 8));
+      } else {
+        pair = *reinterpret_cast<const uint32_t*>(record);
+      }
       if (s % 2 == 0) {
         gl.alpha[s / 2].x = pair;
       } else {
         gl.alpha[s / 2].y = pair;
-      }
-      if constexpr (F == PacketFormat::kNativeAsym) {
-        const uint32_t zb = *(slab + native_zp_offset(G) + lane % 16);
-        gl.beta[s / 2].x = (s % 2 == 0) ? zb : (gl.beta[s / 2].x | (zb << 8));
       }
       if constexpr (G == 128) {
         gl.w[s / 2][2 * (s % 2)] = *reinterpret_cast<const uint4*>(slab + lane * 16);
@@ -217,6 +222,31 @@ __device__ __forceinline__ void mfma_compute_group(const MfmaSmem<G>& sm, const 
     for (int j = 0; j < U; ++j) {
       a[j] = __builtin_bit_cast(half8_t, sm.xs[gl][U * (lane / 16) + j][lane % 16]);
     }
+    // Offsets of the lane's two columns of each slab: kNativeSym beta = -8 alpha exactly, so
+    // beta - 1024 alpha = -1032 alpha; kNativeAsym beta = half_rn(-alpha * zp) for both columns
+    // with one packed fp16 multiply (fp16 0x6400 | z is 1024 + z, 1024 minus it is -z exactly).
+    float cs[kSlicesPerTile][2];
+    float as[kSlicesPerTile][2];
+#pragma unroll
+    for (int sl = 0; sl < kSlicesPerTile; ++sl) {
+      const uint32_t pair = (sl % 2 == 0) ? ld.alpha[sl / 2].x : ld.alpha[sl / 2].y;
+      uint32_t beta_pair = 0;
+      if constexpr (F == PacketFormat::kNativeAsym) {
+        const uint32_t zp_byte = (ld.beta[sl / 2].x >> (8 * (sl % 2))) & 0xFFu;
+        const uint32_t z = (zp_byte & 0xFu) | ((zp_byte & 0xF0u) << 12);
+        const half2_t neg_z = __builtin_bit_cast(half2_t, 0x64006400u) -
+                              __builtin_bit_cast(half2_t, z | 0x64006400u);
+        beta_pair = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, pair) * neg_z);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        as[sl][i] = half_bits_to_float(static_cast<uint16_t>(pair >> (16 * i)));
+        cs[sl][i] = F == PacketFormat::kNativeAsym
+                        ? fmaf(-1024.0f, as[sl][i],
+                               half_bits_to_float(static_cast<uint16_t>(beta_pair >> (16 * i))))
+                        : -1032.0f * as[sl][i];
+      }
+    }
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk) {
       const int sl = blk / 2;  // slab
@@ -238,17 +268,8 @@ __device__ __forceinline__ void mfma_compute_group(const MfmaSmem<G>& sm, const 
       for (int j = 0; j < U; ++j) {
         d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j], unpack_word(words[j], mask), d, 0, 0, 0);
       }
-      const uint32_t pair = (sl % 2 == 0) ? ld.alpha[sl / 2].x : ld.alpha[sl / 2].y;
-      const float alpha = half_bits_to_float(static_cast<uint16_t>(pair >> (16 * i)));
-      float c = -1032.0f * alpha;  // kNativeSym: beta - 1024 alpha with beta = -8 alpha exactly
-      if constexpr (F == PacketFormat::kNativeAsym) {
-        // beta = half_rn(-alpha * zp): fp16 0x6400 | z is 1024 + z, 1024 - that is -z exactly.
-        const uint32_t zp_byte = (ld.beta[sl / 2].x >> (8 * (sl % 2))) & 0xFFu;
-        const uint32_t z = (zp_byte >> (4 * i)) & 0xFu;
-        const _Float16 neg_z = static_cast<_Float16>(1024.0f) - __builtin_bit_cast(_Float16, static_cast<uint16_t>(z | 0x6400u));
-        const _Float16 beta = __builtin_bit_cast(_Float16, static_cast<uint16_t>(pair >> (16 * i))) * neg_z;
-        c = fmaf(-1024.0f, alpha, static_cast<float>(beta));
-      }
+      const float alpha = as[sl][i];
+      const float c = cs[sl][i];  // beta - 1024 alpha
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         float t = fmaf(alpha, d[r], c * s[r]);

@@ -141,9 +141,13 @@ __device__ __forceinline__ void native_load(NativeLoad<G>& ld, const uint8_t* sl
   for (int v = 0; v < NativeLoad<G>::kVecs; ++v) {
     ld.w[v] = *reinterpret_cast<const uint4*>(slab + v * 1024 + lane * 16);
   }
-  ld.alpha = *reinterpret_cast<const uint32_t*>(slab + native_alpha_offset(G) + 4 * (lane % 16));
+  const uint8_t* record = slab + native_record_offset(G) + native_record_bytes(F) * (lane % 16);
   if constexpr (F == PacketFormat::kNativeAsym) {
-    ld.zp = *(slab + native_zp_offset(G) + lane % 16);
+    const uint2 r = *reinterpret_cast<const uint2*>(record);
+    ld.alpha = r.x;
+    ld.zp = r.y;
+  } else {
+    ld.alpha = *reinterpret_cast<const uint32_t*>(record);
   }
 }
 

@@ -68,9 +68,10 @@ enum ActivationDtype : int { kActivationF16 = 0, kActivationBF16 = 1 };
 
 // Packet formats: the reference's packets (codes, alpha, beta per 128-column tile and group,
 // 64*G + 512 bytes) and the native gfx950 slabs, one per (tile, 32-column slice, group) in
-// [tile][slice][group] order, holding the slice's code words and alpha and, instead of the fp16
-// beta, nothing (symmetric, zero point 8: 16*G + 64 bytes) or 32 int4 zero points (asymmetric:
-// 16*G + 80 bytes). A native buffer is [(N/32) * K/G, slab bytes].
+// [tile][slice][group] order, holding the slice's code words and then 16 column-pair records:
+// the two alphas (symmetric, zero point 8: 16*G + 64 bytes) or the two alphas and the two int4
+// zero points padded to 8 bytes (asymmetric: 16*G + 128 bytes). A native buffer is
+// [(N/32) * K/G, slab bytes].
 enum PacketFormatCode : int { kPacketArc = 0, kPacketNativeSym = 1, kPacketNativeAsym = 2 };
 
 struct ArcW4A16Plan {

@@ -11,11 +11,13 @@ carry at most 4.
 The native formats store one slab per (tile, 32-column slice, group), in [tile][slice][group]
 order, so the groups of a slice are one contiguous range:
 
-  * code words: G/8 rows of 32 uint32 (the reference's word packing, 8 codes along K per word);
-  * alpha: 32 fp16;
-  * "native_asym" only: 32 int4 zero points (column c in byte c/2, low nibble for even c).
+  * code words: G/8 words per column (the reference's word packing, 8 codes along K per word),
+    in the quarter order the kernels read (four lanes per column, 1 KB per wave-wide load);
+  * 16 records, one per column pair (n, n + 16): the two fp16 alphas and, for "native_asym",
+    the two int4 zero points in one byte (padded to 8 bytes), so one load brings a lane all the
+    scales of its two columns.
 
-"native_sym" (zp = 8) slabs are 16*G + 64 bytes, "native_asym" slabs 16*G + 80; a buffer is
+"native_sym" (zp = 8) slabs are 16*G + 64 bytes, "native_asym" slabs 16*G + 128; a buffer is
 [(N/32) * K/G, slab bytes]. The kernels rebuild beta = half_rn(-alpha * zp) bit for bit, so a
 forward over native slabs returns exactly what the same launch over the reference packets they
 came from returns. Slabs convert both ways on the GPU; converting reference packets whose betas
@@ -64,13 +66,14 @@ def packet_format_code(packet_format: str | int) -> int:
 
 def packet_stride_bytes(group_size: int, packet_format: str | int) -> int:
     """Bytes per reference packet (code words 64*G, alphas 256, betas 256) or native slab (code
-    words 16*G, alphas 64, and for native_asym 16 bytes of zero points)."""
+    words 16*G, then 16 records of 4 bytes (two alphas) or, for native_asym, 8 bytes (two alphas,
+    two zero points, padding))."""
     code = packet_format_code(packet_format)
     if code == PACKET_ARC:
         return arc_packet_stride_bytes(group_size)
     if group_size not in {64, 128}:
         raise ValueError("group_size must be 64 or 128")
-    return 16 * group_size + (64 if code == PACKET_NATIVE_SYM else 80)
+    return 16 * group_size + (64 if code == PACKET_NATIVE_SYM else 128)
 
 
 def _native_code(packet_format: str | int) -> int:

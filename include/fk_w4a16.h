@@ -129,11 +129,16 @@ int fk_arc_w4a16_forward_ex(const void* activations, const void* packets, void* 
  * every 512; and it stores an fp16 beta that int4 quantisation always fixes as
  * half_rn(-alpha * zp). The native formats store one slab per (128-column tile, 32-column slice,
  * group), in [tile][slice][group] order, so the groups of a slice are one contiguous byte range:
- *   code words  G/8 rows of 32 uint32, word w of slice column c at byte (w*32 + c)*4
- *   alpha       32 fp16
- *   zero points (FK_PACKET_NATIVE_ASYM only) 32 int4, column c in byte c/2, even c low nibble
+ *   code words  G/8 words (8 codes along K each) per column, in "quarter" order: column
+ *               16i + n has four quarters of G/32 words; lane 16t + n of a 64-lane wave owns
+ *               quarter t of columns n and n + 16. G = 128: quarter t of column 16i + n is the
+ *               16 bytes at i*1024 + (16t + n)*16; G = 64: both of a lane's units share the
+ *               16 bytes at (16t + n)*16 (column n first).
+ *   records     16, one per column pair (n, n + 16): the two fp16 alphas (4 bytes), and for
+ *               FK_PACKET_NATIVE_ASYM the two zero points in one byte (zp[n] | zp[n + 16] << 4)
+ *               and three zero bytes (8 bytes per record).
  * FK_PACKET_NATIVE_SYM slabs are 16*G + 64 bytes (zp = 8 for every group), FK_PACKET_NATIVE_ASYM
- * slabs 16*G + 80 bytes; a buffer holds (N/32) * (K/G) slabs. (FK_PACKET_ARC is the reference
+ * slabs 16*G + 128 bytes; a buffer holds (N/32) * (K/G) slabs. (FK_PACKET_ARC is the reference
  * layout above, 64*G + 512 bytes per packet.) The forward over native slabs returns, bit for
  * bit, what it returns over the reference packets they were converted from. */
 #define FK_PACKET_ARC 0

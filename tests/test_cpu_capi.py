@@ -177,10 +177,10 @@ def test_pybind_module_mirrors_reference_names() -> None:
 @pytest.mark.parametrize("group_size", [64, 128])
 def test_packet_format_strides(lib: ctypes.CDLL, group_size: int) -> None:
     """Reference packets: codes (64*G) + alpha + beta (256 + 256) per 128 columns; native slabs:
-    codes (16*G) + alpha (64) per 32 columns, plus 32 int4 zero points (16) when asymmetric."""
+    codes (16*G) + 16 records per 32 columns: 4 bytes of alphas, or 8 with the zero points."""
     from fast_kernels.ops import packet_stride_bytes
 
-    want = {0: 64 * group_size + 512, 1: 16 * group_size + 64, 2: 16 * group_size + 80}
+    want = {0: 64 * group_size + 512, 1: 16 * group_size + 64, 2: 16 * group_size + 128}
     for fmt, stride in want.items():
         assert lib.fk_packet_stride_bytes(group_size, fmt) == stride
         assert packet_stride_bytes(group_size, fmt) == stride

@@ -54,8 +54,9 @@ def _native_word_offset(g: int, i: int, t: int, n: int, j: int) -> int:
 def _expected_native(case, asym: bool) -> np.ndarray:
     """Native slabs rearranged from the oracle's reference packets. Slab (tile, slice, group):
     the slice's code words in quarter order (column 16 i + n has G/8 words in four quarters of
-    U = G/32; lane 16 t + n of a wave owns quarter t of columns n and n + 16), then the alphas as
-    pairs (alpha[n], alpha[n + 16]), then (asymmetric) the zero points, byte n = zp[n] | zp[n+16] << 4."""
+    U = G/32; lane 16 t + n of a wave owns quarter t of columns n and n + 16), then 16 records,
+    one per column pair: (alpha[n], alpha[n + 16]) and, asymmetric, zp[n] | zp[n+16] << 4 and
+    three zero bytes."""
     g = case.group_size
     ng = case.k // g
     tiles = case.n // 128
@@ -63,7 +64,8 @@ def _expected_native(case, asym: bool) -> np.ndarray:
     ref = oracle.pack_packets(case.q_u8, case.alpha, case.beta, g).reshape(tiles, ng, -1)
     words = ref[:, :, : 64 * g].copy().view(np.uint32).reshape(tiles, ng, g // 8, 128)
     alpha = ref[:, :, 64 * g : 64 * g + 256].copy().view(np.uint16).reshape(tiles, ng, 128)
-    stride = 16 * g + 64 + (16 if asym else 0)
+    rec = 8 if asym else 4
+    stride = 16 * g + 16 * rec
     out = np.zeros((tiles, 4, ng, stride), dtype=np.uint8)
     codes = np.zeros((tiles, 4, ng, 4 * g), dtype=np.uint32)  # 16 g bytes per slab
     for i in range(2):
@@ -74,14 +76,16 @@ def _expected_native(case, asym: bool) -> np.ndarray:
                     col = np.arange(4) * 32 + 16 * i + n  # this column in each of the 4 slices
                     codes[:, :, :, dst] = words[:, :, t * u + j, col].transpose(0, 2, 1)
     out[..., : 16 * g] = codes.view(np.uint8).reshape(tiles, 4, ng, 16 * g)
-    pairs = np.zeros((tiles, 4, ng, 32), dtype=np.uint16)
+    records = np.zeros((tiles, 4, ng, 16, rec), dtype=np.uint8)
     for i in range(2):
-        for n in range(16):
-            pairs[..., 2 * n + i] = alpha[:, :, np.arange(4) * 32 + 16 * i + n].transpose(0, 2, 1)
-    out[..., 16 * g : 16 * g + 64] = pairs.view(np.uint8).reshape(tiles, 4, ng, 64)
+        col = np.arange(4)[:, None] * 32 + 16 * i + np.arange(16)[None, :]  # [slice, n]
+        a = alpha[:, :, col].transpose(0, 2, 1, 3)  # [t, s, g, n]
+        records[..., 2 * i] = (a & 0xFF).astype(np.uint8)
+        records[..., 2 * i + 1] = (a >> 8).astype(np.uint8)
     if asym:
         zp = case.zero_points.reshape(tiles, 4, 32, ng).transpose(0, 1, 3, 2)  # [t, s, g, col]
-        out[..., 16 * g + 64 :] = (zp[..., :16] | (zp[..., 16:] << 4)).astype(np.uint8)
+        records[..., 4] = (zp[..., :16] | (zp[..., 16:] << 4)).astype(np.uint8)
+    out[..., 16 * g :] = records.reshape(tiles, 4, ng, 16 * rec)
     return out.reshape(tiles * 4 * ng, stride)
 
 
@@ -151,7 +155,7 @@ def _forward_pair(case, asym: bool, **kwargs) -> tuple[np.ndarray, np.ndarray]:
 
 @pytest.mark.parametrize("asym", [False, True])
 @pytest.mark.parametrize("group_size", [64, 128])
-@pytest.mark.parametrize("batch", [1, 2, 3, 4, 8, 16])
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 7, 8, 16, 33])
 @pytest.mark.parametrize("act", ["f16", "bf16"])
 def test_forward_native_matches_reference_packets(asym, group_size, batch, act) -> None:
     case = make_case(batch, 512, 16 * group_size, group_size, act=act, asymmetric=asym,
