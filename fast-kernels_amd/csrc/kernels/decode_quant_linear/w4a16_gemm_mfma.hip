@@ -62,6 +62,7 @@ struct MfmaStage {
   static constexpr int kUnits = MfmaSmem<G>::kChunk * (G / 8) * kRows;
   static constexpr int kPerThread = kUnits / kThreads;
   uint4 raw[kPerThread];
+  bool ok[kPerThread];  // the unit lies inside the chunk and the batch (else it stages zeros)
 };
 
 // Unit u = ((row * kChunk) + gl) * WR + w: word rows of one (row, group) are consecutive, so the
@@ -78,11 +79,12 @@ __device__ __forceinline__ void mfma_stage_load(MfmaStage<G>& st, const MfmaPara
     const int w = u % WR;
     const int gl = (u / WR) % kChunk;
     const int r = u / (WR * kChunk);
-    st.raw[it] = make_uint4(0u, 0u, 0u, 0u);
-    if (gl < n_chunk && row0 + r < p.M) {
-      st.raw[it] = *reinterpret_cast<const uint4*>(
-          p.x + static_cast<size_t>(row0 + r) * p.K + static_cast<size_t>(g0 + gl) * G + w * 8);
-    }
+    // unconditional loads from clamped addresses (a branch per load serialises them); units
+    // outside the chunk or the batch are zeroed in mfma_stage_store
+    st.ok[it] = gl < n_chunk && row0 + r < p.M;
+    st.raw[it] = *reinterpret_cast<const uint4*>(
+        p.x + static_cast<size_t>(min(row0 + r, p.M - 1)) * p.K +
+        static_cast<size_t>(g0 + min(gl, n_chunk - 1)) * G + w * 8);
   }
 }
 
@@ -97,7 +99,7 @@ __device__ __forceinline__ void mfma_stage_store(MfmaSmem<G>& sm, MfmaStage<G>& 
     const int w = u % WR;
     const int gl = (u / WR) % kChunk;
     const int r = u / (WR * kChunk);
-    uint4 v = st.raw[it];
+    uint4 v = st.ok[it] ? st.raw[it] : make_uint4(0u, 0u, 0u, 0u);
     float undo = 1.0f;
     if constexpr (A == Act::kBF16) {
       const uint32_t e = group_max<WR>(
@@ -367,6 +369,9 @@ __device__ __forceinline__ void mfma_stream_groups(MfmaSmem<G>& sm, const MfmaPa
         mfma_compute_group<G, A, F>(sm, buf[d], wave + (t0 + d) * kWaves, lane, mask, y);
       }
     }
+    // The loads of skipped tail slots are never consumed; retire them here, or the compiler's
+    // wait for their registers lands between the next chunk's first loads and serialises them.
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   }
 }
 

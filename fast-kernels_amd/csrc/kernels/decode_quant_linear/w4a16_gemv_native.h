@@ -29,7 +29,7 @@ constexpr int kCW = kSliceCols;
 
 template <int G, int MT>
 struct NativeSmem {
-  static constexpr int kChunk = chunk_groups<MT, kCW>();
+  static constexpr int kChunk = chunk_groups<G, MT, kCW>();
   static constexpr int kWordRows = G / 8;
   uint4 xs[MT][kChunk][kWordRows];  // re-paired fp16 activations, 16 B per word row
   float2 sums[MT][kChunk][4];       // offset terms per quarter of the group (native_stage_store)
@@ -50,18 +50,18 @@ template <int G, int MT>
 __device__ __forceinline__ void norm_stage_load(NormRegs<G, MT>& nr, const GemvParams& p, int g0,
                                                 int n_chunk) {
   constexpr int WR = G / 8;
-  constexpr int kChunk = chunk_groups<MT, kSliceCols>();
+  constexpr int kChunk = chunk_groups<G, MT, kSliceCols>();
   const int tid = static_cast<int>(threadIdx.x);
 #pragma unroll
   for (int it = 0; it < StageRegs<G, MT, kSliceCols>::kPerThread; ++it) {
     const int u = it * kThreads + tid;
     const int w = u % WR;
     const int gl = (u / WR) % kChunk;
-    nr.raw[it] = make_uint4(0u, 0u, 0u, 0u);
-    if (u < StageRegs<G, MT, kSliceCols>::kUnits && gl < n_chunk) {
-      nr.raw[it] = *reinterpret_cast<const uint4*>(
-          p.norm_weight + static_cast<size_t>(g0 + gl) * G + static_cast<size_t>(w) * 8);
-    }
+    // clamped and unconditional like stage_load; the staged x of a unit outside the chunk is
+    // zero, and so is its normalised value
+    nr.raw[it] = *reinterpret_cast<const uint4*>(
+        p.norm_weight + static_cast<size_t>(g0 + min(gl, n_chunk - 1)) * G +
+        static_cast<size_t>(w) * 8);
   }
 }
 
@@ -179,7 +179,7 @@ __device__ __forceinline__ void native_stage_store(NativeSmem<G, MT>& sm, StageR
     const int w = u % WR;
     const int gl = (u / WR) % kChunk;
     const int m = u / (WR * kChunk);
-    uint4 r = st.raw[it];
+    uint4 r = st.unit(it);
     if constexpr (kNorm) {
       const float inv = sm.inv_rms[m < MT ? m : 0];
       const uint4 gw = nr.raw[it];
@@ -354,6 +354,9 @@ __device__ __forceinline__ void native_stream_groups(NativeSmem<G, MT>& sm, cons
                                           mask_hi, y);
       }
     }
+    // The loads of skipped tail slots are never consumed; retire them here, or the compiler's
+    // wait for their registers lands between the next chunk's first loads and serialises them.
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   }
 }
 
@@ -406,6 +409,8 @@ w4a16_gemv_native_kernel(GemvParams p) {
   const uint32_t mask_hi = vgpr_constant(0x00f000f0u);
   const size_t stride = static_cast<size_t>(format_packet_stride(G, F));
   const int grid = static_cast<int>(gridDim.x);
+  if constexpr (kNorm) {
+    }
   int b = static_cast<int>(blockIdx.x);
   if (p.xcd_remap) {
     b = (b & 7) * (grid >> 3) + (b >> 3);
