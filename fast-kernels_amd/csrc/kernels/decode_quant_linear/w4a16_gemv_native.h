@@ -11,11 +11,13 @@
 //    n and n + 16. Per group it therefore applies scales to two columns, not four, and reads U
 //    16-byte activation vectors per row (broadcast: the 16 lanes of a quarter read the same one).
 //  * The unpack bias and the offsets fold into per-(row, group, quarter) constants formed while
-//    staging, so the epilogue is short. kNativeSym: beta = half_rn(-8 alpha) = -8 alpha exactly,
-//    so y += alpha * (acc_e + acc_o / 16) with acc_e seeded by C = -1032 S_even - 72 S_odd.
-//    kNativeAsym: acc_e is seeded by -1024 S_even - 64 S_odd and
-//    y += alpha * (acc_e + acc_o / 16) + beta * (S_even + S_odd), beta = half_rn(-alpha * zp)
-//    rebuilt from the stored zero point (both columns in one packed fp16 multiply).
+//    staging, so the epilogue is short. The odd-position activations are staged divided by 16,
+//    so the even (1024 + q) and odd (1024 + 16 q) nibble unpacks add into one accumulator:
+//    acc = C + sum (1024 + q) x_e + (64 + q) x_o. kNativeSym: beta = half_rn(-8 alpha) = -8 alpha
+//    exactly, C = -1032 S_even - 72 S_odd and y += alpha * acc. kNativeAsym:
+//    C = -1024 S_even - 64 S_odd and y += alpha * acc + beta * (S_even + S_odd), beta =
+//    half_rn(-alpha * zp) rebuilt from the stored zero point (both columns in one packed fp16
+//    multiply).
 //  * The four quarters of a column are summed across lanes (xor 16, xor 32) once per run, then
 //    across waves in LDS.
 #pragma once
@@ -212,7 +214,14 @@ __device__ __forceinline__ void native_stage_store(NativeSmem<G, MT>& sm, StageR
     se = group_sum<U>(se);
     so = group_sum<U>(so);
     if (u < StageRegs<G, MT, kCW>::kUnits && gl < n_chunk) {
-      sm.xs[m][gl][w] = pair_activations(r);
+      // The odd-position partners (high nibbles, unpacked as 1024 + 16 q) are staged divided by
+      // 16, exact in fp16 (values below 2^-10 become subnormal and keep fewer bits), so both
+      // nibble positions accumulate into one sum: (1024 + q) x_e + (64 + q) x_o.
+      uint4 xp = pair_activations(r);
+      const half2_t sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+      xp.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, xp.y) * sixteenth);
+      xp.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, xp.w) * sixteenth);
+      sm.xs[m][gl][w] = xp;
       if (w % U == 0) {
         // The offset terms of the epilogue divided by alpha, per (row, group, quarter):
         // kNativeSym (beta = -8 alpha): -1032 S_e - 72 S_o; kNativeAsym: -1024 S_e - 64 S_o,
@@ -235,16 +244,21 @@ __device__ __forceinline__ void native_compute_group(const NativeSmem<G, MT>& sm
                                                      float (&y)[MT][2]) {
   constexpr int U = native_unit_words(G);
   constexpr uint32_t kBias = 0x64006400u;  // fp16 1024.0 pair
-  float acc_e[MT][2];
-  float acc_o[MT][2];
+  // One accumulator per (row, column): with the odd activations staged / 16 both nibble
+  // positions add into it. A single row keeps a second one so that the dependent dot2 chains are
+  // interleaved in pairs.
+  constexpr int kAcc = MT == 1 ? 2 : 1;
+  float acc[MT][2][kAcc];
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
-    // The offset term divided by alpha seeds the even accumulator (see native_stage_store).
+    // The offset term divided by alpha seeds the accumulator (see native_stage_store).
     const float seed = sm.sums[m][gl][t].x;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      acc_e[m][i] = seed;
-      acc_o[m][i] = 0.0f;
+      acc[m][i][0] = seed;
+      if constexpr (kAcc == 2) {
+        acc[m][i][kAcc - 1] = 0.0f;
+      }
     }
   }
 #pragma unroll
@@ -264,10 +278,12 @@ __device__ __forceinline__ void native_compute_group(const NativeSmem<G, MT>& sm
       const uint4 xp = sm.xs[m][gl][U * t + j];
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        acc_e[m][i] = dot2<Act::kF16>(e0[i], xp.x, acc_e[m][i]);
-        acc_o[m][i] = dot2<Act::kF16>(o0[i], xp.y, acc_o[m][i]);
-        acc_e[m][i] = dot2<Act::kF16>(e1[i], xp.z, acc_e[m][i]);
-        acc_o[m][i] = dot2<Act::kF16>(o1[i], xp.w, acc_o[m][i]);
+        float& a0 = acc[m][i][0];
+        float& a1 = acc[m][i][kAcc - 1];
+        a0 = dot2<Act::kF16>(e0[i], xp.x, a0);
+        a1 = dot2<Act::kF16>(o0[i], xp.y, a1);
+        a0 = dot2<Act::kF16>(e1[i], xp.z, a0);
+        a1 = dot2<Act::kF16>(o1[i], xp.w, a1);
       }
     }
   }
@@ -286,14 +302,23 @@ __device__ __forceinline__ void native_compute_group(const NativeSmem<G, MT>& sm
     const float b = half_bits_to_float(static_cast<uint16_t>(beta_pair >> (16 * i)));
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-      float t_sum = a * fmaf(0.0625f, acc_o[m][i], acc_e[m][i]);
-      if constexpr (F == PacketFormat::kNativeAsym) {
-        t_sum = fmaf(b, sm.sums[m][gl][t].y, t_sum);
+      float sum = acc[m][i][0];
+      if constexpr (kAcc == 2) {
+        sum += acc[m][i][1];
       }
       if constexpr (A == Act::kBF16) {
-        t_sum *= sm.scale[m][gl];
+        // the staged activations carry a power-of-two scale per (row, group)
+        float t_sum = a * sum;
+        if constexpr (F == PacketFormat::kNativeAsym) {
+          t_sum = fmaf(b, sm.sums[m][gl][t].y, t_sum);
+        }
+        y[m][i] = fmaf(t_sum, sm.scale[m][gl], y[m][i]);
+      } else {
+        y[m][i] = fmaf(a, sum, y[m][i]);
+        if constexpr (F == PacketFormat::kNativeAsym) {
+          y[m][i] = fmaf(b, sm.sums[m][gl][t].y, y[m][i]);
+        }
       }
-      y[m][i] += t_sum;
     }
   }
 }
