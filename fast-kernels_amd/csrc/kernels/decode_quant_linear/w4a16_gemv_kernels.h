@@ -17,9 +17,11 @@
 //    each buffer as soon as it is consumed.
 //  * Register dequant with no per-element conversion: nibbles are OR-ed into fp16 mantissas
 //    (see w4a16_device.h) and multiplied by v_dot2_f32_f16 (fp32 accumulation) against
-//    activations re-paired once per workgroup in LDS. The constant bias the trick adds (1024 for
-//    low nibbles, 1024 + 16x scale for high nibbles) is removed once per group and column with
-//    per-group activation sums: sum((1024 + s*q) x) = 1024*sum(x) + s*sum(q x).
+//    activations re-paired once per workgroup in LDS. High nibbles unpack as 1024 + 16 q, so
+//    their activation partners are staged divided by 16 and both positions add into one fp32
+//    accumulator: sum (1024 + q) x_e + (64 + q) x_o. The constant part is removed by seeding the
+//    accumulator with -1024 S_e - 64 S_o from per-group activation sums, and the group's beta
+//    term is beta * (S_e + S_o).
 //  * bf16 activations are converted to fp16 when staged, after scaling each (row, group) by a
 //    power of two that keeps its largest magnitude inside fp16's range; the scale is re-applied
 //    to the group's fp32 partial. Every bf16 value whose scaled magnitude is >= 2^-17 converts
@@ -87,7 +89,8 @@ struct Smem {
   static constexpr int kWordRows = G / 8;
   static constexpr int kRowsPerLoad = Slice<G, CW>::kRowsPerLoad;
   uint4 xs[MT][kChunk][kWordRows];        // re-paired fp16 activations, 16 B per word row
-  float2 sums[MT][kChunk][kRowsPerLoad];  // {even, odd} sums over word rows r mod kRowsPerLoad
+  // per word-row class r mod kRowsPerLoad: {-1024 S_even - 64 S_odd, S_even + S_odd}
+  float2 sums[MT][kChunk][kRowsPerLoad];
   float scale[MT][kChunk];                // power of two undoing the bf16 staging scale
   float red[kWaves][MT][CW];              // cross-wave reduction
   int last;                               // this workgroup finishes the slice
@@ -204,9 +207,17 @@ __device__ __forceinline__ void stage_store(Smem<G, MT, CW>& sm, StageRegs<G, MT
       }
     }
     if (u < StageRegs<G, MT, CW>::kUnits && gl < n_chunk) {
-      sm.xs[m][gl][w] = pair_activations(r);
+      // Odd-position partners (high nibbles, unpacked as 1024 + 16 q) are staged divided by 16,
+      // exact in fp16 (values below 2^-10 become subnormal and keep fewer bits), so both nibble
+      // positions accumulate into one sum: (1024 + q) x_e + (64 + q) x_o.
+      uint4 xp = pair_activations(r);
+      const half2_t sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+      xp.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, xp.y) * sixteenth);
+      xp.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, xp.w) * sixteenth);
+      sm.xs[m][gl][w] = xp;
       if (w < R) {
-        sm.sums[m][gl][w] = make_float2(se, so);
+        // the unpack bias, which seeds the accumulators, and the sum for the beta term
+        sm.sums[m][gl][w] = make_float2(fmaf(-1024.0f, se, -64.0f * so), se + so);
       }
       if (w == 0) {
         sm.scale[m][gl] = undo;
@@ -254,8 +265,8 @@ __device__ __forceinline__ void load_group(GroupLoad<G, CW, F>& gl, const uint8_
 }
 
 // One group: multiply-accumulate its codes against the staged activations, then apply the
-// group's scales and remove the unpack bias:
-// y += alpha * (acc_e - 1024 S_e) + alpha/16 * (acc_o - 1024 S_o) + beta * (S_e + S_o).
+// group's scales: with the accumulator seeded by the unpack bias C = -1024 S_e - 64 S_o,
+// y += alpha * acc + beta * (S_e + S_o).
 template <int G, Act A, int MT, int CW, PacketFormat F>
 __device__ __forceinline__ void compute_group(const Smem<G, MT, CW>& sm,
                                               const GroupLoad<G, CW, F>& ld, int gl, int sub,
@@ -264,14 +275,19 @@ __device__ __forceinline__ void compute_group(const Smem<G, MT, CW>& sm,
   constexpr int NL = GroupLoad<G, CW, F>::NL;
   constexpr int R = Slice<G, CW>::kRowsPerLoad;
   constexpr uint32_t kBias = 0x64006400u;  // fp16 1024.0 pair
-  float acc_e[MT][4];
-  float acc_o[MT][4];
+  // One accumulator per (row, column); a single row keeps a second one so that its dependent
+  // dot2 chains interleave in pairs.
+  constexpr int kAcc = MT == 1 ? 2 : 1;
+  float acc[MT][4][kAcc];
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
+    const float seed = sm.sums[m][gl][sub].x;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      acc_e[m][j] = 0.0f;
-      acc_o[m][j] = 0.0f;
+      acc[m][j][0] = seed;
+      if constexpr (kAcc == 2) {
+        acc[m][j][kAcc - 1] = 0.0f;
+      }
     }
   }
 
@@ -294,10 +310,12 @@ __device__ __forceinline__ void compute_group(const Smem<G, MT, CW>& sm,
       const uint32_t o1 = (w8 & mask_hi) | kBias;  // k3,k7
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        acc_e[m][j] = dot2<Act::kF16>(e0, xp[m].x, acc_e[m][j]);
-        acc_o[m][j] = dot2<Act::kF16>(o0, xp[m].y, acc_o[m][j]);
-        acc_e[m][j] = dot2<Act::kF16>(e1, xp[m].z, acc_e[m][j]);
-        acc_o[m][j] = dot2<Act::kF16>(o1, xp[m].w, acc_o[m][j]);
+        float& a0 = acc[m][j][0];
+        float& a1 = acc[m][j][kAcc - 1];
+        a0 = dot2<Act::kF16>(e0, xp[m].x, a0);
+        a1 = dot2<Act::kF16>(o0, xp[m].y, a1);
+        a0 = dot2<Act::kF16>(e1, xp[m].z, a0);
+        a1 = dot2<Act::kF16>(o1, xp[m].w, a1);
       }
     }
   }
@@ -310,19 +328,19 @@ __device__ __forceinline__ void compute_group(const Smem<G, MT, CW>& sm,
   for (int j = 0; j < 4; ++j) {
     const float a = half_bits_to_float(a_bits[j]);
     const float b = group_offset<F>(a, b_bits[j], (ld.beta.x >> (4 * j)) & 0xFu);
-    const float a16 = a * 0.0625f;
-    const float ce = fmaf(-1024.0f, a, b);  // beta - 1024 alpha
-    const float co = fmaf(-64.0f, a, b);    // beta - 64 alpha
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-      const float2 s = sm.sums[m][gl][sub];
-      float t = fmaf(a, acc_e[m][j], ce * s.x);
-      t = fmaf(a16, acc_o[m][j], t);
-      t = fmaf(co, s.y, t);
-      if constexpr (A == Act::kBF16) {
-        t *= sm.scale[m][gl];
+      float sum = acc[m][j][0];
+      if constexpr (kAcc == 2) {
+        sum += acc[m][j][1];
       }
-      y[m][j] += t;
+      const float s = sm.sums[m][gl][sub].y;
+      if constexpr (A == Act::kBF16) {
+        // the staged activations carry a power-of-two scale per (row, group)
+        y[m][j] = fmaf(fmaf(b, s, a * sum), sm.scale[m][gl], y[m][j]);
+      } else {
+        y[m][j] = fmaf(b, s, fmaf(a, sum, y[m][j]));
+      }
     }
   }
 }
