@@ -9,11 +9,13 @@
 //    per lane. A wave-wide dwordx4 load gives lane l the words of 4 consecutive columns
 //    (4*(l % 16) + j, j = 0..3) of word row l / 16, so 4 MFMAs (one per j) cover 64 columns x
 //    4 word rows; MFMA j's output column c maps to packet column 4*c + j.
-//  * A code word unpacks into the fp16 values 1024 + q in the k order (0,4)(1,5)(2,6)(3,7),
-//    which is the order the staged activations are paired in, so A and B agree slot by slot.
-//  * The 1024 bias and the group's scale and offset are applied once per (group, row, column):
-//    y += alpha * D + (beta - 1024 alpha) * S, with D the MFMA sum over the group and S the
-//    group's activation sum.
+//  * A code word unpacks into the fp16 values 1024 + q (even k) and 1024 + 16 q (odd k) in the k
+//    order (0,4)(1,5)(2,6)(3,7), one shift and four and-or; the staged activations are paired in
+//    that order with the odd-k values divided by 16, so A and B agree slot by slot.
+//  * Every block's MFMA chain starts from C = -1024 S_e - 64 S_o (S_e, S_o: the group's even- and
+//    odd-k activation sums), which cancels the unpack bias, so the group's scale and offset are
+//    applied once per (group, row, column) as y += alpha * D + beta * (S_e + S_o); kNativeSym
+//    (beta = -8 alpha) also folds -8 (S_e + S_o) into C and is left with y += alpha * D.
 //  * Work split, XCD remap and the cross-workgroup fix-up are those of the GEMV kernel
 //    (stream-K over (tile, group) units, last contributor finishes the tile).
 #include <hip/hip_runtime.h>
@@ -42,7 +44,8 @@ struct MfmaSmem {
   // Paired fp16 activations, row fastest; one spare row per word row staggers the LDS banks of
   // the staging stores (consecutive lanes store consecutive word rows of one activation row).
   uint4 xs[kChunk][kWordRows][kRows + 1];
-  float sums[kChunk][kRows];               // sum of the group's (staged) activations per row
+  // per (group, row) of the staged activations: {-1024 S_even - 64 S_odd, S_even + S_odd}
+  float2 sums[kChunk][kRows];
   float scale[kChunk][kRows];              // power of two undoing the bf16 staging scale
   float red[kWaves][kRows][kTileCols];     // cross-wave reduction
   int last;
@@ -112,18 +115,27 @@ __device__ __forceinline__ void mfma_stage_store(MfmaSmem<G>& sm, MfmaStage<G>& 
       v.z = bf16_pair_to_half_pair(v.z, s);
       v.w = bf16_pair_to_half_pair(v.w, s);
     }
-    float sum = 0.0f;
+    // even k: low halves, odd k: high halves
+    float se = 0.0f;
+    float so = 0.0f;
     const uint32_t words[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      sum += half_bits_to_float(static_cast<uint16_t>(words[q])) +
-             half_bits_to_float(static_cast<uint16_t>(words[q] >> 16));
+      se += half_bits_to_float(static_cast<uint16_t>(words[q]));
+      so += half_bits_to_float(static_cast<uint16_t>(words[q] >> 16));
     }
-    sum = group_sum<WR>(sum);
+    se = group_sum<WR>(se);
+    so = group_sum<WR>(so);
     if (gl < n_chunk) {
-      sm.xs[gl][w][r] = pair_activations(v);
+      // Odd-k partners are staged divided by 16 (exact in fp16; below 2^-10 they become
+      // subnormal and keep fewer bits) to match the high-nibble unpack 1024 + 16 q.
+      uint4 xp = pair_activations(v);
+      const half2_t sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+      xp.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, xp.y) * sixteenth);
+      xp.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, xp.w) * sixteenth);
+      sm.xs[gl][w][r] = xp;
       if (w == 0) {
-        sm.sums[gl][r] = sum;
+        sm.sums[gl][r] = make_float2(fmaf(-1024.0f, se, -64.0f * so), se + so);
         sm.scale[gl][r] = undo;
       }
     }
@@ -189,31 +201,56 @@ __device__ __forceinline__ void mfma_load_group(MfmaGroupLoad<G>& gl, const uint
   }
 }
 
-// Code word -> 8 fp16 values 1024 + q in the slot order (k0,k4)(k1,k5)(k2,k6)(k3,k7).
-__device__ __forceinline__ half8_t unpack_word(uint32_t w, uint32_t mask) {
+// Code word -> 8 fp16 values in the slot order (k0,k4)(k1,k5)(k2,k6)(k3,k7): 1024 + q for even
+// k, 1024 + 16 q for odd k (their activations are staged / 16). One shift, four and-or.
+__device__ __forceinline__ half8_t unpack_word(uint32_t w, uint32_t mask_lo, uint32_t mask_hi) {
   constexpr uint32_t kBias = 0x64006400u;
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const uint32_t w8 = w >> 8;
   u32x4 v;
-  v.x = (w & mask) | kBias;
-  v.y = ((w >> 4) & mask) | kBias;
-  v.z = ((w >> 8) & mask) | kBias;
-  v.w = ((w >> 12) & mask) | kBias;
+  v.x = (w & mask_lo) | kBias;
+  v.y = (w & mask_hi) | kBias;
+  v.z = (w8 & mask_lo) | kBias;
+  v.w = (w8 & mask_hi) | kBias;
   return __builtin_bit_cast(half8_t, v);
 }
 
 template <int G, Act A, PacketFormat F>
 __device__ __forceinline__ void mfma_compute_group(const MfmaSmem<G>& sm, const MfmaGroupLoad<G>& ld,
-                                                   int gl, int lane, uint32_t mask,
-                                                   float (&y)[2][4][4]) {
+                                                   int gl, int lane, uint32_t mask_lo,
+                                                   uint32_t mask_hi, float (&y)[2][4][4]) {
   constexpr int KB = MfmaGroupLoad<G>::KB;
   const int r0 = 4 * (lane / 16);  // output rows r0 .. r0+3 of this lane
-  const float4 s4 = *reinterpret_cast<const float4*>(&sm.sums[gl][r0]);
   float4 sc4 = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
   if constexpr (A == Act::kBF16) {
     sc4 = *reinterpret_cast<const float4*>(&sm.scale[gl][r0]);
   }
-  const float s[4] = {s4.x, s4.y, s4.z, s4.w};
   const float sc[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
+  // Every block's MFMA chain starts from the rows' unpack bias (kNativeSym: and its offset
+  // beta = -8 alpha, i.e. -1032 S_e - 72 S_o), so the epilogue is alpha * D (+ beta * S).
+  float s[4];
+  float4_t seed;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float2 v = sm.sums[gl][r0 + r];
+    s[r] = v.y;
+    seed[r] = F == PacketFormat::kNativeSym ? fmaf(-8.0f, v.y, v.x) : v.x;
+  }
+  // y += sc * (alpha * d + beta * s): the offset term is absent for kNativeSym.
+  auto apply = [&](float& acc, float alpha, float beta, float d, int r) {
+    if constexpr (A == Act::kBF16) {
+      float t = alpha * d;
+      if constexpr (F != PacketFormat::kNativeSym) {
+        t = fmaf(beta, s[r], t);
+      }
+      acc = fmaf(t, sc[r], acc);
+    } else {
+      acc = fmaf(alpha, d, acc);
+      if constexpr (F != PacketFormat::kNativeSym) {
+        acc = fmaf(beta, s[r], acc);
+      }
+    }
+  };
   if constexpr (is_native(F)) {
     // Block (slab s, half i) = columns 32 s + 16 i + (lane % 16); its U MFMAs j multiply the
     // lane's unit word j (k-chunk lane / 16 of the window {j, U + j, 2U + j, 3U + j}) by the
@@ -224,10 +261,10 @@ __device__ __forceinline__ void mfma_compute_group(const MfmaSmem<G>& sm, const 
     for (int j = 0; j < U; ++j) {
       a[j] = __builtin_bit_cast(half8_t, sm.xs[gl][U * (lane / 16) + j][lane % 16]);
     }
-    // Offsets of the lane's two columns of each slab: kNativeSym beta = -8 alpha exactly, so
-    // beta - 1024 alpha = -1032 alpha; kNativeAsym beta = half_rn(-alpha * zp) for both columns
-    // with one packed fp16 multiply (fp16 0x6400 | z is 1024 + z, 1024 minus it is -z exactly).
-    float cs[kSlicesPerTile][2];
+    // Scales of the lane's two columns of each slab; kNativeAsym beta = half_rn(-alpha * zp) for
+    // both columns with one packed fp16 multiply (fp16 0x6400 | z is 1024 + z, 1024 minus it is
+    // -z exactly).
+    float bs[kSlicesPerTile][2];
     float as[kSlicesPerTile][2];
 #pragma unroll
     for (int sl = 0; sl < kSlicesPerTile; ++sl) {
@@ -243,42 +280,47 @@ __device__ __forceinline__ void mfma_compute_group(const MfmaSmem<G>& sm, const 
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         as[sl][i] = half_bits_to_float(static_cast<uint16_t>(pair >> (16 * i)));
-        cs[sl][i] = F == PacketFormat::kNativeAsym
-                        ? fmaf(-1024.0f, as[sl][i],
-                               half_bits_to_float(static_cast<uint16_t>(beta_pair >> (16 * i))))
-                        : -1032.0f * as[sl][i];
+        bs[sl][i] = half_bits_to_float(static_cast<uint16_t>(beta_pair >> (16 * i)));
       }
     }
+    // The MFMA chains of kPass blocks, then their epilogues, so that the matrix core's latency is
+    // not waited out block by block. G = 128 takes four blocks per pass: all eight would need
+    // more than 256 registers and halve the workgroups per CU.
+    constexpr int kPass = G == 64 ? 8 : 4;
 #pragma unroll
-    for (int blk = 0; blk < 8; ++blk) {
-      const int sl = blk / 2;  // slab
-      const int i = blk % 2;   // half of the slab
-      uint32_t words[U];
-      if constexpr (G == 128) {
-        const uint4 v = ld.w[sl / 2][2 * (sl % 2) + i];
-        words[0] = v.x;
-        words[1] = v.y;
-        words[2] = v.z;
-        words[3] = v.w;
-      } else {
-        const uint4 v = ld.w[sl / 2][sl % 2];
-        words[0] = i == 0 ? v.x : v.z;
-        words[1] = i == 0 ? v.y : v.w;
-      }
-      float4_t d = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int b0 = 0; b0 < 8; b0 += kPass) {
+      float4_t d[kPass];
 #pragma unroll
-      for (int j = 0; j < U; ++j) {
-        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j], unpack_word(words[j], mask), d, 0, 0, 0);
-      }
-      const float alpha = as[sl][i];
-      const float c = cs[sl][i];  // beta - 1024 alpha
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float t = fmaf(alpha, d[r], c * s[r]);
-        if constexpr (A == Act::kBF16) {
-          t *= sc[r];
+      for (int bi = 0; bi < kPass; ++bi) {
+        const int blk = b0 + bi;
+        const int sl = blk / 2;  // slab
+        const int i = blk % 2;   // half of the slab
+        uint32_t words[U];
+        if constexpr (G == 128) {
+          const uint4 v = ld.w[sl / 2][2 * (sl % 2) + i];
+          words[0] = v.x;
+          words[1] = v.y;
+          words[2] = v.z;
+          words[3] = v.w;
+        } else {
+          const uint4 v = ld.w[sl / 2][sl % 2];
+          words[0] = i == 0 ? v.x : v.z;
+          words[1] = i == 0 ? v.y : v.w;
         }
-        y[blk / 4][blk % 4][r] += t;
+        d[bi] = seed;
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+          d[bi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              a[j], unpack_word(words[j], mask_lo, mask_hi), d[bi], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int bi = 0; bi < kPass; ++bi) {
+        const int blk = b0 + bi;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          apply(y[blk / 4][blk % 4][r], as[blk / 2][blk % 2], bs[blk / 2][blk % 2], d[bi][r], r);
+        }
       }
     }
     return;
@@ -293,14 +335,15 @@ __device__ __forceinline__ void mfma_compute_group(const MfmaSmem<G>& sm, const 
     float4_t d[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      d[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      d[j] = seed;
     }
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
       const uint32_t words[4] = {ld.w[h][kb].x, ld.w[h][kb].y, ld.w[h][kb].z, ld.w[h][kb].w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        d[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[kb], unpack_word(words[j], mask), d[j], 0, 0, 0);
+        d[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            a[kb], unpack_word(words[j], mask_lo, mask_hi), d[j], 0, 0, 0);
       }
     }
     const uint16_t ab[4] = {static_cast<uint16_t>(ld.alpha[h].x), static_cast<uint16_t>(ld.alpha[h].x >> 16),
@@ -311,14 +354,9 @@ __device__ __forceinline__ void mfma_compute_group(const MfmaSmem<G>& sm, const 
     for (int j = 0; j < 4; ++j) {
       const float alpha = half_bits_to_float(ab[j]);
       const float beta = group_offset<F>(alpha, bb[j], (ld.beta[h].x >> (4 * j)) & 0xFu);
-      const float c = fmaf(-1024.0f, alpha, beta);  // beta - 1024 alpha
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float t = fmaf(alpha, d[j][r], c * s[r]);
-        if constexpr (A == Act::kBF16) {
-          t *= sc[r];
-        }
-        y[h][j][r] += t;
+        apply(y[h][j][r], alpha, beta, d[j][r], r);
       }
     }
   }
@@ -327,7 +365,8 @@ __device__ __forceinline__ void mfma_compute_group(const MfmaSmem<G>& sm, const 
 template <int G, Act A, PacketFormat F>
 __device__ __forceinline__ void mfma_stream_groups(MfmaSmem<G>& sm, const MfmaParams& p,
                                                    const uint8_t* tile_packets, int row0, int g_lo,
-                                                   int g_hi, int lane, int wave, uint32_t mask,
+                                                   int g_hi, int lane, int wave, uint32_t mask_lo,
+                                                   uint32_t mask_hi,
                                                    float (&y)[2][4][4]) {
   constexpr int kChunk = MfmaSmem<G>::kChunk;
   const size_t stride = static_cast<size_t>(format_packet_stride(G, F));
@@ -358,7 +397,8 @@ __device__ __forceinline__ void mfma_stream_groups(MfmaSmem<G>& sm, const MfmaPa
     for (int blk = 0; blk + 1 < n_blocks; ++blk, t0 += 2) {
 #pragma unroll
       for (int d = 0; d < 2; ++d) {
-        mfma_compute_group<G, A, F>(sm, buf[d], wave + (t0 + d) * kWaves, lane, mask, y);
+        mfma_compute_group<G, A, F>(sm, buf[d], wave + (t0 + d) * kWaves, lane, mask_lo, mask_hi,
+                                    y);
         mfma_load_group<G, F>(buf[d], gp + static_cast<size_t>(min(t0 + 2 + d, t_last)) * step,
                               slice_step, lane);
       }
@@ -366,7 +406,8 @@ __device__ __forceinline__ void mfma_stream_groups(MfmaSmem<G>& sm, const MfmaPa
 #pragma unroll
     for (int d = 0; d < 2; ++d) {
       if (t0 + d < n_w) {
-        mfma_compute_group<G, A, F>(sm, buf[d], wave + (t0 + d) * kWaves, lane, mask, y);
+        mfma_compute_group<G, A, F>(sm, buf[d], wave + (t0 + d) * kWaves, lane, mask_lo, mask_hi,
+                                    y);
       }
     }
     // The loads of skipped tail slots are never consumed; retire them here, or the compiler's
@@ -376,13 +417,14 @@ __device__ __forceinline__ void mfma_stream_groups(MfmaSmem<G>& sm, const MfmaPa
 }
 
 template <int G, Act A, PacketFormat F>
-__global__ void __launch_bounds__(kThreads, 1) w4a16_gemm_mfma_kernel(MfmaParams p) {
+__global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_mfma_kernel(MfmaParams p) {
   constexpr int kOut = kRows * kTileCols;
   __shared__ MfmaSmem<G> sm;
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t mask = vgpr_constant(0x000f000fu);
+  const uint32_t mask_lo = vgpr_constant(0x000f000fu);
+  const uint32_t mask_hi = vgpr_constant(0x00f000f0u);
   const size_t stride = static_cast<size_t>(format_packet_stride(G, F));
   const int grid = static_cast<int>(gridDim.x);
   int b = static_cast<int>(blockIdx.x);
@@ -403,7 +445,8 @@ __global__ void __launch_bounds__(kThreads, 1) w4a16_gemm_mfma_kernel(MfmaParams
     float y[2][4][4] = {};
     const uint8_t* tile_packets =
         p.packets + static_cast<size_t>(tile) * (is_native(F) ? kSlicesPerTile : 1) * p.NG * stride;
-    mfma_stream_groups<G, A, F>(sm, p, tile_packets, row0, g_lo, g_hi, lane, wave, mask, y);
+    mfma_stream_groups<G, A, F>(sm, p, tile_packets, row0, g_lo, g_hi, lane, wave, mask_lo,
+                                mask_hi, y);
     if constexpr (is_native(F)) {
       // Lane l holds rows 4*(l/16)+r of column 32*s + 16*i + l%16 in y[s/2][2*(s%2)+i].
 #pragma unroll
