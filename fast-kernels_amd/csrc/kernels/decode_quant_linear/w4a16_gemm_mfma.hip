@@ -437,16 +437,21 @@ __global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_mfma_kernel(MfmaParams
   if (p.xcd_remap) {
     b = (b & 7) * (grid >> 3) + (b >> 3);
   }
-  const long long total_units = static_cast<long long>(p.tiles) * p.mtiles * p.NG;
-  const long long u_begin = static_cast<long long>(b) * p.per;
-  const long long u_end = min(total_units, u_begin + p.per);
-  long long u = u_begin;
+  // 32-bit unit arithmetic (the host keeps the unit count below 2^31): 64-bit divisions put
+  // about 180 instructions ahead of the first weight load.
+  const uint32_t ng = static_cast<uint32_t>(p.NG);
+  const uint32_t total_units = static_cast<uint32_t>(p.tiles) * p.mtiles * p.NG;
+  const uint32_t u_begin = static_cast<uint32_t>(b) * p.per;
+  const uint32_t u_end = min(total_units, u_begin + p.per);
+  uint32_t u = u_begin;
   while (u < u_end) {
-    const int T = static_cast<int>(u / p.NG);
-    const int g_lo = static_cast<int>(u - static_cast<long long>(T) * p.NG);
-    const int g_hi = static_cast<int>(min(static_cast<long long>(p.NG), g_lo + (u_end - u)));
-    const int tile = T % p.tiles;
-    const int row0 = (T / p.tiles) * kRows;
+    const uint32_t Tu = u / ng;
+    const int T = static_cast<int>(Tu);
+    const int g_lo = static_cast<int>(u - Tu * ng);
+    const int g_hi = static_cast<int>(min(ng, g_lo + (u_end - u)));
+    const uint32_t mt = Tu / static_cast<uint32_t>(p.tiles);
+    const int tile = static_cast<int>(Tu - mt * p.tiles);
+    const int row0 = static_cast<int>(mt) * kRows;
     const int col_base = tile * kTileCols;
     float y[2][4][4] = {};
     const uint8_t* tile_packets =
@@ -484,9 +489,9 @@ __global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_mfma_kernel(MfmaParams
       }
       return v;
     };
-    const long long tile_u0 = static_cast<long long>(T) * p.NG;
-    const int first = static_cast<int>(tile_u0 / p.per);
-    const int last = static_cast<int>((tile_u0 + p.NG - 1) / p.per);
+    const uint32_t tile_u0 = Tu * ng;
+    const int first = static_cast<int>(tile_u0 / static_cast<uint32_t>(p.per));
+    const int last = static_cast<int>((tile_u0 + ng - 1) / static_cast<uint32_t>(p.per));
     if (first == last) {
       for (int idx = tid; idx < kOut; idx += kThreads) {
         const int r = idx / kTileCols;

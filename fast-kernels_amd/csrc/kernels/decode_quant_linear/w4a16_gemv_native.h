@@ -440,18 +440,19 @@ w4a16_gemv_native_kernel(GemvParams p) {
   if (p.xcd_remap) {
     b = (b & 7) * (grid >> 3) + (b >> 3);
   }
-  const long long total_units =
-      static_cast<long long>(p.tiles) * kSlicesPerTile * p.mtiles * p.NG;
-  const long long u_begin = static_cast<long long>(b) * p.per;
-  const long long u_end = min(total_units, u_begin + p.per);
-  long long u = u_begin;
+  const uint32_t total_units =
+      static_cast<uint32_t>(p.tiles) * kSlicesPerTile * p.mtiles * p.NG;
+  const uint32_t u_begin = static_cast<uint32_t>(b) * p.per;
+  const uint32_t u_end = min(total_units, u_begin + p.per);
+  uint32_t u = u_begin;
   while (u < u_end) {
-    const int T = static_cast<int>(u / p.NG);
-    const int g_lo = static_cast<int>(u - static_cast<long long>(T) * p.NG);
-    const int g_hi = static_cast<int>(min(static_cast<long long>(p.NG), g_lo + (u_end - u)));
-    const int slice = T % kSlicesPerTile;
-    const int tile = (T / kSlicesPerTile) % p.tiles;
-    const int row0 = (T / (kSlicesPerTile * p.tiles)) * MT;
+    const RunPos r = run_pos(p, u, u_end, kSlicesPerTile);
+    const int T = r.T;
+    const int g_lo = r.g_lo;
+    const int g_hi = r.g_hi;
+    const int slice = r.slice;
+    const int tile = r.tile;
+    const int row0 = r.mtile * MT;
     const uint8_t* slabs =
         p.packets + (static_cast<size_t>(tile) * kSlicesPerTile + slice) * p.NG * stride;
     if constexpr (kNorm) {

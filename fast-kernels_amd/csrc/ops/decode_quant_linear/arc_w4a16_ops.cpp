@@ -309,6 +309,11 @@ void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::u
               fk::PacketFormat format = fk::PacketFormat::kArc,
               fk::GemvFuse fuse = fk::GemvFuse::kNone, std::uintptr_t norm_weight_ptr = 0,
               float eps = 0.0f) {
+  // The kernels index stream-K units (row tile, 32-column slice, group) in 32 bits.
+  const long long units_bound = static_cast<long long>(n / 32) * batch * (k / group_size);
+  if (units_bound >= (1LL << 31)) {
+    throw_invalid("W4A16: batch * (n / 32) * (k / group_size) must stay below 2^31");
+  }
   fk::GemvLaunch l;
   l.x = reinterpret_cast<const void*>(activations_ptr);
   l.packets = reinterpret_cast<const void*>(packets_ptr);
