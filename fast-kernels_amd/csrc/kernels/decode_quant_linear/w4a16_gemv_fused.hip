@@ -52,9 +52,13 @@ w4a16_gemv_silu_mul_kernel(GemvParams p) {
   }
   __syncthreads();
 
+  // When all of K fits one staging chunk, the up half reuses the activations the gate half
+  // staged (normalised, for kNorm) instead of loading and converting them again.
+  const bool one_chunk = p.NG <= NativeSmem<G, MT>::kChunk;
   float z[MT][2] = {};
   native_stream_groups<G, A, MT, F, kNorm>(sm, p, slabs_of(tile + half_tiles), row0, 0, p.NG,
-                                           lane, wave, mask_lo, mask_hi, z);
+                                           lane, wave, mask_lo, mask_hi, z, /*rms_first=*/false,
+                                           /*staged=*/one_chunk);
   native_reduce_run<G, MT>(sm, z, lane, wave);
   const int out_cols = p.N / 2;
   for (int idx = tid; idx < MT * kSliceCols; idx += kThreads) {

@@ -326,12 +326,18 @@ __device__ __forceinline__ void native_compute_group(const NativeSmem<G, MT>& sm
 // Groups [g_lo, g_hi) of one slice: stage the activations of up to kChunk groups in LDS, then
 // each wave streams groups g_lo + wave, g_lo + wave + 4, ... through D register buffers (as the
 // reference-packet kernel's stream_groups).
+//
+// rms_first (kNorm): form the rows' 1 / rms once the first chunk's activation and weight loads
+// are in flight, so the row reduction overlaps their latency instead of preceding it.
+// staged: [g_lo, g_hi) is one chunk whose activations a previous call left in LDS; they are
+// reused as they are (no loads, no staging, no barrier).
 template <int G, Act A, int MT, PacketFormat F, bool kNorm>
 __device__ __forceinline__ void native_stream_groups(NativeSmem<G, MT>& sm, const GemvParams& p,
                                                      const uint8_t* slabs, int row0, int g_lo,
                                                      int g_hi, int lane, int wave,
                                                      uint32_t mask_lo, uint32_t mask_hi,
-                                                     float (&y)[MT][2]) {
+                                                     float (&y)[MT][2], bool rms_first = false,
+                                                     bool staged = false) {
   constexpr int kChunk = NativeSmem<G, MT>::kChunk;
   // 8 KB of weights in flight per wave (4 groups at G = 128, 8 at G = 64): measured on MI355X,
   // deeper pipelines (8 or 16 KB per wave) lower the achieved HBM bandwidth of every decode shape.
@@ -344,10 +350,12 @@ __device__ __forceinline__ void native_stream_groups(NativeSmem<G, MT>& sm, cons
       lds_barrier();  // previous chunk's readers are done with xs / sums
     }
     StageRegs<G, MT, kCW> st;
-    stage_load<G, MT, kCW>(st, p, row0, g0, n_chunk);
     NormRegs<G, MT> nr;
-    if constexpr (kNorm) {
-      norm_stage_load<G, MT>(nr, p, g0, n_chunk);
+    if (!staged) {
+      stage_load<G, MT, kCW>(st, p, row0, g0, n_chunk);
+      if constexpr (kNorm) {
+        norm_stage_load<G, MT>(nr, p, g0, n_chunk);
+      }
     }
     const int n_w = n_chunk > wave ? (n_chunk - wave + kWaves - 1) / kWaves : 0;
     const int t_last = max(n_w - 1, 0);
@@ -359,9 +367,16 @@ __device__ __forceinline__ void native_stream_groups(NativeSmem<G, MT>& sm, cons
     for (int d = 0; d < D; ++d) {
       native_load<G, F>(buf[d], gp + static_cast<size_t>(min(d, t_last)) * step, lane);
     }
+    if constexpr (kNorm) {
+      if (rms_first && g0 == g_lo) {
+        native_row_inv_rms<G, A, MT>(sm, p, row0, lane, wave);
+      }
+    }
     __builtin_amdgcn_sched_barrier(0);  // keep every load above the first use of the activations
-    native_stage_store<G, A, MT, F, kNorm>(sm, st, nr, n_chunk);
-    lds_barrier();
+    if (!staged) {
+      native_stage_store<G, A, MT, F, kNorm>(sm, st, nr, n_chunk);
+      lds_barrier();
+    }
     const int n_blocks = (n_w + D - 1) / D;
     int t0 = 0;
     for (int blk = 0; blk + 1 < n_blocks; ++blk, t0 += D) {
@@ -455,12 +470,9 @@ w4a16_gemv_native_kernel(GemvParams p) {
     const int row0 = r.mtile * MT;
     const uint8_t* slabs =
         p.packets + (static_cast<size_t>(tile) * kSlicesPerTile + slice) * p.NG * stride;
-    if constexpr (kNorm) {
-      native_row_inv_rms<G, A, MT>(sm, p, row0, lane, wave);
-    }
     float y[MT][2] = {};
     native_stream_groups<G, A, MT, F, kNorm>(sm, p, slabs, row0, g_lo, g_hi, lane, wave, mask_lo,
-                                             mask_hi, y);
+                                             mask_hi, y, /*rms_first=*/true);
     native_reduce_run<G, MT>(sm, y, lane, wave);
     finish_run<A, MT, kCW>(p, T, b, row0, tile * kTileCols + slice * kCW, sm.last,
                            [&](int m, int c) { return native_red_sum(sm, m, c); });

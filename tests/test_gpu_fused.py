@@ -93,6 +93,33 @@ def test_silu_mul_matches_unfused_pipeline(act, batch, group_size, asym) -> None
     assert np.all(err <= atol + 2e-2 * np.abs(want_o)), f"max err {err.max():.4g} atol {atol:.4g}"
 
 
+@pytest.mark.parametrize("batch", [1, 3])
+@pytest.mark.parametrize("with_norm", [False, True])
+def test_silu_mul_over_several_staging_chunks(batch, with_norm) -> None:
+    """K = 80 groups: more than one staging chunk, so the up half cannot reuse the activations
+    the gate half staged and restages them; against the unfused pipeline within the GEMV bar."""
+    n, k, g = 1024, 80 * 128, 128
+    case = make_case(batch, n, k, g, act="bf16", seed=1700 + batch)
+    x, slabs, fmt = _slabs(case, False)
+    w = None
+    xin = x
+    if with_norm:
+        gen = torch.Generator(device="cpu").manual_seed(11)
+        w = (0.5 + torch.rand(k, generator=gen)).to(x.dtype).to(DEV)
+        xin = _hf_rmsnorm(x, w, 1e-6)
+    fused = arc_w4a16_forward_silu_mul(x, slabs, n=n, k=k, group_size=g, norm_weight=w, eps=1e-6)
+    y = arc_w4a16_forward_native(xin, slabs, n=n, k=k, group_size=g, packet_format=fmt)
+    gate, up = y[:, : n // 2].float(), y[:, n // 2 :].float()
+    ref = (torch.nn.functional.silu(gate).to(x.dtype).float() * up).to(x.dtype)
+    torch.cuda.synchronize()
+    got = fused.float().cpu().numpy().astype(np.float64)
+    want = ref.float().cpu().numpy().astype(np.float64)
+    max_alpha = float(f16_bits_to_f32(case.alpha).max())
+    atol = 1e-2 * np.sqrt(k) * max_alpha * (np.abs(want).max() + 1.0)
+    err = np.abs(got - want)
+    assert np.all(err <= atol + 2e-2 * np.abs(want)), f"max err {err.max():.4g}"
+
+
 def _hf_rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     """Llama RMSNorm rounding: round(w * round(x * rsqrt(mean(x^2) + eps)))."""
     xf = x.float()
