@@ -163,6 +163,10 @@ fk::PacketFormat to_packet_format(int packet_format, bool allow_arc) {
 
 // Native slabs: shortest K run worth splitting a slice across workgroups.
 constexpr int kMinNativeRunGroups = 32;
+// Long K: one more split of every slice while that keeps at most two workgroups per CU and runs of
+// at least this many groups. Measured on MI355X at 70B down (256 slices x 224 groups): runs of
+// 112 over 512 workgroups take 24.9 us, whole slices 26.6 us; 70B o (64 groups) gets slower.
+constexpr int kMinLongRunGroups = 96;
 
 }  // namespace
 
@@ -241,7 +245,8 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
   // whatever the slice count (more slices than resident workgroups simply run in later rounds).
   // Only when the slices leave at least half the CUs idle and K is long is K split (power of two),
   // keeping runs of at least kMinNativeRunGroups groups, since the fix-up of a split slice costs
-  // about as much as streaming 30 groups.
+  // about as much as streaming 30 groups. With very long K (kMinLongRunGroups) one split more is
+  // taken while it keeps at most two workgroups per CU.
   const int num_groups = k / group_size;
   const long long slices = static_cast<long long>(fk::gemv_tiles(n, batch, plan.m_tile)) * fk::kSlicesPerTile;
   long long per = 0;
@@ -251,6 +256,10 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
   } else {
     long long s_split = 1;
     while (slices * s_split * 2 <= cu_count && num_groups / (s_split * 2) >= kMinNativeRunGroups) {
+      s_split *= 2;
+    }
+    while (slices * s_split * 2 <= 2LL * cu_count &&
+           num_groups / (s_split * 2) >= kMinLongRunGroups) {
       s_split *= 2;
     }
     per = (num_groups + s_split - 1) / s_split;

@@ -214,7 +214,7 @@ def test_native_format_validation_without_gpu(lib: ctypes.CDLL) -> None:
         ((1, 8192, 8192, 128), (32, 64, 256)),      # 256 slices, each over all of K
         ((1, 10240, 8192, 128), (32, 64, 320)),
         ((1, 57344, 8192, 128), (32, 64, 1792)),    # more slices than resident workgroups
-        ((1, 8192, 28672, 128), (32, 224, 256)),
+        ((1, 8192, 28672, 128), (32, 112, 512)),    # long K: two runs of 112, two per CU
         ((1, 4096, 4096, 128), (32, 32, 128)),      # half the CUs idle, but K is short
         ((1, 4096, 14336, 128), (32, 56, 256)),     # 128 slices, 112 groups: two runs of 56
         ((4, 14336, 4096, 64), (32, 64, 448)),      # four rows share a slice's runs
