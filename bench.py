@@ -267,7 +267,8 @@ def measure(torch, native, args, act, g, shapes, packets):
         R = len(b.packets)
         run = make_runner(torch, lambda b=b: [b.launch(native, torch, ws, r) for r in range(R)], R, args.eager)
         reps = max(1, args.per_shape_launches // R)
-        time_events(torch, run, max(1, 20 // R))
+        # warm as long as the timed run: the first shape otherwise pays for the clocks ramping up
+        time_events(torch, run, reps)
         ms = time_events(torch, run, reps)
         us = ms * 1e3 / (reps * R)
         per_shape[b.name] = {
