@@ -39,12 +39,9 @@ w4a16_gemv_silu_mul_kernel(GemvParams p) {
     return p.packets + (static_cast<size_t>(t) * kSlicesPerTile + slice) * p.NG * stride;
   };
 
-  if constexpr (kNorm) {
-    native_row_inv_rms<G, A, MT>(sm, p, row0, lane, wave);
-  }
   float y[MT][2] = {};
   native_stream_groups<G, A, MT, F, kNorm>(sm, p, slabs_of(tile), row0, 0, p.NG, lane, wave,
-                                           mask_lo, mask_hi, y);
+                                           mask_lo, mask_hi, y, /*rms_first=*/true);
   native_reduce_run<G, MT>(sm, y, lane, wave);
   for (int idx = tid; idx < MT * kSliceCols; idx += kThreads) {
     sm.aux[idx / kSliceCols][idx % kSliceCols] =

@@ -82,30 +82,22 @@ __device__ __forceinline__ uint32_t norm_pair(uint32_t xw, uint32_t gw, float in
   return r;
 }
 
-// 1 / sqrt(mean(x^2) + eps) of rows row0 .. row0 + MT - 1 into sm.inv_rms (fp32 sums; every
-// workgroup forms it for its own rows). Uses sm.red; ends with a workgroup barrier.
-template <int G, Act A, int MT>
-__device__ __forceinline__ void native_row_inv_rms(NativeSmem<G, MT>& sm, const GemvParams& p,
-                                                   int row0, int lane, int wave) {
+// Sum of squares of two activations of a word.
+template <Act A>
+__device__ __forceinline__ float sum_sq_word(uint32_t w, float acc) {
+  const float a = act_bits_to_float<A>(static_cast<uint16_t>(w));
+  const float b = act_bits_to_float<A>(static_cast<uint16_t>(w >> 16));
+  return fmaf(b, b, fmaf(a, a, acc));
+}
+
+// Reduces the per-thread sums of squares of rows row0 .. row0 + MT - 1 and writes
+// 1 / sqrt(mean(x^2) + eps) to sm.inv_rms. Uses sm.red; ends with a workgroup barrier.
+template <int G, int MT>
+__device__ __forceinline__ void native_rms_finish(NativeSmem<G, MT>& sm, const GemvParams& p,
+                                                  float (&ss)[MT], int lane, int wave) {
   const int tid = static_cast<int>(threadIdx.x);
-  float ss[MT];
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
-    ss[m] = 0.0f;
-    if (row0 + m < p.M) {
-      const uint16_t* row = p.x + static_cast<size_t>(row0 + m) * p.K;
-      for (int k8 = tid; k8 < p.K / 8; k8 += kThreads) {
-        const uint4 v = *reinterpret_cast<const uint4*>(row + static_cast<size_t>(k8) * 8);
-        const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float a = act_bits_to_float<A>(static_cast<uint16_t>(wv[j]));
-          const float b = act_bits_to_float<A>(static_cast<uint16_t>(wv[j] >> 16));
-          ss[m] = fmaf(a, a, ss[m]);
-          ss[m] = fmaf(b, b, ss[m]);
-        }
-      }
-    }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
       ss[m] += __shfl_xor(ss[m], off);
@@ -127,6 +119,68 @@ __device__ __forceinline__ void native_row_inv_rms(NativeSmem<G, MT>& sm, const 
     sm.inv_rms[tid] = 1.0f / sqrtf(total / static_cast<float>(p.K) + p.eps);
   }
   __syncthreads();
+}
+
+// 1 / sqrt(mean(x^2) + eps) of rows row0 .. row0 + MT - 1 into sm.inv_rms (fp32 sums; every
+// workgroup forms it for its own rows), loading and reducing in one go.
+template <int G, Act A, int MT>
+__device__ __forceinline__ void native_row_inv_rms(NativeSmem<G, MT>& sm, const GemvParams& p,
+                                                   int row0, int lane, int wave) {
+  const int tid = static_cast<int>(threadIdx.x);
+  float ss[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    ss[m] = 0.0f;
+    if (row0 + m < p.M) {
+      const uint16_t* row = p.x + static_cast<size_t>(row0 + m) * p.K;
+      for (int k8 = tid; k8 < p.K / 8; k8 += kThreads) {
+        const uint4 v = *reinterpret_cast<const uint4*>(row + static_cast<size_t>(k8) * 8);
+        ss[m] = sum_sq_word<A>(v.x, ss[m]);
+        ss[m] = sum_sq_word<A>(v.y, ss[m]);
+        ss[m] = sum_sq_word<A>(v.z, ss[m]);
+        ss[m] = sum_sq_word<A>(v.w, ss[m]);
+      }
+    }
+  }
+  native_rms_finish<G, MT>(sm, p, ss, lane, wave);
+}
+
+// One activation row of up to kRmsRegs * kThreads * 8 values held in registers, so that its
+// loads can be issued ahead of the weight loads and its reduction done behind them.
+constexpr int kRmsRegs = 4;
+struct RmsRegs {
+  uint4 v[kRmsRegs];
+};
+
+__device__ __forceinline__ bool rms_fits_registers(const GemvParams& p) {
+  return p.K <= kRmsRegs * kThreads * 8;
+}
+
+__device__ __forceinline__ void rms_preload(RmsRegs& rr, const GemvParams& p, int row) {
+  const int tid = static_cast<int>(threadIdx.x);
+  const uint16_t* x = p.x + static_cast<size_t>(row) * p.K;
+  const int words = p.K / 8;
+#pragma unroll
+  for (int it = 0; it < kRmsRegs; ++it) {
+    const int k8 = min(it * kThreads + tid, words - 1);  // clamped; the excess is masked in use
+    rr.v[it] = *reinterpret_cast<const uint4*>(x + static_cast<size_t>(k8) * 8);
+  }
+}
+
+template <Act A>
+__device__ __forceinline__ float rms_sum(const RmsRegs& rr, const GemvParams& p) {
+  const int tid = static_cast<int>(threadIdx.x);
+  float ss = 0.0f;
+#pragma unroll
+  for (int it = 0; it < kRmsRegs; ++it) {
+    if (it * kThreads + tid < p.K / 8) {
+      ss = sum_sq_word<A>(rr.v[it].x, ss);
+      ss = sum_sq_word<A>(rr.v[it].y, ss);
+      ss = sum_sq_word<A>(rr.v[it].z, ss);
+      ss = sum_sq_word<A>(rr.v[it].w, ss);
+    }
+  }
+  return ss;
 }
 
 template <int G>
@@ -327,8 +381,10 @@ __device__ __forceinline__ void native_compute_group(const NativeSmem<G, MT>& sm
 // each wave streams groups g_lo + wave, g_lo + wave + 4, ... through D register buffers (as the
 // reference-packet kernel's stream_groups).
 //
-// rms_first (kNorm): form the rows' 1 / rms once the first chunk's activation and weight loads
-// are in flight, so the row reduction overlaps their latency instead of preceding it.
+// rms_first (kNorm): form the rows' 1 / rms at the start of the first chunk. One row whose K fits
+// RmsRegs issues the row's loads first and reduces them after the chunk's weight loads are in
+// flight (the in-order load counter then waits for the row alone); otherwise the row is loaded
+// and reduced before any other load.
 // staged: [g_lo, g_hi) is one chunk whose activations a previous call left in LDS; they are
 // reused as they are (no loads, no staging, no barrier).
 template <int G, Act A, int MT, PacketFormat F, bool kNorm>
@@ -349,6 +405,18 @@ __device__ __forceinline__ void native_stream_groups(NativeSmem<G, MT>& sm, cons
     if (g0 != g_lo) {
       lds_barrier();  // previous chunk's readers are done with xs / sums
     }
+    bool rms_late = false;
+    RmsRegs rr;
+    if constexpr (kNorm) {
+      if (rms_first && g0 == g_lo) {
+        if (MT == 1 && rms_fits_registers(p)) {
+          rms_preload(rr, p, row0);
+          rms_late = true;
+        } else {
+          native_row_inv_rms<G, A, MT>(sm, p, row0, lane, wave);
+        }
+      }
+    }
     StageRegs<G, MT, kCW> st;
     NormRegs<G, MT> nr;
     if (!staged) {
@@ -368,8 +436,10 @@ __device__ __forceinline__ void native_stream_groups(NativeSmem<G, MT>& sm, cons
       native_load<G, F>(buf[d], gp + static_cast<size_t>(min(d, t_last)) * step, lane);
     }
     if constexpr (kNorm) {
-      if (rms_first && g0 == g_lo) {
-        native_row_inv_rms<G, A, MT>(sm, p, row0, lane, wave);
+      if (rms_late) {
+        float ss[MT] = {};
+        ss[0] = rms_sum<A>(rr, p);
+        native_rms_finish<G, MT>(sm, p, ss, lane, wave);
       }
     }
     __builtin_amdgcn_sched_barrier(0);  // keep every load above the first use of the activations
