@@ -173,6 +173,9 @@ def test_forward_native_matches_reference_packets(asym, group_size, batch, act) 
         ((1, 10240, 4096, 128), "f16", True),    # 320 slices, two workgroups per CU
         ((1, 4096, 14336, 128), "bf16", False),  # 128 slices, K split in two (fix-up)
         ((1, 57344, 8192, 128), "bf16", False),  # Llama-70B gate_up, four slices per workgroup
+        ((1, 8192, 28672, 128), "bf16", False),  # Llama-70B down: long K, runs of 112 (fix-up)
+        ((3, 1024, 37 * 64, 64), "f16", True),   # odd group count over two 32-group chunks
+        ((2, 2048, 130 * 64, 64), "bf16", False),  # three 64-group chunks, the last of 2 groups
         ((2, 4096, 4096, 64), "f16", True),      # two rows
         ((8, 4096, 4096, 64), "bf16", True),     # eight rows (half-depth pipeline)
         ((16, 4096, 4096, 64), "bf16", True),    # matrix-core tile over four slabs per group
