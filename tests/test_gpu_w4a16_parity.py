@@ -159,6 +159,9 @@ def test_forward_baseline_shapes_match_oracle(shape: tuple[int, int, int, int]) 
         ((1, 4096, 14336, 128), "bf16", False, (32, 56)),  # narrow slices + K split (fix-up)
         ((2, 4096, 4096, 64), "f16", True, (128, 8)),      # two rows: whole tiles, 8 runs per tile
         ((2, 1024, 8192, 64), "bf16", True, (128, 8)),     # two rows, 16 runs per tile
+        ((3, 1024, 37 * 64, 64), "f16", True, (128, 10)),  # odd group count, runs of 10
+        ((2, 2048, 130 * 64, 64), "bf16", False, (128, 9)),  # 130 groups, runs of 9 across chunks
+        ((5, 1024, 4096, 128), "bf16", False, (128, 8)),   # five rows on an 8-row m-tile
     ],
 )
 def test_forward_column_slices_match_oracle(shape, act, asym, want) -> None:
