@@ -203,10 +203,10 @@ PYBIND11_MODULE(_native, m) {
   m.def(
       "arc_w4a16_plan",
       [](int batch, int n, int k, int group_size, int activation_dtype, int split_k_slices,
-         int cu_count, int packet_format) {
+         int cu_count, int packet_format, int kernel) {
         fk_arc_w4a16_plan plan{};
-        check(fk_w4a16_plan_for_format(batch, n, k, group_size, activation_dtype, split_k_slices,
-                                       cu_count, packet_format, &plan));
+        check(fk_w4a16_plan_for_kernel(batch, n, k, group_size, activation_dtype, split_k_slices,
+                                       cu_count, packet_format, kernel, &plan));
         py::dict d;
         d["m_tile"] = plan.m_tile;
         d["workgroups"] = plan.workgroups;
@@ -218,7 +218,8 @@ PYBIND11_MODULE(_native, m) {
       },
       py::arg("batch"), py::arg("n"), py::arg("k"), py::arg("group_size"),
       py::arg("activation_dtype") = FK_ACT_F16, py::arg("split_k_slices") = 0,
-      py::arg("cu_count") = 0, py::arg("packet_format") = FK_PACKET_ARC);
+      py::arg("cu_count") = 0, py::arg("packet_format") = FK_PACKET_ARC,
+      py::arg("kernel") = FK_KERNEL_AUTO);
   m.def(
       "arc_w4a16_forward_ex",
       [](std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::uintptr_t output_ptr,
@@ -302,6 +303,23 @@ PYBIND11_MODULE(_native, m) {
       py::arg("workspace_ptr"), py::arg("workspace_bytes"), py::arg("batch"), py::arg("n"),
       py::arg("k"), py::arg("group_size"), py::arg("packet_format"), py::arg("activation_dtype"),
       py::arg("split_k_slices"), py::arg("stream_ptr"));
+  m.def(
+      "w4a16_forward_kernel",
+      [](std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::uintptr_t output_ptr,
+         std::uintptr_t workspace_ptr, std::size_t workspace_bytes, int batch, int n, int k,
+         int group_size, int packet_format, int activation_dtype, int split_k_slices, int kernel,
+         std::uintptr_t stream_ptr) {
+        call([&] {
+          return fk_w4a16_forward_kernel(cp(activations_ptr), cp(packets_ptr), mp(output_ptr),
+                                         mp(workspace_ptr), workspace_bytes, batch, n, k,
+                                         group_size, packet_format, activation_dtype,
+                                         split_k_slices, kernel, mp(stream_ptr));
+        });
+      },
+      py::arg("activations_ptr"), py::arg("packets_ptr"), py::arg("output_ptr"),
+      py::arg("workspace_ptr"), py::arg("workspace_bytes"), py::arg("batch"), py::arg("n"),
+      py::arg("k"), py::arg("group_size"), py::arg("packet_format"), py::arg("activation_dtype"),
+      py::arg("split_k_slices"), py::arg("kernel"), py::arg("stream_ptr"));
   m.def(
       "w4a16_plan_rmsnorm",
       [](int batch, int n, int k, int group_size, int activation_dtype, int split_k_slices,

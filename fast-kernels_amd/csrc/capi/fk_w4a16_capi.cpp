@@ -219,6 +219,30 @@ int fk_convert_native_to_arc_packets(const void* native_packets, void* arc_packe
   });
 }
 
+int fk_w4a16_plan_for_kernel(int batch, int n, int k, int group_size, int activation_dtype,
+                             int split_k_slices, int cu_count, int packet_format, int kernel,
+                             fk_arc_w4a16_plan* plan) {
+  return guarded([&] {
+    if (plan == nullptr) {
+      throw std::invalid_argument("plan must not be null");
+    }
+    copy_plan(ops::plan_w4a16_for_kernel(batch, n, k, group_size, activation_dtype,
+                                         split_k_slices, cu_count, packet_format, kernel),
+              plan);
+  });
+}
+
+int fk_w4a16_forward_kernel(const void* activations, const void* packets, void* output,
+                            void* workspace, size_t workspace_bytes, int batch, int n, int k,
+                            int group_size, int packet_format, int activation_dtype,
+                            int split_k_slices, int kernel, void* stream) {
+  return guarded([&] {
+    ops::w4a16_forward_kernel(P(activations), P(packets), P(output), P(workspace), workspace_bytes,
+                              batch, n, k, group_size, packet_format, activation_dtype,
+                              split_k_slices, kernel, P(stream));
+  });
+}
+
 int fk_arc_w4a16_forward_native(const void* activations, const void* packets, void* output,
                                 void* workspace, size_t workspace_bytes, int batch, int n, int k,
                                 int group_size, int packet_format, int activation_dtype,

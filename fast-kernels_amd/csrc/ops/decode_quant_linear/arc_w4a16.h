@@ -161,4 +161,19 @@ void arc_w4a16_forward_native(std::uintptr_t activations_ptr, std::uintptr_t pac
                               int packet_format, int activation_dtype, int split_k_slices,
                               std::uintptr_t stream_ptr);
 
+// Kernel choice: the automatic dispatch (dot2 loop below 8 rows, matrix cores from 8), the dot2
+// loop for every batch (m-tiles of at most 8 rows), or the matrix-core kernel for every batch
+// (16-row m-tiles over whole 128-column tiles). The suites time each against the others.
+enum KernelChoice : int { kKernelAuto = 0, kKernelDot2 = 1, kKernelMfma = 2 };
+
+// plan_w4a16_for_format / arc_w4a16_forward_native with a kernel choice.
+ArcW4A16Plan plan_w4a16_for_kernel(int batch, int n, int k, int group_size, int activation_dtype,
+                                   int split_k_slices, int cu_count, int packet_format,
+                                   int kernel);
+void w4a16_forward_kernel(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
+                          std::uintptr_t output_ptr, std::uintptr_t workspace_ptr,
+                          std::size_t workspace_bytes, int batch, int n, int k, int group_size,
+                          int packet_format, int activation_dtype, int split_k_slices, int kernel,
+                          std::uintptr_t stream_ptr);
+
 }  // namespace fast_kernels::decode_quant_linear

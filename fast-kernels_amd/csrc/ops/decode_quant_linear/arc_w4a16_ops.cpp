@@ -170,8 +170,35 @@ constexpr int kMinLongRunGroups = 96;
 
 }  // namespace
 
+namespace {
+
+// Activation rows per m-tile for a kernel choice: the automatic dispatch, the dot2 loop forced
+// (at most 8-row tiles) or the matrix-core kernel forced (16-row tiles).
+int m_tile_for_kernel(int batch, int kernel) {
+  switch (kernel) {
+    case kKernelAuto: return fk::gemv_m_tile_for_batch(batch);
+    case kKernelDot2: return fk::gemv_partials_m_tile_for_batch(batch);
+    case kKernelMfma: return fk::kMfmaRows;
+    default: throw_invalid("kernel must be 0 (automatic), 1 (dot2) or 2 (matrix cores)");
+  }
+}
+
+ArcW4A16Plan plan_arc_impl(int batch, int n, int k, int group_size, int activation_dtype,
+                           int split_k_slices, int cu_count, int m_tile);
+
+}  // namespace
+
 ArcW4A16Plan plan_arc_w4a16_for_cu_count(int batch, int n, int k, int group_size,
                                          int activation_dtype, int split_k_slices, int cu_count) {
+  validate_dimensions(batch, n, k, group_size);
+  return plan_arc_impl(batch, n, k, group_size, activation_dtype, split_k_slices, cu_count,
+                       fk::gemv_m_tile_for_batch(batch));
+}
+
+namespace {
+
+ArcW4A16Plan plan_arc_impl(int batch, int n, int k, int group_size, int activation_dtype,
+                           int split_k_slices, int cu_count, int m_tile) {
   validate_dimensions(batch, n, k, group_size);
   validate_activation_dtype(activation_dtype);
   if (split_k_slices < 0) {
@@ -181,7 +208,7 @@ ArcW4A16Plan plan_arc_w4a16_for_cu_count(int batch, int n, int k, int group_size
     throw_invalid("cu_count must be positive");
   }
   ArcW4A16Plan plan{};
-  plan.m_tile = fk::gemv_m_tile_for_batch(batch);
+  plan.m_tile = m_tile;
   const int num_groups = k / group_size;
   const long long tiles = static_cast<long long>(fk::gemv_tiles(n, batch, plan.m_tile));
   long long slices = 1;
@@ -220,23 +247,17 @@ ArcW4A16Plan plan_arc_w4a16_for_cu_count(int batch, int n, int k, int group_size
   return plan;
 }
 
-namespace {
-
-// plan_w4a16_for_format; dot2_only keeps batches of 8+ rows on the dot2 kernel (m-tiles of at
-// most 8 rows), which the fused kernels need.
+// plan_w4a16_for_format for a kernel choice (kKernelDot2 is what the fused kernels need).
 ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int activation_dtype,
                                   int split_k_slices, int cu_count, int packet_format,
-                                  bool dot2_only) {
+                                  int kernel) {
   const fk::PacketFormat format = to_packet_format(packet_format, true);
   validate_dimensions(batch, n, k, group_size);
   if (cu_count == 0) {
     cu_count = device_cu_count();
   }
-  ArcW4A16Plan plan = plan_arc_w4a16_for_cu_count(batch, n, k, group_size, activation_dtype,
-                                                  split_k_slices, cu_count);
-  if (dot2_only) {
-    plan.m_tile = fk::gemv_partials_m_tile_for_batch(batch);
-  }
+  ArcW4A16Plan plan = plan_arc_impl(batch, n, k, group_size, activation_dtype, split_k_slices,
+                                    cu_count, m_tile_for_kernel(batch, kernel));
   if (format == fk::PacketFormat::kArc || plan.m_tile == fk::kMfmaRows) {
     return plan;  // the matrix-core kernel reads whole tiles in every format
   }
@@ -274,7 +295,14 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
 ArcW4A16Plan plan_w4a16_for_format(int batch, int n, int k, int group_size, int activation_dtype,
                                    int split_k_slices, int cu_count, int packet_format) {
   return plan_for_format_impl(batch, n, k, group_size, activation_dtype, split_k_slices, cu_count,
-                              packet_format, false);
+                              packet_format, kKernelAuto);
+}
+
+ArcW4A16Plan plan_w4a16_for_kernel(int batch, int n, int k, int group_size, int activation_dtype,
+                                   int split_k_slices, int cu_count, int packet_format,
+                                   int kernel) {
+  return plan_for_format_impl(batch, n, k, group_size, activation_dtype, split_k_slices, cu_count,
+                              packet_format, kernel);
 }
 
 namespace {
@@ -622,15 +650,15 @@ void forward_with_format(std::uintptr_t activations_ptr, std::uintptr_t packets_
                          std::uintptr_t output_ptr, std::uintptr_t workspace_ptr,
                          std::size_t workspace_bytes, int batch, int n, int k, int group_size,
                          fk::PacketFormat format, int activation_dtype, int split_k_slices,
-                         std::uintptr_t stream_ptr) {
+                         std::uintptr_t stream_ptr, int kernel = kKernelAuto) {
   validate_activation_dtype(activation_dtype);
   validate_forward_buffers(activations_ptr, packets_ptr, output_ptr);
   if (split_k_slices < 0) {
     throw_invalid("split_k_slices must be >= 0 (0 = automatic)");
   }
   const ArcW4A16Plan plan =
-      plan_w4a16_for_format(batch, n, k, group_size, activation_dtype, split_k_slices,
-                            device_cu_count(), static_cast<int>(format));
+      plan_w4a16_for_kernel(batch, n, k, group_size, activation_dtype, split_k_slices,
+                            device_cu_count(), static_cast<int>(format), kernel);
   if (plan.workspace_bytes > 0) {
     validate_pointer(workspace_ptr, kCounterRegionAlign, "workspace");
     if (workspace_bytes < plan.workspace_bytes) {
@@ -750,6 +778,18 @@ void arc_w4a16_forward_native(std::uintptr_t activations_ptr, std::uintptr_t pac
                       activation_dtype, split_k_slices, stream_ptr);
 }
 
+void w4a16_forward_kernel(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
+                          std::uintptr_t output_ptr, std::uintptr_t workspace_ptr,
+                          std::size_t workspace_bytes, int batch, int n, int k, int group_size,
+                          int packet_format, int activation_dtype, int split_k_slices, int kernel,
+                          std::uintptr_t stream_ptr) {
+  validate_dimensions(batch, n, k, group_size);
+  m_tile_for_kernel(batch, kernel);  // validates the choice before any pointer check
+  forward_with_format(activations_ptr, packets_ptr, output_ptr, workspace_ptr, workspace_bytes,
+                      batch, n, k, group_size, to_packet_format(packet_format, true),
+                      activation_dtype, split_k_slices, stream_ptr, kernel);
+}
+
 void arc_w4a16_forward_rmsnorm(std::uintptr_t activations_ptr, std::uintptr_t norm_weight_ptr,
                                float eps, std::uintptr_t packets_ptr, std::uintptr_t output_ptr,
                                std::uintptr_t workspace_ptr, std::size_t workspace_bytes, int batch,
@@ -786,7 +826,7 @@ ArcW4A16Plan plan_w4a16_rmsnorm(int batch, int n, int k, int group_size, int act
                                 int split_k_slices, int cu_count, int packet_format) {
   to_packet_format(packet_format, false);
   return plan_for_format_impl(batch, n, k, group_size, activation_dtype, split_k_slices, cu_count,
-                              packet_format, true);
+                              packet_format, kKernelDot2);
 }
 
 void arc_w4a16_forward_silu_mul(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,

@@ -227,6 +227,7 @@ def _run_shape(torch: Any, device: Any, suite: BenchmarkSuite, dtype: str, layou
         group_size_for_layout,
         pack_arc_w4a16_packets,
     )
+    from fast_kernels.ops.decode_quant_linear import KERNEL_AUTO, KERNEL_DOT2, KERNEL_MFMA
 
     dims = shape.dimensions()
     name = shape.name
@@ -378,10 +379,12 @@ def _run_shape(torch: Any, device: Any, suite: BenchmarkSuite, dtype: str, layou
             rot = packet_rot
 
         extra = {"max_abs_err": checked.get(kernel_id, float("nan"))}
-        if impl in (None, "scalar", NATIVE_IMPL):
+        if impl in (None, "scalar", "mfma", NATIVE_IMPL):
+            kernel = {"scalar": KERNEL_DOT2, "mfma": KERNEL_MFMA}.get(impl, KERNEL_AUTO)
             plan = arc_w4a16_plan(batch=batch, n=n, k=k, group_size=group_size,
                                   activation_dtype=x.dtype,
-                                  packet_format=PACKET_FORMATS[native_format] if impl == NATIVE_IMPL else 0)
+                                  packet_format=PACKET_FORMATS[native_format] if impl == NATIVE_IMPL else 0,
+                                  kernel=kernel)
             extra.update({f"plan_{key}": float(val) for key, val in plan.items()})
         out.append(timed("kernel", kernel_id, run_kernel, lambda r, f=run_kernel, rot=rot: f(rot[r]), extra))
     if vendor_id is not None and vendor_id in latencies:

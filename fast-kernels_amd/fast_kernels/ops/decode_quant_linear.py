@@ -6,6 +6,9 @@ the gfx950 library (libfk_w4a16.so) through ``fast_kernels._native``; nothing he
 CPU, and every op raises RuntimeError when the extension is missing.
 
 Differences from the reference, by design:
+  * impl "auto" dispatches by batch on the HIP kernels (dot2 loop below 8 rows, matrix cores from
+    8); "scalar" is the dot2 (FMA) loop for every batch and "mfma" (no reference counterpart) the
+    matrix-core kernel for every batch, so the suites can time the two against each other.
   * impl "scalar" is one HIP launch (in-kernel activation sums and split-K fix-up) instead of a
     group-sum prepass plus a GEMV plus an optional reduction; "auto" picks it by a static rule
     rather than timing candidates on the first call (decode_quant_linear.py:442-682), so results
@@ -35,7 +38,14 @@ _ARC_IMPL_AUTO = "auto"
 _ARC_IMPL_SCALAR = "scalar"
 _ARC_IMPL_TC = "tc"
 _ARC_IMPL_WGMMA = "wgmma"
-_ARC_IMPLS = {_ARC_IMPL_AUTO, _ARC_IMPL_SCALAR, _ARC_IMPL_TC, _ARC_IMPL_WGMMA}
+_ARC_IMPL_MFMA = "mfma"
+_ARC_IMPLS = {_ARC_IMPL_AUTO, _ARC_IMPL_SCALAR, _ARC_IMPL_TC, _ARC_IMPL_WGMMA, _ARC_IMPL_MFMA}
+# Kernel choice of the HIP GEMV per impl (FK_KERNEL_* in include/fk_w4a16.h): "auto" dispatches
+# by batch (dot2 loop below 8 rows, matrix cores from 8), "scalar" is the dot2 (FMA) loop for every
+# batch, "mfma" the matrix-core kernel for every batch.
+KERNEL_AUTO, KERNEL_DOT2, KERNEL_MFMA = 0, 1, 2
+_IMPL_KERNEL = {_ARC_IMPL_AUTO: KERNEL_AUTO, _ARC_IMPL_SCALAR: KERNEL_DOT2,
+                _ARC_IMPL_MFMA: KERNEL_MFMA}
 _VENDOR_WORKSPACE_BYTES = 32 * 1024 * 1024
 
 ACT_F16 = 0
@@ -119,8 +129,9 @@ def _device_index(device: Any) -> int:
 
 
 def arc_w4a16_supported_impls(device: Any | None = None) -> tuple[str, ...]:
-    """Implementations available on this build: auto, scalar (HIP GEMV) and tc (hipBLASLt)."""
-    impls = [_ARC_IMPL_AUTO, _ARC_IMPL_SCALAR]
+    """Implementations available on this build: auto, scalar (HIP dot2 GEMV), mfma (HIP
+    matrix-core kernel) and tc (hipBLASLt)."""
+    impls = [_ARC_IMPL_AUTO, _ARC_IMPL_SCALAR, _ARC_IMPL_MFMA]
     if hip_decode_available():
         impls.append(_ARC_IMPL_TC)
     return tuple(impls)
@@ -138,10 +149,9 @@ def _resolve_arc_impl(device: Any, impl: str | None) -> str:
             f"impl={normalized!r} is unsupported on device {device}; "
             f"supported implementations are {sorted(supported)}"
         )
-    if normalized == _ARC_IMPL_AUTO:
-        # The HIP GEMV streams the packed weights once; the vendor path first writes and re-reads
-        # an fp16 copy of the whole weight (4.5x the bytes), so it cannot win at decode batch sizes.
-        normalized = _ARC_IMPL_SCALAR
+    # "auto" stays on the HIP kernels: they stream the packed weights once, while the vendor path
+    # first writes and re-reads an fp16 copy of the whole weight (4.5x the bytes), so it cannot win
+    # at decode batch sizes.
     return normalized
 
 
@@ -155,15 +165,17 @@ def arc_w4a16_plan(
     split_k_slices: int = 0,
     cu_count: int = 0,
     packet_format: int = 0,
+    kernel: int = KERNEL_AUTO,
 ) -> dict[str, int]:
     """Launch plan: m_tile, workgroups, groups_per_workgroup, max_tile_contributors,
     workspace_bytes and slice_cols (columns of a tile per workgroup), for reference packets
-    (packet_format 0) or the native formats (1 symmetric, 2 asymmetric)."""
+    (packet_format 0) or the native formats (1 symmetric, 2 asymmetric), for a kernel choice
+    (KERNEL_AUTO, KERNEL_DOT2, KERNEL_MFMA)."""
     native = native_module()
     return dict(
         native.arc_w4a16_plan(
             batch, n, k, group_size, _act_code(activation_dtype), split_k_slices, cu_count,
-            packet_format,
+            packet_format, kernel,
         )
     )
 
@@ -357,7 +369,7 @@ def arc_w4a16_forward(
     resolved = _resolve_arc_impl(activations.device, impl)
     if split_k_slices is not None and split_k_slices < 1:
         raise ValueError("split_k_slices must be positive")
-    if resolved == _ARC_IMPL_TC and split_k_slices not in {None, 1}:
+    if resolved in (_ARC_IMPL_TC, _ARC_IMPL_MFMA) and split_k_slices not in {None, 1}:
         raise ValueError(f"split_k_slices is only supported by impl={_ARC_IMPL_SCALAR!r}")
     stream_ptr = _current_stream_ptr(activations.device)
 
@@ -414,13 +426,20 @@ def arc_w4a16_forward(
 
     act = _act_code(out_dtype)
     requested = 0 if split_k_slices is None else split_k_slices
-    plan = native.arc_w4a16_plan(batch, n, k, group_size, act, requested, 0)
+    kernel = _IMPL_KERNEL[resolved]
+    plan = native.arc_w4a16_plan(batch, n, k, group_size, act, requested, 0, 0, kernel)
     ws_bytes = int(plan["workspace_bytes"])
     ws_ptr = 0
     if ws_bytes > 0:
         ws = arc_workspace(activations.device, ws_bytes)
         ws_ptr = ws.data_ptr()
         ws_bytes = ws.numel()
+    if kernel != KERNEL_AUTO:
+        native.w4a16_forward_kernel(
+            activations.data_ptr(), packets.data_ptr(), output.data_ptr(), ws_ptr, ws_bytes,
+            batch, n, k, group_size, 0, act, requested, kernel, stream_ptr,
+        )
+        return output
     native.arc_w4a16_forward_ex(
         activations.data_ptr(),
         packets.data_ptr(),

@@ -32,8 +32,9 @@ def kernel_registry() -> dict[str, KernelSpec]:
         KernelSpec(
             "decode/w4a16_linear_scalar",
             "decode_quant_linear",
-            "Stream-K W4A16 GEMV: 128-bit packet loads, in-register nibble dequant, v_dot2 fp32 "
-            "accumulation, in-kernel activation sums and split-K fix-up (gfx950 HIP).",
+            "Stream-K W4A16 GEMV for every batch size: 128-bit packet loads, in-register nibble "
+            "dequant, v_dot2 fp32 accumulation, in-kernel activation sums and split-K fix-up "
+            "(gfx950 HIP).",
             "experimental",
             "scalar",
         ),
@@ -51,6 +52,15 @@ def kernel_registry() -> dict[str, KernelSpec]:
             "Matrix-core path: packet dequant to fp16, then a hipBLASLt fp16 GEMM.",
             "experimental",
             "tc",
+        ),
+        KernelSpec(
+            "decode/w4a16_linear_mfma",
+            "decode_quant_linear",
+            "The matrix-core kernel (v_mfma_f32_16x16x32_f16, 16-row m-tiles over 128-column "
+            "tiles) for every batch size; no reference counterpart (successor of the tensor-core "
+            "ids), timed against decode/w4a16_linear_scalar, the dot2 loop (gfx950 HIP).",
+            "experimental",
+            "mfma",
         ),
         KernelSpec(
             "decode/w4a16_linear_wgmma",

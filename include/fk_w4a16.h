@@ -178,6 +178,27 @@ int fk_arc_w4a16_forward_native(const void* activations, const void* packets, vo
                                 int group_size, int packet_format, int activation_dtype,
                                 int split_k_slices, void* stream);
 
+/* Kernel choice for fk_w4a16_plan_for_kernel / fk_w4a16_forward_kernel. No counterpart in the
+ * reference; they succeed the reference's per-kernel suite ids (decode/w4a16_linear_scalar and the
+ * tensor-core ids), so that the suites can time one kernel against another:
+ *   FK_KERNEL_AUTO  the dispatch of fk_arc_w4a16_forward_native (dot2 loop below 8 activation
+ *                   rows, the matrix-core kernel from 8);
+ *   FK_KERNEL_DOT2  the dot2 loop for every batch (m-tiles of at most 8 rows);
+ *   FK_KERNEL_MFMA  the matrix-core kernel for every batch (16-row m-tiles, 128-column tiles). */
+#define FK_KERNEL_AUTO 0
+#define FK_KERNEL_DOT2 1
+#define FK_KERNEL_MFMA 2
+
+/* fk_w4a16_plan_for_format / fk_arc_w4a16_forward_native with a kernel choice; same workspace
+ * contract (workspace_bytes from fk_w4a16_plan_for_kernel with the same choice). */
+int fk_w4a16_plan_for_kernel(int batch, int n, int k, int group_size, int activation_dtype,
+                             int split_k_slices, int cu_count, int packet_format, int kernel,
+                             fk_arc_w4a16_plan* plan);
+int fk_w4a16_forward_kernel(const void* activations, const void* packets, void* output,
+                            void* workspace, size_t workspace_bytes, int batch, int n, int k,
+                            int group_size, int packet_format, int activation_dtype,
+                            int split_k_slices, int kernel, void* stream);
+
 /* Fused decode-step neighbours over native slabs (FK_PACKET_NATIVE_SYM / _ASYM); no counterpart
  * in the reference, whose decode step runs these as separate launches.
  *

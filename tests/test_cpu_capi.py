@@ -249,3 +249,21 @@ def test_fused_entry_points_validate_without_gpu(lib: ctypes.CDLL) -> None:
     assert lib.fk_w4a16_plan_rmsnorm(16, 4096, 4096, 128, 0, 0, 256, 1, ctypes.byref(p)) == 0
     assert (p.m_tile, p.slice_cols) == (8, 32)
     assert lib.fk_w4a16_plan_rmsnorm(1, 4096, 4096, 128, 0, 0, 256, 0, ctypes.byref(p)) == 1
+
+
+def test_kernel_choice_plans_without_gpu(lib: ctypes.CDLL) -> None:
+    """FK_KERNEL_DOT2 keeps every batch on m-tiles of at most 8 rows, FK_KERNEL_MFMA puts every
+    batch on 16-row tiles over whole 128-column tiles, FK_KERNEL_AUTO is the forward's dispatch;
+    another value is an invalid argument."""
+    lib.fk_last_error.restype = ctypes.c_char_p
+    for batch, kernel, want in [(16, 1, (8, 32)), (2, 2, (16, 128)), (2, 0, (2, 32)),
+                                (16, 0, (16, 128))]:
+        p = Plan()
+        assert lib.fk_w4a16_plan_for_kernel(batch, 14336, 4096, 64, 0, 0, 256, 1, kernel,
+                                            ctypes.byref(p)) == 0
+        assert (p.m_tile, p.slice_cols) == want, (batch, kernel)
+    p = Plan()
+    assert lib.fk_w4a16_plan_for_kernel(2, 14336, 4096, 64, 0, 0, 256, 0, 3, ctypes.byref(p)) == 1
+    assert b"kernel" in lib.fk_last_error()
+    rc = lib.fk_w4a16_forward_kernel(None, None, None, None, 0, 1, 128, 256, 128, 0, 0, 0, 5, None)
+    assert rc == 1 and b"kernel" in lib.fk_last_error()

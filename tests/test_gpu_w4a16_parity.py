@@ -37,6 +37,8 @@ from fast_kernels.ops import (  # noqa: E402
     pack_arc_w4a16_packets,
 )
 from oracle import oracle  # noqa: E402
+from fast_kernels.native import native_module  # noqa: E402
+from fast_kernels.ops.decode_quant_linear import _IMPL_KERNEL  # noqa: E402
 
 DEV = "cuda"
 
@@ -330,6 +332,45 @@ def test_tc_impl_and_env_override(monkeypatch: pytest.MonkeyPatch) -> None:
     _assert_gemv_close(_run_forward(case), ref, case, "env impl=tc")
     monkeypatch.setenv("FK_ARC_W4A16_IMPL", "scalar")
     _assert_gemv_close(_run_forward(case), ref, case, "env impl=scalar")
+
+
+@pytest.mark.parametrize("impl,batch", [("scalar", 8), ("scalar", 16), ("scalar", 33),
+                                        ("mfma", 1), ("mfma", 2), ("mfma", 5), ("mfma", 33)])
+@pytest.mark.parametrize("asym", [False, True])
+def test_forced_kernel_impls_match_oracle(impl: str, batch: int, asym: bool) -> None:
+    """impl "scalar" keeps every batch on the dot2 loop and "mfma" on the matrix-core kernel:
+    both within the GEMV bar of the oracle at the batch sizes the automatic dispatch sends to the
+    other kernel."""
+    case = make_case(batch, 512, 16 * 64, 64, asymmetric=asym, seed=4000 + batch)
+    ref, _ = oracle.gemv(case.x, case.q_u8, case.alpha, case.beta, 64)
+    _assert_gemv_close(_run_forward(case, impl=impl), ref, case, f"impl={impl} M={batch}")
+    want = 16 if impl == "mfma" else min(8, 1 << (batch - 1).bit_length())
+    plan = arc_w4a16_plan(batch=batch, n=512, k=1024, group_size=64, kernel=_IMPL_KERNEL[impl])
+    assert plan["m_tile"] == want
+
+
+@pytest.mark.parametrize("kernel", [1, 2])
+@pytest.mark.parametrize("batch", [3, 8])
+def test_forced_kernels_over_native_slabs(kernel: int, batch: int) -> None:
+    """fk_w4a16_forward_kernel over native asymmetric slabs, both forced kernels."""
+    from fast_kernels.ops import convert_arc_to_native_packets
+
+    case = make_case(batch, 512, 32 * 128, 128, act="bf16", asymmetric=True, seed=77 + batch)
+    x, q, a, b = _upload(case)
+    packets = pack_arc_w4a16_packets(q, a, b, group_size=128)
+    slabs = convert_arc_to_native_packets(packets, n=512, k=4096, group_size=128,
+                                          packet_format="native_asym")
+    native = native_module()
+    plan = arc_w4a16_plan(batch=batch, n=512, k=4096, group_size=128,
+                          activation_dtype=torch.bfloat16, packet_format=2, kernel=kernel)
+    ws = torch.zeros(max(1, plan["workspace_bytes"]) + 256, device=DEV, dtype=torch.uint8)
+    y = torch.empty((batch, 512), device=DEV, dtype=torch.bfloat16)
+    native.w4a16_forward_kernel(x.data_ptr(), slabs.data_ptr(), y.data_ptr(), ws.data_ptr(),
+                                ws.numel(), batch, 512, 4096, 128, 2, 1, 0, kernel,
+                                torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    ref, _ = oracle.gemv(case.x, case.q_u8, case.alpha, case.beta, 128, "bf16")
+    _assert_gemv_close(_bits(y), ref, case, f"native kernel={kernel} M={batch}")
 
 
 def test_forward_respects_current_stream() -> None:
