@@ -181,22 +181,17 @@ __device__ __forceinline__ uint16_t* slab_alpha(NativeSlot s) {
          s.i;
 }
 
-// kNativeAsym: the word after the column pair's alphas (zero points in byte 0, three zero bytes).
+// kNativeAsym: the word after the column pair's alphas (-zp[n] and -zp[n + 16] as fp16).
 template <int G>
 __device__ __forceinline__ uint32_t* slab_zp_word(NativeSlot s) {
   return reinterpret_cast<uint32_t*>(s.slab + native_record_offset(G) +
                                      native_record_bytes(PacketFormat::kNativeAsym) * s.n + 4);
 }
 
-// Writes the zero points of this thread's column pair. Columns n and n + 16 of a slab share a
-// byte; they are the threads c and c + 16 of one wave.
+// Writes -zp of this thread's column (half s.i of the column pair's word).
 template <int G>
-__device__ __forceinline__ void store_zp_pair(NativeSlot s, uint32_t zp) {
-  const int lane = static_cast<int>(threadIdx.x) % 64;
-  const uint32_t hi = static_cast<uint32_t>(__shfl(static_cast<int>(zp), min(lane + 16, 63)));
-  if (s.i == 0) {
-    *slab_zp_word<G>(s) = (zp & 0xFu) | ((hi & 0xFu) << 4);
-  }
+__device__ __forceinline__ void store_neg_zp(NativeSlot s, uint32_t zp) {
+  reinterpret_cast<uint16_t*>(slab_zp_word<G>(s))[s.i] = neg_zp_half_bits(zp & 0xFu);
 }
 
 // Native slabs from q_u8 / alpha / zero points (uint8 [N, NG], values 0..15, unused for
@@ -224,7 +219,7 @@ pack_native_kernel(const uint8_t* __restrict__ q, const uint16_t* __restrict__ a
   }
   *slab_alpha<G, F>(s) = alpha[row * num_groups + g];
   if constexpr (F == PacketFormat::kNativeAsym) {
-    store_zp_pair<G>(s, zero_points[row * num_groups + g]);
+    store_neg_zp<G>(s, zero_points[row * num_groups + g]);
   }
 }
 
@@ -265,7 +260,7 @@ arc_to_native_kernel(const uint8_t* __restrict__ arc, uint8_t* __restrict__ nati
     zp = 0;
   }
   if constexpr (F == PacketFormat::kNativeAsym) {
-    store_zp_pair<G>(s, static_cast<uint32_t>(zp));
+    store_neg_zp<G>(s, static_cast<uint32_t>(zp));
   }
 }
 
@@ -289,7 +284,8 @@ native_to_arc_kernel(const uint8_t* __restrict__ native, uint8_t* __restrict__ a
   const uint16_t a_bits = *slab_alpha<G, F>(s);
   uint32_t zp = 8;
   if constexpr (F == PacketFormat::kNativeAsym) {
-    zp = (*slab_zp_word<G>(s) >> (4 * s.i)) & 0xFu;
+    const uint16_t neg = reinterpret_cast<const uint16_t*>(slab_zp_word<G>(s))[s.i];
+    zp = static_cast<uint32_t>(static_cast<float>(__builtin_bit_cast(_Float16, neg)) * -1.0f);
   }
   reinterpret_cast<uint16_t*>(dst + QB)[c] = a_bits;
   reinterpret_cast<uint16_t*>(dst + QB)[kTileCols + c] = neg_alpha_zp_bits(a_bits, zp);

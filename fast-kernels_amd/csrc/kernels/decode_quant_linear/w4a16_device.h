@@ -43,10 +43,9 @@ __host__ __device__ constexpr int packet_stride_bytes(int group_size) {
 //    are the 16 bytes at i*1024 + l*16, so each 64-lane dwordx4 load reads 1 KB contiguous.
 //    G = 64 (U = 2): both of the lane's units share the 16 bytes at l*16 (column n first). Then
 //    16 records, one per column pair (n, n + 16): the two alphas, and for kNativeAsym the two
-//    zero points in a byte (zp[n] | zp[n + 16] << 4, padded to 8 bytes). The fp16 offsets are
-//    not stored: the kernels rebuild
-//    beta = half_rn(-alpha * zp) exactly (zp = 8 for kNativeSym), the reference recipe's
-//    definition of beta. A lane thus applies each group's scale to two columns, and the same
+//    negated zero points as fp16 (-zp[n], -zp[n + 16]). The fp16 offsets are not stored: the
+//    kernels rebuild beta = half_rn(-alpha * zp) exactly, one packed fp16 multiply for both
+//    columns (zp = 8 for kNativeSym), the reference recipe's definition of beta. A lane thus applies each group's scale to two columns, and the same
 //    layout feeds the matrix cores (w4a16_gemm_mfma.hip).
 enum class PacketFormat : int { kArc = 0, kNativeSym = 1, kNativeAsym = 2 };
 
@@ -64,8 +63,8 @@ __host__ __device__ constexpr int native_word_offset(int group_size, int i, int 
 
 // The scales (and zero points) of a slab follow its code words as 16 records, record n for
 // columns n and n + 16: kNativeSym 4 bytes (alpha[n], alpha[n + 16]); kNativeAsym 8 bytes (the
-// two alphas, then zp[n] | zp[n + 16] << 4, then three zero bytes), so a lane reads everything
-// its two columns need with one load.
+// two alphas, then -zp[n] and -zp[n + 16] as fp16), so a lane reads everything its two columns
+// need with one load and forms both betas with one packed fp16 multiply.
 __host__ __device__ constexpr int native_record_offset(int group_size) {
   return kSliceCols * group_size / 2;
 }
@@ -106,6 +105,11 @@ __device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
 // fp32 -> fp16, round to nearest even (v_cvt_f16_f32 under the default round mode).
 __device__ __forceinline__ uint16_t float_to_half_bits(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// fp16 bits of -zp (zp in 0..15, exact; zp = 0 gives -0), as stored in asymmetric native slabs.
+__device__ __forceinline__ uint16_t neg_zp_half_bits(uint32_t zp) {
+  return static_cast<uint16_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(zp)) ^ 0x8000u);
 }
 
 // Bits of half_rn(-alpha * zp) for an fp16 alpha and an integer zp in 0..15, signed zeros

@@ -147,7 +147,7 @@ struct MfmaGroupLoad {
   static constexpr int KB = G / 32;  // MFMA k-blocks per group
   uint4 w[2][KB];                    // [half of the tile][k-block]
   uint2 alpha[2];
-  uint2 beta[2];  // kArc: 4 fp16 offsets; kNativeAsym: the zero-point bytes of slabs 2h, 2h+1 in beta[h].x
+  uint2 beta[2];  // kArc: 4 fp16 offsets; kNativeAsym: (-zp) fp16 pairs of slabs 2h (.x), 2h+1 (.y)
 };
 
 // packet: the group's reference packet (kArc), or its slab of slice 0 (native formats: the slab
@@ -169,8 +169,11 @@ __device__ __forceinline__ void mfma_load_group(MfmaGroupLoad<G>& gl, const uint
       if constexpr (F == PacketFormat::kNativeAsym) {
         const uint2 r = *reinterpret_cast<const uint2*>(record);
         pair = r.x;
-        const uint32_t zb = r.y & 0xFFu;
-        gl.beta[s / 2].x = (s % 2 == 0) ? zb : (gl.beta[s / 2].x | (zb << 8));
+        if (s % 2 == 0) {
+          gl.beta[s / 2].x = r.y;
+        } else {
+          gl.beta[s / 2].y = r.y;
+        }
       } else {
         pair = *reinterpret_cast<const uint32_t*>(record);
       }
@@ -262,8 +265,7 @@ __device__ __forceinline__ void mfma_compute_group(const MfmaSmem<G>& sm, const 
       a[j] = __builtin_bit_cast(half8_t, sm.xs[gl][U * (lane / 16) + j][lane % 16]);
     }
     // Scales of the lane's two columns of each slab; kNativeAsym beta = half_rn(-alpha * zp) for
-    // both columns with one packed fp16 multiply (fp16 0x6400 | z is 1024 + z, 1024 minus it is
-    // -z exactly).
+    // both columns with one packed fp16 multiply of the alphas by the stored (-zp) pair.
     float bs[kSlicesPerTile][2];
     float as[kSlicesPerTile][2];
 #pragma unroll
@@ -271,11 +273,9 @@ __device__ __forceinline__ void mfma_compute_group(const MfmaSmem<G>& sm, const 
       const uint32_t pair = (sl % 2 == 0) ? ld.alpha[sl / 2].x : ld.alpha[sl / 2].y;
       uint32_t beta_pair = 0;
       if constexpr (F == PacketFormat::kNativeAsym) {
-        const uint32_t zp_byte = (ld.beta[sl / 2].x >> (8 * (sl % 2))) & 0xFFu;
-        const uint32_t z = (zp_byte & 0xFu) | ((zp_byte & 0xF0u) << 12);
-        const half2_t neg_z = __builtin_bit_cast(half2_t, 0x64006400u) -
-                              __builtin_bit_cast(half2_t, z | 0x64006400u);
-        beta_pair = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, pair) * neg_z);
+        const uint32_t neg_zp = (sl % 2 == 0) ? ld.beta[sl / 2].x : ld.beta[sl / 2].y;
+        beta_pair = __builtin_bit_cast(
+            uint32_t, __builtin_bit_cast(half2_t, pair) * __builtin_bit_cast(half2_t, neg_zp));
       }
 #pragma unroll
       for (int i = 0; i < 2; ++i) {

@@ -188,7 +188,7 @@ struct NativeLoad {
   static constexpr int kVecs = G == 128 ? 2 : 1;
   uint4 w[kVecs];
   uint32_t alpha;  // alpha of columns n (bits 0-15) and n + 16
-  uint32_t zp;     // kNativeAsym: zero points of columns n (bits 0-3) and n + 16 (bits 4-7)
+  uint32_t zp;     // kNativeAsym: -zp of columns n (bits 0-15) and n + 16 as fp16
 };
 
 template <int G, PacketFormat F>
@@ -341,14 +341,12 @@ __device__ __forceinline__ void native_compute_group(const NativeSmem<G, MT>& sm
       }
     }
   }
-  // kNativeAsym: beta = half_rn(-alpha * zp) for both columns with one packed fp16 multiply
-  // (fp16 0x6400 | z is 1024 + z, so 1024 - that is -z exactly).
+  // kNativeAsym: beta = half_rn(-alpha * zp) for both columns with one packed fp16 multiply of
+  // the alphas by the stored (-zp) pair.
   uint32_t beta_pair = 0;
   if constexpr (F == PacketFormat::kNativeAsym) {
-    const uint32_t z = (ld.zp & 0xFu) | ((ld.zp & 0xF0u) << 12);
-    const half2_t neg_z = __builtin_bit_cast(half2_t, 0x64006400u) -
-                          __builtin_bit_cast(half2_t, z | 0x64006400u);
-    beta_pair = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, ld.alpha) * neg_z);
+    beta_pair = __builtin_bit_cast(
+        uint32_t, __builtin_bit_cast(half2_t, ld.alpha) * __builtin_bit_cast(half2_t, ld.zp));
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {

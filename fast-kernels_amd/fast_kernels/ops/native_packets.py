@@ -14,8 +14,8 @@ order, so the groups of a slice are one contiguous range:
   * code words: G/8 words per column (the reference's word packing, 8 codes along K per word),
     in the quarter order the kernels read (four lanes per column, 1 KB per wave-wide load);
   * 16 records, one per column pair (n, n + 16): the two fp16 alphas and, for "native_asym",
-    the two int4 zero points in one byte (padded to 8 bytes), so one load brings a lane all the
-    scales of its two columns.
+    the two negated zero points as fp16 (-zp[n], -zp[n + 16]), so one load brings a lane all the
+    scales of its two columns and one packed fp16 multiply both betas.
 
 "native_sym" (zp = 8) slabs are 16*G + 64 bytes, "native_asym" slabs 16*G + 128; a buffer is
 [(N/32) * K/G, slab bytes]. The kernels rebuild beta = half_rn(-alpha * zp) bit for bit, so a
@@ -67,7 +67,7 @@ def packet_format_code(packet_format: str | int) -> int:
 def packet_stride_bytes(group_size: int, packet_format: str | int) -> int:
     """Bytes per reference packet (code words 64*G, alphas 256, betas 256) or native slab (code
     words 16*G, then 16 records of 4 bytes (two alphas) or, for native_asym, 8 bytes (two alphas,
-    two zero points, padding))."""
+    two negated zero points as fp16))."""
     code = packet_format_code(packet_format)
     if code == PACKET_ARC:
         return arc_packet_stride_bytes(group_size)

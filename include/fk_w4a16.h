@@ -135,8 +135,8 @@ int fk_arc_w4a16_forward_ex(const void* activations, const void* packets, void* 
  *               16 bytes at i*1024 + (16t + n)*16; G = 64: both of a lane's units share the
  *               16 bytes at (16t + n)*16 (column n first).
  *   records     16, one per column pair (n, n + 16): the two fp16 alphas (4 bytes), and for
- *               FK_PACKET_NATIVE_ASYM the two zero points in one byte (zp[n] | zp[n + 16] << 4)
- *               and three zero bytes (8 bytes per record).
+ *               FK_PACKET_NATIVE_ASYM the two negated zero points as fp16 (-zp[n], -zp[n + 16];
+ *               zp = 0 is stored as -0) (8 bytes per record).
  * FK_PACKET_NATIVE_SYM slabs are 16*G + 64 bytes (zp = 8 for every group), FK_PACKET_NATIVE_ASYM
  * slabs 16*G + 128 bytes; a buffer holds (N/32) * (K/G) slabs. (FK_PACKET_ARC is the reference
  * layout above, 64*G + 512 bytes per packet.) The forward over native slabs returns, bit for

@@ -55,8 +55,8 @@ def _expected_native(case, asym: bool) -> np.ndarray:
     """Native slabs rearranged from the oracle's reference packets. Slab (tile, slice, group):
     the slice's code words in quarter order (column 16 i + n has G/8 words in four quarters of
     U = G/32; lane 16 t + n of a wave owns quarter t of columns n and n + 16), then 16 records,
-    one per column pair: (alpha[n], alpha[n + 16]) and, asymmetric, zp[n] | zp[n+16] << 4 and
-    three zero bytes."""
+    one per column pair: (alpha[n], alpha[n + 16]) and, asymmetric, (-zp[n], -zp[n + 16]) as
+    fp16 (zp = 0 as -0)."""
     g = case.group_size
     ng = case.k // g
     tiles = case.n // 128
@@ -84,7 +84,11 @@ def _expected_native(case, asym: bool) -> np.ndarray:
         records[..., 2 * i + 1] = (a >> 8).astype(np.uint8)
     if asym:
         zp = case.zero_points.reshape(tiles, 4, 32, ng).transpose(0, 1, 3, 2)  # [t, s, g, col]
-        records[..., 4] = (zp[..., :16] | (zp[..., 16:] << 4)).astype(np.uint8)
+        for i in range(2):
+            neg = (-zp[..., 16 * i : 16 * i + 16].astype(np.float16)).view(np.uint16)
+            neg = np.where(zp[..., 16 * i : 16 * i + 16] == 0, np.uint16(0x8000), neg)
+            records[..., 4 + 2 * i] = (neg & 0xFF).astype(np.uint8)
+            records[..., 5 + 2 * i] = (neg >> 8).astype(np.uint8)
     out[..., 16 * g :] = records.reshape(tiles, 4, ng, 16 * rec)
     return out.reshape(tiles * 4 * ng, stride)
 
