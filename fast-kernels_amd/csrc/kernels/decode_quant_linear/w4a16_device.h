@@ -92,14 +92,9 @@ __device__ __forceinline__ float bf16_bits_to_float(uint16_t bits) {
   return __builtin_bit_cast(float, static_cast<uint32_t>(bits) << 16);
 }
 
-// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN.
+// fp32 -> bf16, round to nearest even; NaN stays a NaN (gfx950's v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) {
-    return static_cast<uint16_t>((u >> 16) | 0x0040u);
-  }
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 // fp32 -> fp16, round to nearest even (v_cvt_f16_f32 under the default round mode).

@@ -164,6 +164,10 @@ __device__ __forceinline__ void stage_store(Smem<G, MT, CW>& sm, StageRegs<G, MT
     const int w = u % WR;
     const int gl = (u / WR) % kChunk;
     const int m = u / (WR * kChunk);
+    // Units past the chunk stage nothing; a group's WR lanes share gl (see the native staging).
+    if (u >= StageRegs<G, MT, CW>::kUnits || gl >= n_chunk) {
+      continue;
+    }
     uint4 r = st.unit(it);
     float undo = 1.0f;
     if constexpr (A == Act::kBF16) {
@@ -206,7 +210,7 @@ __device__ __forceinline__ void stage_store(Smem<G, MT, CW>& sm, StageRegs<G, MT
         so += __shfl_xor(so, off);
       }
     }
-    if (u < StageRegs<G, MT, CW>::kUnits && gl < n_chunk) {
+    {
       // Odd-position partners (high nibbles, unpacked as 1024 + 16 q) are staged divided by 16,
       // exact in fp16 (values below 2^-10 become subnormal and keep fewer bits), so both nibble
       // positions accumulate into one sum: (1024 + q) x_e + (64 + q) x_o.

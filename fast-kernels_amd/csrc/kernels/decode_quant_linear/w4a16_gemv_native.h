@@ -235,6 +235,11 @@ __device__ __forceinline__ void native_stage_store(NativeSmem<G, MT>& sm, StageR
     const int w = u % WR;
     const int gl = (u / WR) % kChunk;
     const int m = u / (WR * kChunk);
+    // Units past the chunk (a short last chunk, or K shorter than a chunk) stage nothing; a
+    // group's WR lanes share gl, so the cross-lane sums below stay within live lanes.
+    if (u >= StageRegs<G, MT, kCW>::kUnits || gl >= n_chunk) {
+      continue;
+    }
     uint4 r = st.unit(it);
     if constexpr (kNorm) {
       const float inv = sm.inv_rms[m < MT ? m : 0];
@@ -267,7 +272,7 @@ __device__ __forceinline__ void native_stage_store(NativeSmem<G, MT>& sm, StageR
                half_bits_to_float(static_cast<uint16_t>(r.w >> 16));
     se = group_sum<U>(se);
     so = group_sum<U>(so);
-    if (u < StageRegs<G, MT, kCW>::kUnits && gl < n_chunk) {
+    {
       // The odd-position partners (high nibbles, unpacked as 1024 + 16 q) are staged divided by
       // 16, exact in fp16 (values below 2^-10 become subnormal and keep fewer bits), so both
       // nibble positions accumulate into one sum: (1024 + q) x_e + (64 + q) x_o.
