@@ -102,7 +102,20 @@ __device__ __forceinline__ void mfma_stage_store(MfmaSmem<G>& sm, MfmaStage<G>& 
     const int w = u % WR;
     const int gl = (u / WR) % kChunk;
     const int r = u / (WR * kChunk);
-    uint4 v = st.ok[it] ? st.raw[it] : make_uint4(0u, 0u, 0u, 0u);
+    if (gl >= n_chunk) {
+      continue;  // past a short chunk: never read
+    }
+    if (!st.ok[it]) {
+      // A row past the batch: zeros, without the conversions (a group's WR lanes share r and gl,
+      // so the cross-lane sums below only ever combine live lanes).
+      sm.xs[gl][w][r] = make_uint4(0u, 0u, 0u, 0u);
+      if (w == 0) {
+        sm.sums[gl][r] = make_float2(0.0f, 0.0f);
+        sm.scale[gl][r] = 1.0f;
+      }
+      continue;
+    }
+    uint4 v = st.raw[it];
     float undo = 1.0f;
     if constexpr (A == Act::kBF16) {
       const uint32_t e = group_max<WR>(
@@ -126,7 +139,7 @@ __device__ __forceinline__ void mfma_stage_store(MfmaSmem<G>& sm, MfmaStage<G>& 
     }
     se = group_sum<WR>(se);
     so = group_sum<WR>(so);
-    if (gl < n_chunk) {
+    {
       // Odd-k partners are staged divided by 16 (exact in fp16; below 2^-10 they become
       // subnormal and keep fewer bits) to match the high-nibble unpack 1024 + 16 q.
       uint4 xp = pair_activations(v);
