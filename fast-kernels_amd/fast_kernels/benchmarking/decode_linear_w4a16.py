@@ -33,6 +33,7 @@ from fast_kernels.schemas import BenchmarkCase, BenchmarkSuite
 WARMUP_ITERS = 4
 TIMING_ITERS = 12
 DEVICE_TIMING_BLOCKS = 7
+WARM_SECONDS = 0.25
 CACHE_BUST_BYTES = 2 * 256 * 1024 * 1024
 PEAK_HBM_GBS = 8000.0
 SubjectKind = Literal["kernel", "baseline"]
@@ -94,7 +95,8 @@ def _time_wall(fn: Callable[[], Any], torch: Any) -> tuple[float, float]:
 def _time_device(fn: Callable[[int], Any], rotations: int, launches: int, torch: Any) -> tuple[float, float]:
     """Per-launch device time of `launches` back-to-back launches cycling through `rotations`
     weight copies, captured in one HIP graph so host launch overhead does not hide the kernels;
-    HIP events around graph replays, median and p95 over DEVICE_TIMING_BLOCKS replays."""
+    HIP events between back-to-back graph replays, median and p95 over DEVICE_TIMING_BLOCKS
+    replays after at least WARM_SECONDS of warm-up replays."""
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
         for r in range(2 * rotations):  # warm-up on the capture stream: workspaces exist before capture
@@ -106,16 +108,25 @@ def _time_device(fn: Callable[[int], Any], rotations: int, launches: int, torch:
             fn(i % rotations)
     samples: list[float] = []
     with torch.cuda.stream(stream):
+        # Warm for at least WARM_SECONDS of back-to-back replays, so the clocks have ramped
+        # after the host-side setup before the first timed block; the blocks then run back to
+        # back with no host wait between them.
+        first = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        first[0].record(stream)
         graph.replay()
-        torch.cuda.synchronize()
-        for _ in range(DEVICE_TIMING_BLOCKS):
-            start = torch.cuda.Event(enable_timing=True)
-            end = torch.cuda.Event(enable_timing=True)
-            start.record(stream)
+        first[1].record(stream)
+        first[1].synchronize()
+        block_s = max(first[0].elapsed_time(first[1]) * 1e-3, 1e-6)
+        for _ in range(max(DEVICE_TIMING_BLOCKS, min(4096, math.ceil(WARM_SECONDS / block_s)))):
             graph.replay()
-            end.record(stream)
-            end.synchronize()
-            samples.append(start.elapsed_time(end) * 1e3 / launches)
+        events = [torch.cuda.Event(enable_timing=True) for _ in range(DEVICE_TIMING_BLOCKS + 1)]
+        events[0].record(stream)
+        for i in range(DEVICE_TIMING_BLOCKS):
+            graph.replay()
+            events[i + 1].record(stream)
+        events[-1].synchronize()
+        for i in range(DEVICE_TIMING_BLOCKS):
+            samples.append(events[i].elapsed_time(events[i + 1]) * 1e3 / launches)
     del graph
     return float(median(samples)), _p95(samples)
 
@@ -332,29 +343,6 @@ def _run_shape(torch: Any, device: Any, suite: BenchmarkSuite, dtype: str, layou
                      throughput=batch * 1e6 / dev_med, decode_tokens_per_second=batch * 1e6 / dev_med,
                      metrics=metrics)
 
-    vendor_id = next((v for v in suite.baselines.ids if v in VENDOR_BASELINES), None)
-    for baseline_id in suite.baselines.ids:
-        if baseline_id == REFERENCE_BASELINE:
-            out.append(timed("baseline", baseline_id, run_reference,
-                             lambda r: run_reference(*qab_rot[r]),
-                             {"max_abs_err": _max_err(ref_out, explicit)}))
-        elif baseline_id in VENDOR_BASELINES:
-            if act != "f16":
-                out.append(_case("baseline", baseline_id, dtype, layout, name, dims, "skipped",
-                                 reason="the hipBLASLt baseline takes fp16 activations only"))
-                continue
-
-            def run_vendor(qq: Any = q, aa: Any = a, bb: Any = b) -> Any:
-                return cublaslt_fp16_after_dequant(x, qq, aa, bb, group_size=group_size,
-                                                   output=vendor_out, weight_buffer=vendor_weight,
-                                                   workspace=workspace)
-
-            out.append(timed("baseline", baseline_id, run_vendor, lambda r: run_vendor(*qab_rot[r]),
-                             {"max_abs_err": _max_err(vendor_out, explicit)}))
-        else:
-            out.append(_case("baseline", baseline_id, dtype, layout, name, dims, "not_implemented",
-                             reason=f"{baseline_id} has no runner in this suite family"))
-
     for kernel_id in suite.kernels.ids:
         impl = kernels[kernel_id].impl
         if impl is not None and impl not in supported:
@@ -387,6 +375,34 @@ def _run_shape(torch: Any, device: Any, suite: BenchmarkSuite, dtype: str, layou
                                   kernel=kernel)
             extra.update({f"plan_{key}": float(val) for key, val in plan.items()})
         out.append(timed("kernel", kernel_id, run_kernel, lambda r, f=run_kernel, rot=rot: f(rot[r]), extra))
+    # The kernels are timed before the baselines: the reference baseline's large temporaries and
+    # long runs measurably slowed the next case timed after them. Cases are reported baselines first.
+    kernel_cases = out
+    out = []
+    vendor_id = next((v for v in suite.baselines.ids if v in VENDOR_BASELINES), None)
+    for baseline_id in suite.baselines.ids:
+        if baseline_id == REFERENCE_BASELINE:
+            out.append(timed("baseline", baseline_id, run_reference,
+                             lambda r: run_reference(*qab_rot[r]),
+                             {"max_abs_err": _max_err(ref_out, explicit)}))
+        elif baseline_id in VENDOR_BASELINES:
+            if act != "f16":
+                out.append(_case("baseline", baseline_id, dtype, layout, name, dims, "skipped",
+                                 reason="the hipBLASLt baseline takes fp16 activations only"))
+                continue
+
+            def run_vendor(qq: Any = q, aa: Any = a, bb: Any = b) -> Any:
+                return cublaslt_fp16_after_dequant(x, qq, aa, bb, group_size=group_size,
+                                                   output=vendor_out, weight_buffer=vendor_weight,
+                                                   workspace=workspace)
+
+            out.append(timed("baseline", baseline_id, run_vendor, lambda r: run_vendor(*qab_rot[r]),
+                             {"max_abs_err": _max_err(vendor_out, explicit)}))
+        else:
+            out.append(_case("baseline", baseline_id, dtype, layout, name, dims, "not_implemented",
+                             reason=f"{baseline_id} has no runner in this suite family"))
+
+    out.extend(kernel_cases)
     if vendor_id is not None and vendor_id in latencies:
         for c in out:
             if c.status == "ok" and c.subject_id != vendor_id and c.device_latency_us_median:
