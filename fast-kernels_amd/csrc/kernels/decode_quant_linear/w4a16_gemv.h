@@ -40,6 +40,9 @@ struct GemvLaunch {
   GemvFuse fuse = GemvFuse::kNone;           // native formats: fused decode-step neighbour
   const void* norm_weight = nullptr;         // GemvFuse::kRmsNorm: gamma [K], activation dtype
   float eps = 0.0f;                          // GemvFuse::kRmsNorm: epsilon
+  // Native formats, unfused: each workgroup run streams two adjacent whole 32-column slices at
+  // once (two waves per slice), which needs units_per_workgroup to be a multiple of 2 K/G.
+  bool slice_pair = false;
 };
 
 // Activation rows per m-tile for a batch: 1, 2, 4, 8 on the dot2 GEMV kernel, kMfmaRows (from

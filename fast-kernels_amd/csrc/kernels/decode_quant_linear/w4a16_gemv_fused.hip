@@ -115,7 +115,8 @@ hipError_t fused_dispatch(const GemvLaunch& l, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_w4a16_gemv_fused(const GemvLaunch& l, hipStream_t stream) {
-  if (l.mode != GemvMode::kStreamK || l.slice_cols != kSliceCols || l.fuse == GemvFuse::kNone) {
+  if (l.mode != GemvMode::kStreamK || l.slice_cols != kSliceCols || l.fuse == GemvFuse::kNone ||
+      l.slice_pair) {
     return hipErrorInvalidValue;
   }
   switch (l.format) {

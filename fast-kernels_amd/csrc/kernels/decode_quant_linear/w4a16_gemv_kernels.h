@@ -109,6 +109,7 @@ struct GemvParams {
   int xcd_remap;
   const uint16_t* norm_weight;      // RMSNorm prologue: gamma [K] (activation dtype), else null
   float eps;                        // RMSNorm prologue: epsilon
+  int pair;                         // native slabs: each run streams two adjacent whole slices
 };
 
 template <int G, int MT, int CW>
@@ -639,6 +640,7 @@ hipError_t launch_t(const GemvLaunch& l, hipStream_t stream) {
   p.NG = l.K / G;
   p.tiles = l.N / kTileCols;
   p.mtiles = (l.M + MT - 1) / MT;
+  p.pair = 0;
   p.splits = l.splits;
   p.gps = l.gps;
   p.per = l.units_per_workgroup;

@@ -396,7 +396,7 @@ __device__ __forceinline__ void native_stream_groups(NativeSmem<G, MT>& sm, cons
                                                      int g_hi, int lane, int wave,
                                                      uint32_t mask_lo, uint32_t mask_hi,
                                                      float (&y)[MT][2], bool rms_first = false,
-                                                     bool staged = false) {
+                                                     bool staged = false, bool pair = false) {
   constexpr int kChunk = NativeSmem<G, MT>::kChunk;
   // 8 KB of weights in flight per wave (4 groups at G = 128, 8 at G = 64): measured on MI355X,
   // deeper pipelines (8 or 16 KB per wave) lower the achieved HBM bandwidth of every decode shape.
@@ -428,11 +428,17 @@ __device__ __forceinline__ void native_stream_groups(NativeSmem<G, MT>& sm, cons
         norm_stage_load<G, MT>(nr, p, g0, n_chunk);
       }
     }
-    const int n_w = n_chunk > wave ? (n_chunk - wave + kWaves - 1) / kWaves : 0;
+    // Slice pairs: waves 0 and 2 stream the first slice, waves 1 and 3 the second, each over
+    // every other group of the chunk; a single slice is shared by all four waves.
+    const int ws = pair ? (wave >> 1) : wave;
+    const int lw = pair ? 1 : 2;  // log2 of the waves per slice
+    const int W = 1 << lw;
+    const int n_w = n_chunk > ws ? (n_chunk - ws + W - 1) >> lw : 0;
     const int t_last = max(n_w - 1, 0);
-    const int gl_base = n_w > 0 ? wave : n_chunk - 1;
-    const uint8_t* gp = slabs + static_cast<size_t>(g0 + gl_base) * stride;
-    const size_t step = static_cast<size_t>(kWaves) * stride;
+    const int gl_base = n_w > 0 ? ws : n_chunk - 1;
+    const uint8_t* gp = slabs + (pair ? static_cast<size_t>(wave & 1) * p.NG * stride : 0) +
+                        static_cast<size_t>(g0 + gl_base) * stride;
+    const size_t step = static_cast<size_t>(W) * stride;
     NativeLoad<G> buf[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) {
@@ -455,7 +461,7 @@ __device__ __forceinline__ void native_stream_groups(NativeSmem<G, MT>& sm, cons
     for (int blk = 0; blk + 1 < n_blocks; ++blk, t0 += D) {
 #pragma unroll
       for (int d = 0; d < D; ++d) {
-        native_compute_group<G, A, MT, F>(sm, buf[d], wave + (t0 + d) * kWaves, t, mask_lo,
+        native_compute_group<G, A, MT, F>(sm, buf[d], ws + ((t0 + d) << lw), t, mask_lo,
                                           mask_hi, y);
         native_load<G, F>(buf[d], gp + static_cast<size_t>(min(t0 + D + d, t_last)) * step, lane);
       }
@@ -463,7 +469,7 @@ __device__ __forceinline__ void native_stream_groups(NativeSmem<G, MT>& sm, cons
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       if (t0 + d < n_w) {
-        native_compute_group<G, A, MT, F>(sm, buf[d], wave + (t0 + d) * kWaves, t, mask_lo,
+        native_compute_group<G, A, MT, F>(sm, buf[d], ws + ((t0 + d) << lw), t, mask_lo,
                                           mask_hi, y);
       }
     }
@@ -494,6 +500,14 @@ __device__ __forceinline__ void native_reduce_run(NativeSmem<G, MT>& sm, float (
     }
   }
   __syncthreads();
+}
+
+// Column c of a slice pair (0-31 first slice, 32-63 second): waves 0 and 2 hold the first
+// slice's totals, waves 1 and 3 the second's.
+template <int G, int MT>
+__device__ __forceinline__ float native_pair_red_sum(const NativeSmem<G, MT>& sm, int m, int c) {
+  const int s = c >> 5;
+  return sm.red[s][m][c & 31] + sm.red[s + 2][m][c & 31];
 }
 
 template <int G, int MT>
@@ -533,6 +547,7 @@ w4a16_gemv_native_kernel(GemvParams p) {
   const uint32_t u_begin = static_cast<uint32_t>(b) * p.per;
   const uint32_t u_end = min(total_units, u_begin + p.per);
   uint32_t u = u_begin;
+  const bool pair = p.pair != 0;
   while (u < u_end) {
     const RunPos r = run_pos(p, u, u_end, kSlicesPerTile);
     const int T = r.T;
@@ -545,11 +560,19 @@ w4a16_gemv_native_kernel(GemvParams p) {
         p.packets + (static_cast<size_t>(tile) * kSlicesPerTile + slice) * p.NG * stride;
     float y[MT][2] = {};
     native_stream_groups<G, A, MT, F, kNorm>(sm, p, slabs, row0, g_lo, g_hi, lane, wave, mask_lo,
-                                             mask_hi, y, /*rms_first=*/true);
+                                             mask_hi, y, /*rms_first=*/true, /*staged=*/false,
+                                             pair);
     native_reduce_run<G, MT>(sm, y, lane, wave);
-    finish_run<A, MT, kCW>(p, T, b, row0, tile * kTileCols + slice * kCW, sm.last,
-                           [&](int m, int c) { return native_red_sum(sm, m, c); });
-    u += g_hi - g_lo;
+    if (pair) {
+      // Runs are whole slice pairs (the host checks per % (2 NG) == 0): written directly.
+      finish_run<A, MT, 2 * kCW>(p, T, b, row0, tile * kTileCols + slice * kCW, sm.last,
+                                 [&](int m, int c) { return native_pair_red_sum(sm, m, c); });
+      u += 2 * (g_hi - g_lo);
+    } else {
+      finish_run<A, MT, kCW>(p, T, b, row0, tile * kTileCols + slice * kCW, sm.last,
+                             [&](int m, int c) { return native_red_sum(sm, m, c); });
+      u += g_hi - g_lo;
+    }
   }
 }
 
@@ -574,6 +597,7 @@ GemvParams native_params(const GemvLaunch& l, int* grid) {
   p.max_contrib = l.max_contributors;
   p.norm_weight = static_cast<const uint16_t*>(l.norm_weight);
   p.eps = l.eps;
+  p.pair = l.slice_pair ? 1 : 0;
   const long long total = static_cast<long long>(p.tiles) * kSlicesPerTile * p.mtiles * p.NG;
   *grid = p.per > 0 ? static_cast<int>((total + p.per - 1) / p.per) : 0;
   p.xcd_remap = (*grid % 8 == 0) ? 1 : 0;

@@ -41,6 +41,14 @@ hipError_t launch_w4a16_gemv_native(const GemvLaunch& l, hipStream_t stream) {
   if (l.mode != GemvMode::kStreamK || l.slice_cols != kSliceCols) {
     return hipErrorInvalidValue;
   }
+  if (l.slice_pair) {
+    // Whole slice pairs per run: no fused neighbour, runs of a multiple of two slices' groups.
+    const int ng = l.group_size > 0 ? l.K / l.group_size : 0;
+    if (l.fuse != GemvFuse::kNone || ng <= 0 || l.units_per_workgroup <= 0 ||
+        l.units_per_workgroup % (2 * ng) != 0) {
+      return hipErrorInvalidValue;
+    }
+  }
   switch (l.format) {
     case PacketFormat::kNativeSym: return native_dispatch<PacketFormat::kNativeSym>(l, stream);
     case PacketFormat::kNativeAsym: return native_dispatch<PacketFormat::kNativeAsym>(l, stream);

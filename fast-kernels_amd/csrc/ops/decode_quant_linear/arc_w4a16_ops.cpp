@@ -120,6 +120,8 @@ constexpr int kMinGroupsPerWorkgroup = 8;
 constexpr int kMaxRunGroups = 64;
 // Narrowest column slice (the GEMV kernel serves 128, 64 and 32 columns per workgroup).
 constexpr int kMaxSlicesPerTile = 4;
+// Longest K for which one-row native plans stream slice pairs.
+constexpr int kMaxPairK = 4096;
 
 // Grid, run length and fix-up workspace of a stream-K plan over tiles x slices x num_groups units.
 void finish_plan(ArcW4A16Plan& plan, long long tiles, long long slices, int num_groups,
@@ -250,7 +252,7 @@ ArcW4A16Plan plan_arc_impl(int batch, int n, int k, int group_size, int activati
 // plan_w4a16_for_format for a kernel choice (kKernelDot2 is what the fused kernels need).
 ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int activation_dtype,
                                   int split_k_slices, int cu_count, int packet_format,
-                                  int kernel) {
+                                  int kernel, bool allow_pair = true) {
   const fk::PacketFormat format = to_packet_format(packet_format, true);
   validate_dimensions(batch, n, k, group_size);
   if (cu_count == 0) {
@@ -284,6 +286,24 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
       s_split *= 2;
     }
     per = (num_groups + s_split - 1) / s_split;
+  }
+  // Slice pairs (one row, whole slices): a workgroup streams two adjacent slices at once, two waves
+  // each, i.e. 64 columns over all of K. Half the workgroups, each with twice the loads in flight
+  // and half the per-workgroup start-up cost per byte. Taken when the pairs fill the chip's rounds
+  // of workgroups at least as evenly as the single slices: ceil(S / CUs) >= 2 ceil(S / (2 CUs)).
+  // Measured on MI355X: 7B qkv (384 slices) 8.2 -> 7.8 us, 8B gate_up (896) 14.6 -> 13.6 us,
+  // 7B gate_up (688 slices, 344 pairs) got 1 us slower, pairs that leave part of the chip idle
+  // (70B o, 256 slices) 3 us slower, and with longer K, whose single-slice runs already stream
+  // 135 KB, pairs gain nothing (70B qkv, K = 8192: 12.12 -> 12.20 us).
+  if (allow_pair && split_k_slices == 0 && per == num_groups && plan.m_tile == 1 &&
+      k <= kMaxPairK) {
+    const long long rounds = (slices + cu_count - 1) / cu_count;
+    const long long pair_rounds = (slices / 2 + cu_count - 1) / cu_count;
+    if (rounds >= 2 * pair_rounds) {
+      finish_plan(plan, fk::gemv_tiles(n, batch, plan.m_tile), fk::kSlicesPerTile / 2,
+                  num_groups, per, n, batch);
+      return plan;
+    }
   }
   finish_plan(plan, fk::gemv_tiles(n, batch, plan.m_tile), fk::kSlicesPerTile, num_groups, per, n,
               batch);
@@ -365,6 +385,13 @@ void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::u
   l.units_per_workgroup = plan.groups_per_workgroup;
   l.max_contributors = plan.max_tile_contributors;
   l.slice_cols = plan.slice_cols;
+  if (format != fk::PacketFormat::kArc && plan.m_tile != fk::kMfmaRows &&
+      plan.slice_cols == 2 * fk::kSliceCols) {
+    // Native slice pairs: the kernel counts its units in 32-column slices.
+    l.slice_cols = fk::kSliceCols;
+    l.slice_pair = true;
+    l.units_per_workgroup = 2 * plan.groups_per_workgroup;
+  }
   l.format = format;
   l.fuse = fuse;
   l.norm_weight = reinterpret_cast<const void*>(norm_weight_ptr);
@@ -826,7 +853,7 @@ ArcW4A16Plan plan_w4a16_rmsnorm(int batch, int n, int k, int group_size, int act
                                 int split_k_slices, int cu_count, int packet_format) {
   to_packet_format(packet_format, false);
   return plan_for_format_impl(batch, n, k, group_size, activation_dtype, split_k_slices, cu_count,
-                              packet_format, kKernelDot2);
+                              packet_format, kKernelDot2, /*allow_pair=*/false);
 }
 
 void arc_w4a16_forward_silu_mul(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,

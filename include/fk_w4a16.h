@@ -166,7 +166,8 @@ int fk_convert_native_to_arc_packets(const void* native_packets, void* arc_packe
                                      int group_size, int packet_format, void* stream);
 
 /* Launch plan of fk_arc_w4a16_forward_native for a packet format (arguments as
- * fk_arc_w4a16_plan_for); slice_cols is 32 for the native formats below 16 activation rows. */
+ * fk_arc_w4a16_plan_for). For the native formats below 16 activation rows slice_cols is 32, or
+ * 64 for one activation row when a workgroup streams two adjacent 32-column slabs at once. */
 int fk_w4a16_plan_for_format(int batch, int n, int k, int group_size, int activation_dtype,
                              int split_k_slices, int cu_count, int packet_format,
                              fk_arc_w4a16_plan* plan);

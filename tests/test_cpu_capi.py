@@ -212,7 +212,12 @@ def test_native_format_validation_without_gpu(lib: ctypes.CDLL) -> None:
     [
         # (batch, n, k, G) -> (slice_cols, groups per workgroup, workgroups) on 256 CUs
         ((1, 8192, 8192, 128), (32, 64, 256)),      # 256 slices, each over all of K
-        ((1, 10240, 8192, 128), (32, 64, 320)),
+        ((1, 10240, 8192, 128), (32, 64, 320)),     # pairs would fill as evenly, but K is long
+        ((1, 10240, 4096, 128), (64, 32, 160)),     # 320 slices in 160 pairs
+        ((1, 12288, 4096, 128), (64, 32, 192)),     # 7B qkv: 384 slices in 192 pairs
+        ((1, 28672, 4096, 128), (64, 32, 448)),     # 8B gate_up: 896 slices in 448 pairs
+        ((1, 22016, 4096, 128), (32, 32, 688)),     # 7B gate_up: 344 pairs would fill 2 rounds unevenly
+        ((2, 12288, 4096, 128), (32, 32, 384)),     # pairs for one row only
         ((1, 57344, 8192, 128), (32, 64, 1792)),    # more slices than resident workgroups
         ((1, 8192, 28672, 128), (32, 112, 512)),    # long K: two runs of 112, two per CU
         ((1, 4096, 4096, 128), (32, 32, 128)),      # half the CUs idle, but K is short

@@ -171,26 +171,31 @@ def test_forward_native_matches_reference_packets(asym, group_size, batch, act) 
 
 
 @pytest.mark.parametrize(
-    "shape,act,asym",
+    "shape,act,asym,cols",
     [
-        ((1, 1024, 2048, 128), "f16", False),    # 32 slices, one per workgroup
-        ((1, 10240, 4096, 128), "f16", True),    # 320 slices, two workgroups per CU
-        ((1, 4096, 14336, 128), "bf16", False),  # 128 slices, K split in two (fix-up)
-        ((1, 57344, 8192, 128), "bf16", False),  # Llama-70B gate_up, four slices per workgroup
-        ((1, 8192, 28672, 128), "bf16", False),  # Llama-70B down: long K, runs of 112 (fix-up)
-        ((3, 1024, 37 * 64, 64), "f16", True),   # odd group count over two 32-group chunks
-        ((2, 2048, 130 * 64, 64), "bf16", False),  # three 64-group chunks, the last of 2 groups
-        ((2, 4096, 4096, 64), "f16", True),      # two rows
-        ((8, 4096, 4096, 64), "bf16", True),     # eight rows (half-depth pipeline)
-        ((16, 4096, 4096, 64), "bf16", True),    # matrix-core tile over four slabs per group
+        ((1, 1024, 2048, 128), "f16", False, 32),    # 32 slices, one per workgroup
+        ((1, 10240, 4096, 128), "f16", True, 64),    # 320 slices in 160 slice pairs
+        ((1, 4096, 14336, 128), "bf16", False, 32),  # 128 slices, K split in two (fix-up)
+        ((1, 57344, 8192, 128), "bf16", False, 32),  # Llama-70B gate_up, four slices per workgroup
+        ((1, 8192, 28672, 128), "bf16", False, 32),  # Llama-70B down: long K, runs of 112 (fix-up)
+        ((1, 12288, 1024, 64), "f16", False, 64),    # slice pairs over 16 groups
+        ((1, 28672, 4096, 128), "bf16", True, 64),   # Llama-8B gate_up: 448 slice pairs
+        ((1, 12288, 37 * 64, 64), "bf16", True, 64),  # slice pairs, odd group count
+        ((1, 10240, 7 * 128, 128), "f16", False, 64),  # slice pairs, odd group count at G=128
+        ((1, 12288, 130 * 64, 64), "f16", False, 32),  # pairs would fit, but K is long
+        ((3, 1024, 37 * 64, 64), "f16", True, 32),   # odd group count over two 32-group chunks
+        ((2, 2048, 130 * 64, 64), "bf16", False, 32),  # three 64-group chunks, the last of 2 groups
+        ((2, 4096, 4096, 64), "f16", True, 32),      # two rows
+        ((8, 4096, 4096, 64), "bf16", True, 128),    # eight rows (half-depth pipeline)
+        ((16, 4096, 4096, 64), "bf16", True, 128),   # matrix-core tile over four slabs per group
     ],
 )
-def test_forward_native_plans_match_oracle(shape, act, asym) -> None:
+def test_forward_native_plans_match_oracle(shape, act, asym, cols) -> None:
     batch, n, k, g = shape
     plan = arc_w4a16_plan(batch=batch, n=n, k=k, group_size=g,
                           activation_dtype=torch.float16 if act == "f16" else torch.bfloat16,
                           packet_format=2 if asym else 1)
-    assert plan["slice_cols"] == (128 if batch >= 8 else 32)
+    assert plan["slice_cols"] == cols, plan
     case = make_case(batch, n, k, g, act=act, asymmetric=asym)
     y_nat, _ = _forward_pair(case, asym)
     if n > 8192:  # the oracle checks a spread subset of rows of the large shape
