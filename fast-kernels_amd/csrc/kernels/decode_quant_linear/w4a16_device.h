@@ -171,6 +171,28 @@ __device__ __forceinline__ uint4 pair_activations(uint4 x) {
 }
 
 
+// Weight loads. Every weight byte is read once per call, so the GEMV kernels load them
+// non-temporally (global_load ... nt): measured on MI355X with a pure streaming kernel
+// (benchmarks/hbm_read_floor.hip), nt loads read 242 MB in 36.1 us against 39.3 us for plain
+// loads of the same pattern, and 121 MB in 18.7 against 20.1 us. Activations, which every
+// workgroup re-reads from L2, keep plain loads.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint4 stream_load16(const uint8_t* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint2 stream_load8(const uint8_t* p) {
+  const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+  return make_uint2(v.x, v.y);
+}
+
+__device__ __forceinline__ uint32_t stream_load4(const uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+}
+
 // s_waitcnt immediate for gfx9 waiting until at most n vector-memory operations are outstanding:
 // vmcnt in bits 3:0 and 15:14, expcnt (6:4) and lgkmcnt (11:8) left at their maximum (no wait).
 constexpr int wait_vmcnt(int n) {

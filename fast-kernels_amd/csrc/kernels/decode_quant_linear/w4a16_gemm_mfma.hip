@@ -180,7 +180,7 @@ __device__ __forceinline__ void mfma_load_group(MfmaGroupLoad<G>& gl, const uint
       const uint8_t* record = slab + native_record_offset(G) + native_record_bytes(F) * (lane % 16);
       uint32_t pair = 0;
       if constexpr (F == PacketFormat::kNativeAsym) {
-        const uint2 r = *reinterpret_cast<const uint2*>(record);
+        const uint2 r = stream_load8(record);
         pair = r.x;
         if (s % 2 == 0) {
           gl.beta[s / 2].x = r.y;
@@ -188,7 +188,7 @@ __device__ __forceinline__ void mfma_load_group(MfmaGroupLoad<G>& gl, const uint
           gl.beta[s / 2].y = r.y;
         }
       } else {
-        pair = *reinterpret_cast<const uint32_t*>(record);
+        pair = stream_load4(record);
       }
       if (s % 2 == 0) {
         gl.alpha[s / 2].x = pair;
@@ -196,10 +196,10 @@ __device__ __forceinline__ void mfma_load_group(MfmaGroupLoad<G>& gl, const uint
         gl.alpha[s / 2].y = pair;
       }
       if constexpr (G == 128) {
-        gl.w[s / 2][2 * (s % 2)] = *reinterpret_cast<const uint4*>(slab + lane * 16);
-        gl.w[s / 2][2 * (s % 2) + 1] = *reinterpret_cast<const uint4*>(slab + 1024 + lane * 16);
+        gl.w[s / 2][2 * (s % 2)] = stream_load16(slab + lane * 16);
+        gl.w[s / 2][2 * (s % 2) + 1] = stream_load16(slab + 1024 + lane * 16);
       } else {
-        gl.w[s / 2][s % 2] = *reinterpret_cast<const uint4*>(slab + lane * 16);
+        gl.w[s / 2][s % 2] = stream_load16(slab + lane * 16);
       }
     }
   } else {
@@ -207,11 +207,11 @@ __device__ __forceinline__ void mfma_load_group(MfmaGroupLoad<G>& gl, const uint
     const int code = (lane / 16) * kWordRowBytes + col4 * 4;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      gl.alpha[h] = *reinterpret_cast<const uint2*>(packet + QB + (h * 64 + col4) * 2);
-      gl.beta[h] = *reinterpret_cast<const uint2*>(packet + QB + kTileCols * 2 + (h * 64 + col4) * 2);
+      gl.alpha[h] = stream_load8(packet + QB + (h * 64 + col4) * 2);
+      gl.beta[h] = stream_load8(packet + QB + kTileCols * 2 + (h * 64 + col4) * 2);
 #pragma unroll
       for (int kb = 0; kb < MfmaGroupLoad<G>::KB; ++kb) {
-        gl.w[h][kb] = *reinterpret_cast<const uint4*>(packet + code + kb * 4 * kWordRowBytes + h * 256);
+        gl.w[h][kb] = stream_load16(packet + code + kb * 4 * kWordRowBytes + h * 256);
       }
     }
   }

@@ -261,11 +261,11 @@ __device__ __forceinline__ void load_group(GroupLoad<G, CW, F>& gl, const uint8_
                                            LaneAddr la) {
   static_assert(F == PacketFormat::kArc, "native slabs are read by w4a16_gemv_native.hip");
   constexpr int R = Slice<G, CW>::kRowsPerLoad;
-  gl.alpha = *reinterpret_cast<const uint2*>(packet + la.scale);
-  gl.beta = *reinterpret_cast<const uint2*>(packet + la.scale + kTileCols * 2);
+  gl.alpha = stream_load8(packet + la.scale);
+  gl.beta = stream_load8(packet + la.scale + kTileCols * 2);
 #pragma unroll
   for (int i = 0; i < GroupLoad<G, CW, F>::NL; ++i) {
-    gl.w[i] = *reinterpret_cast<const uint4*>(packet + la.code + i * R * kWordRowBytes);
+    gl.w[i] = stream_load16(packet + la.code + i * R * kWordRowBytes);
   }
 }
 

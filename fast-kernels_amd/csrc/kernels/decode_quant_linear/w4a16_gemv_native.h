@@ -195,15 +195,15 @@ template <int G, PacketFormat F>
 __device__ __forceinline__ void native_load(NativeLoad<G>& ld, const uint8_t* slab, int lane) {
 #pragma unroll
   for (int v = 0; v < NativeLoad<G>::kVecs; ++v) {
-    ld.w[v] = *reinterpret_cast<const uint4*>(slab + v * 1024 + lane * 16);
+    ld.w[v] = stream_load16(slab + v * 1024 + lane * 16);
   }
   const uint8_t* record = slab + native_record_offset(G) + native_record_bytes(F) * (lane % 16);
   if constexpr (F == PacketFormat::kNativeAsym) {
-    const uint2 r = *reinterpret_cast<const uint2*>(record);
+    const uint2 r = stream_load8(record);
     ld.alpha = r.x;
     ld.zp = r.y;
   } else {
-    ld.alpha = *reinterpret_cast<const uint32_t*>(record);
+    ld.alpha = stream_load4(record);
   }
 }
 
