@@ -46,6 +46,11 @@ WORKLOADS = {
         128,
         [("qkv", 10240, 8192), ("o", 8192, 8192), ("gate_up", 57344, 8192), ("down", 8192, 28672)],
     ),
+    "llama8b_layer_m1_bf16": (
+        "bf16",
+        128,
+        [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)],
+    ),
     "llama7b_layer_m1_fp16": (
         "f16",
         128,

@@ -144,6 +144,7 @@ void copy_plan(const ops::ArcW4A16Plan& p, fk_arc_w4a16_plan* plan) {
   plan->max_tile_contributors = p.max_tile_contributors;
   plan->workspace_bytes = p.workspace_bytes;
   plan->slice_cols = p.slice_cols;
+  plan->schedule = p.schedule;
 }
 
 }  // namespace

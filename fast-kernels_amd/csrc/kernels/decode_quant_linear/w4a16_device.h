@@ -6,8 +6,8 @@
 //
 // Nibble -> 16-bit float without a conversion instruction: OR-ing a nibble into the low mantissa
 // bits of a constant gives an exactly representable "bias + scale*q":
-//   fp16 0x6400 | q        = 1024 + q        (nibble in bits 0-3)
-//   fp16 0x6400 | (q << 4) = 1024 + 16*q     (nibble in bits 4-7)
+//   fp16 0x6400 | q        = 1024 + q        (nibble in bits 0-3: exponent 2^10, ulp 1)
+//   fp16 0x5400 | (q << 4) = 64 + q          (nibble in bits 4-7: exponent 2^6, ulp 1/16)
 //   bf16 0x4300 | q        = 128 + q         (bf16 keeps only 7 mantissa bits, so bits 0-3 only)
 // One v_and_or_b32 turns a masked word into two such values (bits 0-15 and 16-31). A 32-bit word
 // of codes therefore unpacks into the four half2 pairs (k0,k4) (k1,k5) (k2,k6) (k3,k7); the GEMV
@@ -202,16 +202,43 @@ constexpr int kWaitVmcnt0 = wait_vmcnt(0);
 // Largest bf16 biased exponent whose values all fit in fp16 (2^15 * (2 - 2^-7) < 65504).
 constexpr int kMaxFp16SafeBf16Exp = 142;
 
-// Larger of the biased exponents of the two bf16 values in a word.
-__device__ __forceinline__ uint32_t bf16_exp(uint32_t pair_word) {
-  return max((pair_word >> 7) & 0xffu, (pair_word >> 23) & 0xffu);
+// Unpack biases of a masked code word: the low nibbles of each half (bits 0-3) become
+// 1024 + q, the high nibbles (bits 4-7) 64 + q, both exact fp16 values.
+constexpr uint32_t kBiasLow = 0x64006400u;
+constexpr uint32_t kBiasHigh = 0x54005400u;
+
+// Power-of-two staging shift for a (row, group) of bf16 activations whose largest biased
+// exponent is e: the group is multiplied by 2^-shift so that its largest magnitude lands in
+// [2^15, 2^16), the top binade of fp16. Large groups scale down (no fp16 overflow), small ones
+// scale up, so every bf16 value within 2^-29 of the group maximum converts exactly (an fp16
+// normal). Clamped so that 2^-shift and 2^shift stay normal fp32 values.
+__device__ __forceinline__ int bf16_stage_shift(uint32_t e) {
+  return max(-126, static_cast<int>(e) - kMaxFp16SafeBf16Exp);
 }
 
-// Two bf16 values, each multiplied by s (a power of two), as an fp16 pair.
+typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
+
+// Largest magnitude (bits without the sign, so its biased exponent is bits >> 7) of the eight
+// bf16 values in four words: packed 16-bit maxima (v_pk_max_u16), one per pair of words. The
+// magnitude bits of bf16 order as the values do (NaN above Inf above finite values).
+__device__ __forceinline__ uint32_t bf16_max_mag(uint4 r) {
+  const uint32_t k = 0x7fff7fffu;
+  const u16x2_t a = __builtin_elementwise_max(__builtin_bit_cast(u16x2_t, r.x & k),
+                                              __builtin_bit_cast(u16x2_t, r.y & k));
+  const u16x2_t b = __builtin_elementwise_max(__builtin_bit_cast(u16x2_t, r.z & k),
+                                              __builtin_bit_cast(u16x2_t, r.w & k));
+  const u16x2_t m = __builtin_elementwise_max(a, b);
+  return max(static_cast<uint32_t>(m.x), static_cast<uint32_t>(m.y));
+}
+
+// Two bf16 values, each multiplied by s (a power of two), as an fp16 pair: exact whenever the
+// scaled value is an fp16 normal (bf16 has 8 significant bits, fp16 11), which the staging shift
+// guarantees for every value within 2^-29 of its group's largest; smaller ones are truncated
+// (the conversion rounds toward zero: one v_cvt_pkrtz_f16_f32 for both). Inf and NaN stay so.
 __device__ __forceinline__ uint32_t bf16_pair_to_half_pair(uint32_t w, float s) {
-  const uint32_t lo = float_to_half_bits(bf16_bits_to_float(static_cast<uint16_t>(w)) * s);
-  const uint32_t hi = float_to_half_bits(bf16_bits_to_float(static_cast<uint16_t>(w >> 16)) * s);
-  return lo | (hi << 16);
+  const float lo = __builtin_bit_cast(float, w << 16) * s;
+  const float hi = __builtin_bit_cast(float, w & 0xffff0000u) * s;
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
 }
 
 // A value the compiler must keep in a VGPR and cannot fold: gfx9 VOP3 encodings take no literal,

@@ -9,9 +9,9 @@
 //    per lane. A wave-wide dwordx4 load gives lane l the words of 4 consecutive columns
 //    (4*(l % 16) + j, j = 0..3) of word row l / 16, so 4 MFMAs (one per j) cover 64 columns x
 //    4 word rows; MFMA j's output column c maps to packet column 4*c + j.
-//  * A code word unpacks into the fp16 values 1024 + q (even k) and 1024 + 16 q (odd k) in the k
+//  * A code word unpacks into the fp16 values 1024 + q (even k) and 64 + q (odd k) in the k
 //    order (0,4)(1,5)(2,6)(3,7), one shift and four and-or; the staged activations are paired in
-//    that order with the odd-k values divided by 16, so A and B agree slot by slot.
+//    that order, so A and B agree slot by slot.
 //  * Every block's MFMA chain starts from C = -1024 S_e - 64 S_o (S_e, S_o: the group's even- and
 //    odd-k activation sums), which cancels the unpack bias, so the group's scale and offset are
 //    applied once per (group, row, column) as y += alpha * D + beta * (S_e + S_o); kNativeSym
@@ -118,9 +118,8 @@ __device__ __forceinline__ void mfma_stage_store(MfmaSmem<G>& sm, MfmaStage<G>& 
     uint4 v = st.raw[it];
     float undo = 1.0f;
     if constexpr (A == Act::kBF16) {
-      const uint32_t e = group_max<WR>(
-          max(max(bf16_exp(v.x), bf16_exp(v.y)), max(bf16_exp(v.z), bf16_exp(v.w))));
-      const int shift = max(0, static_cast<int>(e) - kMaxFp16SafeBf16Exp);
+      const uint32_t e = group_max<WR>(bf16_max_mag(v)) >> 7;
+      const int shift = bf16_stage_shift(e);
       const float s = __builtin_bit_cast(float, static_cast<uint32_t>(127 - shift) << 23);
       undo = __builtin_bit_cast(float, static_cast<uint32_t>(127 + shift) << 23);
       v.x = bf16_pair_to_half_pair(v.x, s);
@@ -140,12 +139,8 @@ __device__ __forceinline__ void mfma_stage_store(MfmaSmem<G>& sm, MfmaStage<G>& 
     se = group_sum<WR>(se);
     so = group_sum<WR>(so);
     {
-      // Odd-k partners are staged divided by 16 (exact in fp16; below 2^-10 they become
-      // subnormal and keep fewer bits) to match the high-nibble unpack 1024 + 16 q.
-      uint4 xp = pair_activations(v);
-      const half2_t sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
-      xp.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, xp.y) * sixteenth);
-      xp.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, xp.w) * sixteenth);
+      // Staged as they are: the high-nibble unpack is 64 + q (see unpack_word).
+      const uint4 xp = pair_activations(v);
       sm.xs[gl][w][r] = xp;
       if (w == 0) {
         sm.sums[gl][r] = make_float2(fmaf(-1024.0f, se, -64.0f * so), se + so);
@@ -218,16 +213,15 @@ __device__ __forceinline__ void mfma_load_group(MfmaGroupLoad<G>& gl, const uint
 }
 
 // Code word -> 8 fp16 values in the slot order (k0,k4)(k1,k5)(k2,k6)(k3,k7): 1024 + q for even
-// k, 1024 + 16 q for odd k (their activations are staged / 16). One shift, four and-or.
+// k, 64 + q for odd k. One shift, four and-or.
 __device__ __forceinline__ half8_t unpack_word(uint32_t w, uint32_t mask_lo, uint32_t mask_hi) {
-  constexpr uint32_t kBias = 0x64006400u;
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   const uint32_t w8 = w >> 8;
   u32x4 v;
-  v.x = (w & mask_lo) | kBias;
-  v.y = (w & mask_hi) | kBias;
-  v.z = (w8 & mask_lo) | kBias;
-  v.w = (w8 & mask_hi) | kBias;
+  v.x = (w & mask_lo) | kBiasLow;
+  v.y = (w & mask_hi) | kBiasHigh;
+  v.z = (w8 & mask_lo) | kBiasLow;
+  v.w = (w8 & mask_hi) | kBiasHigh;
   return __builtin_bit_cast(half8_t, v);
 }
 

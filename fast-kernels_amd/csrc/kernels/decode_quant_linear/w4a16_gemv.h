@@ -43,7 +43,31 @@ struct GemvLaunch {
   // Native formats, unfused: each workgroup run streams two adjacent whole 32-column slices at
   // once (two waves per slice), which needs units_per_workgroup to be a multiple of 2 K/G.
   bool slice_pair = false;
+  // Native formats, one activation row, unfused: the persistent stream schedule
+  // (w4a16_gemv_stream.hip): each workgroup streams one contiguous run of units_per_workgroup
+  // slabs with the whole activation row staged in LDS.
+  bool stream = false;
+  int stream_waves = 0;   // stream schedule: waves per workgroup (kStreamWaves)
+  int stream_depth = 0;   // stream schedule: units in flight per wave
+  int stream_grid = 0;    // stream schedule: workgroups
+  int stream_whole = 0;   // stream schedule: whole slices per workgroup
 };
+
+// Longest K the stream schedule stages (its LDS holds the whole activation row).
+constexpr int kStreamMaxK = 32768;
+// Dynamic LDS of the stream schedule for num_groups group slots (K / G and one spare): the
+// re-paired row (G/8 16-byte words per group), four float2 offset terms and one float staging
+// scale per group.
+inline size_t stream_lds_bytes(int group_size, int num_groups) {
+  return static_cast<size_t>(num_groups) * (static_cast<size_t>(group_size / 8) * 16 + 32 + 4);
+}
+// Waves per workgroup of the stream schedule, and the units (slabs) in flight per wave it may
+// use: 4 or 8 KB of weights per wave (a G = 128 slab is 2 KB, a G = 64 slab 1 KB). K/G and
+// units_per_workgroup must be multiples of kStreamWaves * depth.
+constexpr int kStreamWaves = 8;
+constexpr int stream_depth_for_kb(int group_size, int kb) { return kb / (group_size == 128 ? 2 : 1); }
+// Static LDS of the stream kernel besides the dynamic part (two reduction slots, up to 8 waves).
+constexpr size_t kStreamStaticLdsBytes = 2 * 8 * 32 * sizeof(float);
 
 // Activation rows per m-tile for a batch: 1, 2, 4, 8 on the dot2 GEMV kernel, kMfmaRows (from
 // kMfmaMinBatch rows) on the matrix-core kernel.
@@ -69,5 +93,6 @@ hipError_t launch_w4a16_gemv(const GemvLaunch& launch, hipStream_t stream);
 // native packet formats (w4a16_gemv_native.hip); launch_w4a16_gemv forwards such launches.
 hipError_t launch_w4a16_gemm_mfma(const GemvLaunch& launch, hipStream_t stream);
 hipError_t launch_w4a16_gemv_native(const GemvLaunch& launch, hipStream_t stream);
+hipError_t launch_w4a16_gemv_stream(const GemvLaunch& launch, hipStream_t stream);
 
 }  // namespace fk

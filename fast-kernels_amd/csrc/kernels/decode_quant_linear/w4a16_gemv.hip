@@ -25,6 +25,9 @@ hipError_t launch_w4a16_gemv(const GemvLaunch& l, hipStream_t stream) {
   if (l.m_tile == kMfmaRows) {
     return launch_w4a16_gemm_mfma(l, stream);
   }
+  if (l.stream) {
+    return launch_w4a16_gemv_stream(l, stream);
+  }
   if (l.format != PacketFormat::kArc) {
     return launch_w4a16_gemv_native(l, stream);
   }

@@ -17,16 +17,16 @@
 //    each buffer as soon as it is consumed.
 //  * Register dequant with no per-element conversion: nibbles are OR-ed into fp16 mantissas
 //    (see w4a16_device.h) and multiplied by v_dot2_f32_f16 (fp32 accumulation) against
-//    activations re-paired once per workgroup in LDS. High nibbles unpack as 1024 + 16 q, so
-//    their activation partners are staged divided by 16 and both positions add into one fp32
+//    activations re-paired once per workgroup in LDS. High nibbles unpack as 64 + q (fp16
+//    0x5400 | q << 4), so both positions add into one fp32
 //    accumulator: sum (1024 + q) x_e + (64 + q) x_o. The constant part is removed by seeding the
 //    accumulator with -1024 S_e - 64 S_o from per-group activation sums, and the group's beta
 //    term is beta * (S_e + S_o).
 //  * bf16 activations are converted to fp16 when staged, after scaling each (row, group) by a
-//    power of two that keeps its largest magnitude inside fp16's range; the scale is re-applied
-//    to the group's fp32 partial. Every bf16 value whose scaled magnitude is >= 2^-17 converts
-//    exactly (bf16 has 8 significant bits, fp16 normals 11), so bf16 runs the same fp16 inner
-//    loop.
+//    power of two that puts its largest magnitude in fp16's top binade (bf16_stage_shift); the
+//    scale is re-applied to the group's fp32 partial. Every bf16 value within 2^-24 of its
+//    group's largest converts exactly (bf16 has 8 significant bits, fp16 normals 11), so bf16
+//    runs the same fp16 inner loop.
 //  * Stream-K work split: the grid is sized to be resident on the chip at once and each
 //    workgroup takes an equal run of (slice, group) units, crossing slice boundaries; slices
 //    shared by several workgroups are finished in-kernel by their last contributor (see the
@@ -110,6 +110,8 @@ struct GemvParams {
   const uint16_t* norm_weight;      // RMSNorm prologue: gamma [K] (activation dtype), else null
   float eps;                        // RMSNorm prologue: epsilon
   int pair;                         // native slabs: each run streams two adjacent whole slices
+  int stream_whole;                 // stream schedule (w4a16_gemv_stream.hip): whole slices
+                                    // per workgroup
 };
 
 template <int G, int MT, int CW>
@@ -172,9 +174,8 @@ __device__ __forceinline__ void stage_store(Smem<G, MT, CW>& sm, StageRegs<G, MT
     uint4 r = st.unit(it);
     float undo = 1.0f;
     if constexpr (A == Act::kBF16) {
-      const uint32_t e = group_max<WR>(
-          max(max(bf16_exp(r.x), bf16_exp(r.y)), max(bf16_exp(r.z), bf16_exp(r.w))));
-      const int shift = max(0, static_cast<int>(e) - kMaxFp16SafeBf16Exp);
+      const uint32_t e = group_max<WR>(bf16_max_mag(r)) >> 7;
+      const int shift = bf16_stage_shift(e);
       const float s = __builtin_bit_cast(float, static_cast<uint32_t>(127 - shift) << 23);
       undo = __builtin_bit_cast(float, static_cast<uint32_t>(127 + shift) << 23);
       r.x = bf16_pair_to_half_pair(r.x, s);
@@ -212,13 +213,9 @@ __device__ __forceinline__ void stage_store(Smem<G, MT, CW>& sm, StageRegs<G, MT
       }
     }
     {
-      // Odd-position partners (high nibbles, unpacked as 1024 + 16 q) are staged divided by 16,
-      // exact in fp16 (values below 2^-10 become subnormal and keep fewer bits), so both nibble
-      // positions accumulate into one sum: (1024 + q) x_e + (64 + q) x_o.
-      uint4 xp = pair_activations(r);
-      const half2_t sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
-      xp.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, xp.y) * sixteenth);
-      xp.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, xp.w) * sixteenth);
+      // Both nibble positions accumulate into one sum, (1024 + q) x_e + (64 + q) x_o (the high
+      // nibbles unpack as 64 + q), so the activations are staged as they are.
+      const uint4 xp = pair_activations(r);
       sm.xs[m][gl][w] = xp;
       if (w < R) {
         // the unpack bias, which seeds the accumulators, and the sum for the beta term
@@ -279,7 +276,6 @@ __device__ __forceinline__ void compute_group(const Smem<G, MT, CW>& sm,
                                               float (&y)[MT][4]) {
   constexpr int NL = GroupLoad<G, CW, F>::NL;
   constexpr int R = Slice<G, CW>::kRowsPerLoad;
-  constexpr uint32_t kBias = 0x64006400u;  // fp16 1024.0 pair
   // One accumulator per (row, column); a single row keeps a second one so that its dependent
   // dot2 chains interleave in pairs.
   constexpr int kAcc = MT == 1 ? 2 : 1;
@@ -308,11 +304,11 @@ __device__ __forceinline__ void compute_group(const Smem<G, MT, CW>& sm,
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t wv = words[j];
-      const uint32_t e0 = (wv & mask_lo) | kBias;  // 1024+q for k0,k4
-      const uint32_t o0 = (wv & mask_hi) | kBias;  // 1024+16q for k1,k5
+      const uint32_t e0 = (wv & mask_lo) | kBiasLow;   // 1024+q for k0,k4
+      const uint32_t o0 = (wv & mask_hi) | kBiasHigh;  // 64+q for k1,k5
       const uint32_t w8 = wv >> 8;
-      const uint32_t e1 = (w8 & mask_lo) | kBias;  // k2,k6
-      const uint32_t o1 = (w8 & mask_hi) | kBias;  // k3,k7
+      const uint32_t e1 = (w8 & mask_lo) | kBiasLow;   // k2,k6
+      const uint32_t o1 = (w8 & mask_hi) | kBiasHigh;  // k3,k7
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
         float& a0 = acc[m][j][0];

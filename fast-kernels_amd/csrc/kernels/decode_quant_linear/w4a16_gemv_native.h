@@ -11,8 +11,8 @@
 //    n and n + 16. Per group it therefore applies scales to two columns, not four, and reads U
 //    16-byte activation vectors per row (broadcast: the 16 lanes of a quarter read the same one).
 //  * The unpack bias and the offsets fold into per-(row, group, quarter) constants formed while
-//    staging, so the epilogue is short. The odd-position activations are staged divided by 16,
-//    so the even (1024 + q) and odd (1024 + 16 q) nibble unpacks add into one accumulator:
+//    staging, so the epilogue is short. The even (1024 + q) and odd (64 + q) nibble unpacks
+//    add into one accumulator:
 //    acc = C + sum (1024 + q) x_e + (64 + q) x_o. kNativeSym: beta = half_rn(-8 alpha) = -8 alpha
 //    exactly, C = -1032 S_even - 72 S_odd and y += alpha * acc. kNativeAsym:
 //    C = -1024 S_even - 64 S_odd and y += alpha * acc + beta * (S_even + S_odd), beta =
@@ -40,6 +40,14 @@ struct NativeSmem {
   float aux[MT][kCW];               // SiLU-and-multiply epilogue: the gate half's totals
   float inv_rms[MT];                // RMSNorm prologue: 1 / rms of each row
   int last;                         // this workgroup finishes the slice
+
+  // The staged activations as native_stage_unit writes and native_compute_group reads them.
+  __device__ uint4 x_at(int m, int gl, int i) const { return xs[m][gl][i]; }
+  __device__ float2 sums_at(int m, int gl, int t) const { return sums[m][gl][t]; }
+  __device__ float scale_at(int m, int gl) const { return scale[m][gl]; }
+  __device__ void set_x(int m, int gl, int i, uint4 v) { xs[m][gl][i] = v; }
+  __device__ void set_sums(int m, int gl, int t, float2 v) { sums[m][gl][t] = v; }
+  __device__ void set_scale(int m, int gl, float v) { scale[m][gl] = v; }
 };
 
 // RMSNorm prologue: gamma for the staged units (the same k as the activation units).
@@ -219,6 +227,48 @@ __device__ __forceinline__ uint32_t unit_word(const NativeLoad<G>& ld, int i, in
   }
 }
 
+// One staged unit (word row w of group gl of row m: 8 activations) into LDS: converted (bf16) and
+// re-paired, with the {even, odd} sums over its quarter (U consecutive word rows, U consecutive
+// lanes: every lane of a quarter must call this together). S is the LDS view (NativeSmem or
+// StreamLds).
+template <int G, Act A, PacketFormat F, class S>
+__device__ __forceinline__ void native_stage_unit(S& sm, uint4 r, int m, int gl, int w) {
+  constexpr int WR = G / 8;
+  constexpr int U = native_unit_words(G);
+  float undo = 1.0f;
+  if constexpr (A == Act::kBF16) {
+    const uint32_t e = group_max<WR>(bf16_max_mag(r)) >> 7;
+    const int shift = bf16_stage_shift(e);
+    const float s = __builtin_bit_cast(float, static_cast<uint32_t>(127 - shift) << 23);
+    undo = __builtin_bit_cast(float, static_cast<uint32_t>(127 + shift) << 23);
+    r.x = bf16_pair_to_half_pair(r.x, s);
+    r.y = bf16_pair_to_half_pair(r.y, s);
+    r.z = bf16_pair_to_half_pair(r.z, s);
+    r.w = bf16_pair_to_half_pair(r.w, s);
+  }
+  // Both nibble positions accumulate into one sum, (1024 + q) x_e + (64 + q) x_o (the high
+  // nibbles unpack as 64 + q), so the activations are staged as they are, re-paired
+  // (x0,x4) (x1,x5) (x2,x6) (x3,x7).
+  const uint4 xp = pair_activations(r);
+  // even k: x0 x2 x4 x6 (xp.x, xp.z), odd k: x1 x3 x5 x7 (xp.y, xp.w); v_dot2 by (1, 1) adds
+  // two fp16 values into an fp32 sum
+  constexpr uint32_t kOnes = 0x3c003c00u;
+  float se = dot2<Act::kF16>(xp.z, kOnes, dot2<Act::kF16>(xp.x, kOnes, 0.0f));
+  float so = dot2<Act::kF16>(xp.w, kOnes, dot2<Act::kF16>(xp.y, kOnes, 0.0f));
+  se = group_sum<U>(se);
+  so = group_sum<U>(so);
+  sm.set_x(m, gl, w, xp);
+  // The offset terms of the epilogue divided by alpha, per (row, group, quarter):
+  // kNativeSym (beta = -8 alpha): -1032 S_e - 72 S_o; kNativeAsym: -1024 S_e - 64 S_o, plus
+  // S_e + S_o for the beta * S term. Every lane of the quarter (and, for the scale, of the group)
+  // holds the same value and writes it, so the staging has no branch.
+  sm.set_sums(m, gl, w / U,
+              F == PacketFormat::kNativeSym
+                  ? make_float2(fmaf(-1032.0f, se, -72.0f * so), 0.0f)
+                  : make_float2(fmaf(-1024.0f, se, -64.0f * so), se + so));
+  sm.set_scale(m, gl, undo);
+}
+
 // Activations of one chunk into LDS: the staged, re-paired values as in the reference-packet
 // kernel, and the {even, odd} sums over each quarter (U consecutive word rows, U consecutive
 // lanes here).
@@ -226,7 +276,6 @@ template <int G, Act A, int MT, PacketFormat F, bool kNorm>
 __device__ __forceinline__ void native_stage_store(NativeSmem<G, MT>& sm, StageRegs<G, MT, kCW>& st,
                                                    const NormRegs<G, MT>& nr, int n_chunk) {
   constexpr int WR = G / 8;
-  constexpr int U = native_unit_words(G);
   constexpr int kChunk = NativeSmem<G, MT>::kChunk;
   const int tid = static_cast<int>(threadIdx.x);
 #pragma unroll
@@ -249,61 +298,17 @@ __device__ __forceinline__ void native_stage_store(NativeSmem<G, MT>& sm, StageR
       r.z = norm_pair<A>(r.z, gw.z, inv);
       r.w = norm_pair<A>(r.w, gw.w, inv);
     }
-    float undo = 1.0f;
-    if constexpr (A == Act::kBF16) {
-      const uint32_t e = group_max<WR>(
-          max(max(bf16_exp(r.x), bf16_exp(r.y)), max(bf16_exp(r.z), bf16_exp(r.w))));
-      const int shift = max(0, static_cast<int>(e) - kMaxFp16SafeBf16Exp);
-      const float s = __builtin_bit_cast(float, static_cast<uint32_t>(127 - shift) << 23);
-      undo = __builtin_bit_cast(float, static_cast<uint32_t>(127 + shift) << 23);
-      r.x = bf16_pair_to_half_pair(r.x, s);
-      r.y = bf16_pair_to_half_pair(r.y, s);
-      r.z = bf16_pair_to_half_pair(r.z, s);
-      r.w = bf16_pair_to_half_pair(r.w, s);
-    }
-    // even k: x0 x2 x4 x6 (low halves), odd k: x1 x3 x5 x7 (high halves)
-    float se = half_bits_to_float(static_cast<uint16_t>(r.x)) +
-               half_bits_to_float(static_cast<uint16_t>(r.y)) +
-               half_bits_to_float(static_cast<uint16_t>(r.z)) +
-               half_bits_to_float(static_cast<uint16_t>(r.w));
-    float so = half_bits_to_float(static_cast<uint16_t>(r.x >> 16)) +
-               half_bits_to_float(static_cast<uint16_t>(r.y >> 16)) +
-               half_bits_to_float(static_cast<uint16_t>(r.z >> 16)) +
-               half_bits_to_float(static_cast<uint16_t>(r.w >> 16));
-    se = group_sum<U>(se);
-    so = group_sum<U>(so);
-    {
-      // The odd-position partners (high nibbles, unpacked as 1024 + 16 q) are staged divided by
-      // 16, exact in fp16 (values below 2^-10 become subnormal and keep fewer bits), so both
-      // nibble positions accumulate into one sum: (1024 + q) x_e + (64 + q) x_o.
-      uint4 xp = pair_activations(r);
-      const half2_t sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
-      xp.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, xp.y) * sixteenth);
-      xp.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, xp.w) * sixteenth);
-      sm.xs[m][gl][w] = xp;
-      if (w % U == 0) {
-        // The offset terms of the epilogue divided by alpha, per (row, group, quarter):
-        // kNativeSym (beta = -8 alpha): -1032 S_e - 72 S_o; kNativeAsym: -1024 S_e - 64 S_o,
-        // plus S_e + S_o for the beta * S term.
-        sm.sums[m][gl][w / U] = F == PacketFormat::kNativeSym
-                                    ? make_float2(fmaf(-1032.0f, se, -72.0f * so), 0.0f)
-                                    : make_float2(fmaf(-1024.0f, se, -64.0f * so), se + so);
-      }
-      if (w == 0) {
-        sm.scale[m][gl] = undo;
-      }
-    }
+    native_stage_unit<G, A, F>(sm, r, m, gl, w);
   }
 }
 
-template <int G, Act A, int MT, PacketFormat F>
-__device__ __forceinline__ void native_compute_group(const NativeSmem<G, MT>& sm,
+template <int G, Act A, int MT, PacketFormat F, class S>
+__device__ __forceinline__ void native_compute_group(const S& sm,
                                                      const NativeLoad<G>& ld, int gl, int t,
                                                      uint32_t mask_lo, uint32_t mask_hi,
                                                      float (&y)[MT][2]) {
   constexpr int U = native_unit_words(G);
-  constexpr uint32_t kBias = 0x64006400u;  // fp16 1024.0 pair
-  // One accumulator per (row, column): with the odd activations staged / 16 both nibble
+  // One accumulator per (row, column): with the odd nibbles unpacked as 64 + q both nibble
   // positions add into it. A single row keeps a second one so that the dependent dot2 chains are
   // interleaved in pairs.
   constexpr int kAcc = MT == 1 ? 2 : 1;
@@ -311,7 +316,7 @@ __device__ __forceinline__ void native_compute_group(const NativeSmem<G, MT>& sm
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
     // The offset term divided by alpha seeds the accumulator (see native_stage_store).
-    const float seed = sm.sums[m][gl][t].x;
+    const float seed = sm.sums_at(m, gl, t).x;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       acc[m][i][0] = seed;
@@ -327,14 +332,14 @@ __device__ __forceinline__ void native_compute_group(const NativeSmem<G, MT>& sm
     for (int i = 0; i < 2; ++i) {
       const uint32_t wv = unit_word<G>(ld, i, j);
       const uint32_t w8 = wv >> 8;
-      e0[i] = (wv & mask_lo) | kBias;  // 1024+q for k0,k4
-      o0[i] = (wv & mask_hi) | kBias;  // 1024+16q for k1,k5
-      e1[i] = (w8 & mask_lo) | kBias;  // k2,k6
-      o1[i] = (w8 & mask_hi) | kBias;  // k3,k7
+      e0[i] = (wv & mask_lo) | kBiasLow;   // 1024+q for k0,k4
+      o0[i] = (wv & mask_hi) | kBiasHigh;  // 64+q for k1,k5
+      e1[i] = (w8 & mask_lo) | kBiasLow;   // k2,k6
+      o1[i] = (w8 & mask_hi) | kBiasHigh;  // k3,k7
     }
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-      const uint4 xp = sm.xs[m][gl][U * t + j];
+      const uint4 xp = sm.x_at(m, gl, U * t + j);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         float& a0 = acc[m][i][0];
@@ -367,13 +372,13 @@ __device__ __forceinline__ void native_compute_group(const NativeSmem<G, MT>& sm
         // the staged activations carry a power-of-two scale per (row, group)
         float t_sum = a * sum;
         if constexpr (F == PacketFormat::kNativeAsym) {
-          t_sum = fmaf(b, sm.sums[m][gl][t].y, t_sum);
+          t_sum = fmaf(b, sm.sums_at(m, gl, t).y, t_sum);
         }
-        y[m][i] = fmaf(t_sum, sm.scale[m][gl], y[m][i]);
+        y[m][i] = fmaf(t_sum, sm.scale_at(m, gl), y[m][i]);
       } else {
         y[m][i] = fmaf(a, sum, y[m][i]);
         if constexpr (F == PacketFormat::kNativeAsym) {
-          y[m][i] = fmaf(b, sm.sums[m][gl][t].y, y[m][i]);
+          y[m][i] = fmaf(b, sm.sums_at(m, gl, t).y, y[m][i]);
         }
       }
     }

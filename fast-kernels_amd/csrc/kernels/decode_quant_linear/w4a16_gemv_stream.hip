@@ -1,0 +1,267 @@
+// W4A16 GEMV over native slabs for one activation row: the persistent "stream" schedule.
+//
+// The native slabs of a buffer are laid out [slice][group] (w4a16_device.h), so the slices
+// b * whole .. (b + 1) * whole - 1 are one contiguous byte range. When the 32-column slices divide
+// evenly over one workgroup per CU (Llama-70B o, gate_up and down: 256, 1792 and 256 slices on
+// 256 CUs), workgroup b streams that range without a break:
+//
+//  * The whole activation row is staged in LDS once per workgroup (dynamic LDS: K/G groups of
+//    re-paired fp16 values and per-quarter sums, as native_stage_unit writes them) instead of
+//    once per slice and chunk. Wave w only ever computes groups g = w (mod 8), so each wave
+//    stages its own groups and no workgroup barrier separates staging from streaming. Staging
+//    is spread over the first slice: one pass of the wave's groups before its first block, one
+//    more after each block, so that the first weights are consumed as soon as they arrive.
+//  * The staging loads are issued before the first weight loads, so the conversion overlaps
+//    the weights' HBM latency (the load counter retires in order, so waiting for the activations
+//    does not wait for the weights behind them).
+//  * Wave w takes slabs w, w + 8, w + 16, ... of the range through D register buffers, and the
+//    pipeline runs across slice boundaries: the loads of the next slice's first slabs are in
+//    flight while a slice is reduced, so the stream does not drain at each slice as it does when
+//    every slice is its own workgroup run.
+//  * At a slice boundary each wave folds its lane partials over the column's four quarters,
+//    writes them to one of two LDS slots and meets the others at a barrier (its loads stay in
+//    flight); one wave, rotating with the slice, adds the eight waves' totals in wave order and
+//    writes the 32 outputs. No slice is shared, so there is no fix-up and no workspace.
+//
+// Math per group is native_compute_group's (w4a16_gemv_native.h); results equal the per-slice
+// kernel's up to fp32 summation order across waves.
+#include "w4a16_gemv_native.h"
+
+namespace fk {
+namespace {
+
+// LDS view of a whole staged activation row: xs [NG][G/8] re-paired fp16 words, sums [NG][4]
+// per-quarter offset terms, scale [NG] bf16 staging scales (the layout of NativeSmem for one row
+// and every group of K).
+template <int G>
+struct StreamLds {
+  uint4* xs;
+  float2* sums;
+  float* scale;
+
+  __device__ uint4 x_at(int, int gl, int i) const { return xs[gl * (G / 8) + i]; }
+  __device__ float2 sums_at(int, int gl, int t) const { return sums[gl * 4 + t]; }
+  __device__ float scale_at(int, int gl) const { return scale[gl]; }
+  __device__ void set_x(int, int gl, int i, uint4 v) { xs[gl * (G / 8) + i] = v; }
+  __device__ void set_sums(int, int gl, int t, float2 v) { sums[gl * 4 + t] = v; }
+  __device__ void set_scale(int, int gl, float v) { scale[gl] = v; }
+};
+
+// kW waves per workgroup, D register buffers (slabs in flight) per wave: kW * D slabs of 2 KB
+// (G = 128) or 1 KB (G = 64) in flight per workgroup, one workgroup per CU. kStageSlots passes
+// of 64 / (G / 8) groups per wave stage K <= kStageSlots * 64 * kW * 8 activations.
+template <int G, Act A, PacketFormat F, int kStageSlots, int kW, int D>
+__global__ void __launch_bounds__(64 * kW, 1) w4a16_gemv_stream_kernel(GemvParams p) {
+  extern __shared__ uint4 stream_lds[];
+  __shared__ float red[2][kW][kSliceCols];
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int t = lane / 16;
+  const uint32_t mask_lo = vgpr_constant(0x000f000fu);
+  const uint32_t mask_hi = vgpr_constant(0x00f000f0u);
+  const size_t stride = static_cast<size_t>(format_packet_stride(G, F));
+  const int grid = static_cast<int>(gridDim.x);
+  int b = static_cast<int>(blockIdx.x);
+  // Consecutive logical workgroups on one XCD (the hardware deals workgroup b to XCD b % 8).
+  if (p.xcd_remap) {
+    b = (b & 7) * (grid >> 3) + (b >> 3);
+  }
+  const uint32_t ng = static_cast<uint32_t>(p.NG);
+  const int whole = p.stream_whole;
+
+  StreamLds<G> sm;
+  sm.xs = stream_lds;
+  // K/G groups and one spare group slot (stage_one)
+  sm.sums = reinterpret_cast<float2*>(stream_lds + static_cast<size_t>(p.NG + 1) * (G / 8));
+  sm.scale = reinterpret_cast<float*>(sm.sums + static_cast<size_t>(p.NG + 1) * 4);
+
+  // This wave's slabs: u0 + wave + kW j, j < n_w. Past its last slab a wave re-reads that slab,
+  // so every buffer slot is loaded unconditionally (and never past the range).
+  const uint32_t u0 = static_cast<uint32_t>(b) * static_cast<uint32_t>(whole) * ng;
+  const int n_blk = static_cast<int>(ng) / (kW * D);  // blocks of D slabs per wave and slice
+  const int n_w = whole * n_blk * D;
+  const int j_last = n_w - 1;
+  const uint8_t* base = p.packets + static_cast<size_t>(u0 + wave) * stride;
+  const size_t step = static_cast<size_t>(kW) * stride;
+
+  // Activations: every pass's loads first. Pass i stages groups wave + kW (i * 64 / WR + l / WR)
+  // (lane l, word row l % WR); pass 0 before the first block, one more after each block of the
+  // first slice (pass i covers the wave's slabs 64 / WR * i .. of a slice, and a block needs D of
+  // them), and any left after it.
+  constexpr int WR = G / 8;
+  constexpr int kGroupsPerPass = 64 / WR;
+  const int n_pass = (p.NG / kW + kGroupsPerPass - 1) / kGroupsPerPass;
+  uint4 raw[kStageSlots];
+#pragma unroll
+  for (int i = 0; i < kStageSlots; ++i) {
+    // clamped and unconditional (a load under a branch waits for the one before it); slots past
+    // the wave's passes and groups past the row are never staged
+    const int g = min(wave + kW * (i * kGroupsPerPass + lane / WR), p.NG - 1);
+    raw[i] = *reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(g) * G + (lane % WR) * 8);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  NativeLoad<G> buf[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    native_load<G, F>(buf[d], base + static_cast<size_t>(min(d, j_last)) * step, lane);
+    __builtin_amdgcn_sched_barrier(0);  // the same issue order as the refills in the loop
+  }
+  int staged = 0;
+  // Stages the next pass from raw[0] and shifts the slots down (register moves; a runtime slot
+  // index would put the slots in scratch memory).
+  auto stage_one = [&]() {
+    // Groups past the row (the wave's last pass may be partial) are staged into a spare group
+    // slot past the row's, so the staging has no branch.
+    const int g = min(wave + kW * (staged * kGroupsPerPass + lane / WR), p.NG);
+    native_stage_unit<G, A, F>(sm, raw[0], 0, g, lane % WR);
+#pragma unroll
+    for (int i = 0; i + 1 < kStageSlots; ++i) {
+      raw[i] = raw[i + 1];
+    }
+    ++staged;
+    // The wave reads back only what it wrote: its LDS accesses complete in order, so a
+    // wave-scope fence (no instruction) is all that keeps the compiler from hoisting the reads.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  stage_one();
+
+  float y[1][2] = {{0.0f, 0.0f}};
+  int j = 0;  // the wave's next slab to compute
+  // A block of D slabs of slice-local groups gl0 .., kW apart. Each slice gives every wave n_blk
+  // whole blocks (the host plans K/G as a multiple of kW * D), so the block loops have no branch:
+  // the compiler's wait for a buffer is then the in-order count of the loads issued after it,
+  // not a drain of the pipeline.
+  auto block = [&](int gl0) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      native_compute_group<G, A, 1, F>(sm, buf[d], gl0 + kW * d, t, mask_lo, mask_hi, y);
+      native_load<G, F>(buf[d], base + static_cast<size_t>(min(j + d + D, j_last)) * step, lane);
+      // Issue the refill here, not after the block's later slabs: the scheduler would otherwise
+      // sink every load below the block's arithmetic and drain the pipeline once per block.
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    j += D;
+  };
+  for (int r = 0; r < whole; ++r) {
+    // Blocks that each stage one more pass, then blocks that do not: two loops, no branch in
+    // either.
+    const int n_staging = min(n_blk, n_pass - staged);
+    int blk = 0;
+    for (; blk < n_staging; ++blk) {
+      block(wave + kW * D * blk);
+      stage_one();
+    }
+    for (; blk < n_blk; ++blk) {
+      block(wave + kW * D * blk);
+    }
+    while (staged < n_pass) {
+      stage_one();
+    }
+
+    // Fold the lane partials over the column's four quarters (lanes n, n+16, n+32, n+48) and
+    // meet the other waves; the loads of the next slice's first slabs stay in flight.
+    float y0 = y[0][0];
+    float y1 = y[0][1];
+    y0 += __shfl_xor(y0, 16);
+    y1 += __shfl_xor(y1, 16);
+    y0 += __shfl_xor(y0, 32);
+    y1 += __shfl_xor(y1, 32);
+    y[0][0] = 0.0f;
+    y[0][1] = 0.0f;
+    const int slot = r & 1;
+    if (lane < 16) {
+      red[slot][wave][lane] = y0;
+      red[slot][wave][lane + 16] = y1;
+    }
+    lds_barrier();
+    // One wave, rotating with the slice, writes it. Slot reuse is safe: slot (r & 1) is written
+    // again only after the next slice's barrier, which this wave reaches after finishing here.
+    if (wave == (r & (kW - 1)) && lane < kSliceCols) {
+      float v = red[slot][0][lane];
+#pragma unroll
+      for (int w = 1; w < kW; ++w) {
+        v += red[slot][w][lane];
+      }
+      const size_t slice = static_cast<size_t>(b) * whole + r;
+      p.out[slice * kSliceCols + lane] = float_to_act_bits<A>(v);
+    }
+  }
+  // Retire the loads of re-read tail slots before the workgroup ends.
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+}
+
+template <int G, Act A, PacketFormat F, int kStageSlots, int kW, int D>
+hipError_t launch_stream_t(const GemvLaunch& l, hipStream_t stream) {
+  int grid = 0;
+  GemvParams p = native_params<G, 1>(l, &grid);
+  p.pair = 0;
+  p.stream_whole = l.stream_whole;
+  grid = l.stream_grid;
+  p.xcd_remap = grid % 8 == 0 ? 1 : 0;
+  const size_t lds = stream_lds_bytes(G, l.K / G + 1);
+  hipLaunchKernelGGL((w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D>), dim3(grid),
+                     dim3(64 * kW), lds, stream, p);
+  return hipGetLastError();
+}
+
+template <int G, Act A, PacketFormat F, int kW, int D>
+hipError_t stream_dispatch_slots(const GemvLaunch& l, hipStream_t stream) {
+  constexpr int kPerPass = 64 * kW * 8;  // activations staged per slot
+  if (l.K <= kPerPass * (16 / kW)) {
+    return launch_stream_t<G, A, F, 16 / kW, kW, D>(l, stream);
+  }
+  if (l.K <= kPerPass * (64 / kW)) {
+    return launch_stream_t<G, A, F, 64 / kW, kW, D>(l, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+// Waves and depth: units_per_workgroup and K / G are multiples of stream_waves * stream_depth
+// (the host plans them so).
+template <int G, Act A, PacketFormat F>
+hipError_t stream_dispatch_waves(const GemvLaunch& l, hipStream_t stream) {
+  constexpr int kUnitKB = G == 128 ? 2 : 1;
+  if (l.stream_waves != kStreamWaves) {
+    return hipErrorInvalidValue;
+  }
+  switch (l.stream_depth * kUnitKB) {
+    case 4: return stream_dispatch_slots<G, A, F, kStreamWaves, 4 / kUnitKB>(l, stream);
+    case 8: return stream_dispatch_slots<G, A, F, kStreamWaves, 8 / kUnitKB>(l, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <PacketFormat F>
+hipError_t stream_dispatch(const GemvLaunch& l, hipStream_t stream) {
+  if (l.group_size == 64) {
+    return l.act == Act::kF16 ? stream_dispatch_waves<64, Act::kF16, F>(l, stream)
+                              : stream_dispatch_waves<64, Act::kBF16, F>(l, stream);
+  }
+  return l.act == Act::kF16 ? stream_dispatch_waves<128, Act::kF16, F>(l, stream)
+                            : stream_dispatch_waves<128, Act::kBF16, F>(l, stream);
+}
+
+}  // namespace
+
+hipError_t launch_w4a16_gemv_stream(const GemvLaunch& l, hipStream_t stream) {
+  if (l.mode != GemvMode::kStreamK || l.m_tile != 1 || l.M != 1 || l.fuse != GemvFuse::kNone ||
+      l.slice_cols != kSliceCols || l.slice_pair || l.K > kStreamMaxK || l.stream_depth <= 0 ||
+      l.stream_grid <= 0) {
+    return hipErrorInvalidValue;
+  }
+  // Whole slices only, the same count per workgroup, in blocks of waves * depth units.
+  const int ng = l.K / l.group_size;
+  if (l.stream_whole <= 0 || ng % (l.stream_waves * l.stream_depth) != 0 ||
+      static_cast<long long>(l.stream_whole) * l.stream_grid != l.N / kSliceCols) {
+    return hipErrorInvalidValue;
+  }
+  switch (l.format) {
+    case PacketFormat::kNativeSym: return stream_dispatch<PacketFormat::kNativeSym>(l, stream);
+    case PacketFormat::kNativeAsym: return stream_dispatch<PacketFormat::kNativeAsym>(l, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace fk

@@ -81,7 +81,17 @@ struct ArcW4A16Plan {
   int max_tile_contributors;    // workgroups that can share one slice
   std::size_t workspace_bytes;  // caller workspace needed by arc_w4a16_forward_ex
   int slice_cols;               // columns per workgroup slice of a tile (128, 64 or 32)
+  int schedule;                 // kSchedule*: how the workgroups walk their units
+  int stream_depth;             // kScheduleStream: slabs in flight per wave
+  int stream_whole;             // kScheduleStream: whole slices per workgroup
 };
+
+// Launch schedules of a plan. kScheduleRuns: workgroups stream runs of one slice (or tile) at a
+// time; kSchedulePairs: one-row native plans whose workgroups stream two adjacent whole 32-column
+// slices at once (slice_cols 64); kScheduleStream: one-row native plans on a persistent grid,
+// each workgroup streaming one contiguous range of slabs across slices with the whole activation
+// row staged in LDS (w4a16_gemv_stream.hip).
+enum Schedule : int { kScheduleRuns = 0, kSchedulePairs = 1, kScheduleStream = 2 };
 
 // The launch the GEMV will use for this shape on the current device. split_k_slices = 0 picks
 // the built-in policy; S > 0 gives every workgroup ceil(K / G / S) groups of whole 128-column

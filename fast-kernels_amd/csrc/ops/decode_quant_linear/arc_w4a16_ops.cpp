@@ -12,6 +12,7 @@
 #include <algorithm>
 #include <array>
 #include <cstddef>
+#include <cstdlib>
 #include <cstdint>
 #include <mutex>
 #include <sstream>
@@ -112,6 +113,28 @@ int device_cu_count() {
 }
 
 
+// Largest LDS one workgroup may hold on the current device, read once. A host-only plan (a given
+// CU count) assumes gfx950's 160 KB.
+constexpr std::size_t kGfx950LdsBytes = 160 * 1024;
+
+std::size_t device_lds_per_block() {
+  static std::array<std::size_t, kMaxDevices> cache{};
+  static std::mutex mutex;
+  int device = 0;
+  check_hip(hipGetDevice(&device), "hipGetDevice");
+  if (device < 0 || device >= kMaxDevices) {
+    throw std::runtime_error("device index out of range");
+  }
+  std::lock_guard<std::mutex> lock(mutex);
+  if (cache[device] == 0) {
+    int bytes = 0;
+    check_hip(hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, device),
+              "hipDeviceGetAttribute(maxSharedMemoryPerBlock)");
+    cache[device] = static_cast<std::size_t>(std::max(bytes, 1));
+  }
+  return cache[device];
+}
+
 // Smallest run per workgroup: two groups per wave, so every wave has a buffered group behind
 // the one it computes.
 constexpr int kMinGroupsPerWorkgroup = 8;
@@ -127,6 +150,7 @@ constexpr int kMaxPairK = 4096;
 void finish_plan(ArcW4A16Plan& plan, long long tiles, long long slices, int num_groups,
                  long long per, int n, int batch) {
   plan.slice_cols = static_cast<int>(fk::kTileCols / slices);
+  plan.schedule = kScheduleRuns;
   const long long units = tiles * slices * num_groups;
   const long long workgroups = (units + per - 1) / per;
   if (workgroups > 0x7fffffffLL || per > 0x7fffffffLL) {
@@ -249,12 +273,42 @@ ArcW4A16Plan plan_arc_impl(int batch, int n, int k, int group_size, int activati
   return plan;
 }
 
+// Stream schedule switches, read once: FK_W4A16_STREAM=0 turns it off (the per-slice runs then
+// serve one-row native plans), FK_W4A16_STREAM_WPC=2 runs two workgroups per CU.
+bool stream_schedule_enabled() {
+  static const bool enabled = [] {
+    const char* v = std::getenv("FK_W4A16_STREAM");
+    return v == nullptr || std::string(v) != "0";
+  }();
+  return enabled;
+}
+
+// FK_W4A16_STREAM_KB=4|8 pins the weights in flight per wave (else the plan's choice).
+int stream_kb_override() {
+  static const int kb = [] {
+    const char* v = std::getenv("FK_W4A16_STREAM_KB");
+    const int n = v == nullptr ? 0 : std::atoi(v);
+    return n == 4 || n == 8 ? n : 0;
+  }();
+  return kb;
+}
+
+int stream_workgroups_per_cu() {
+  static const int wpc = [] {
+    const char* v = std::getenv("FK_W4A16_STREAM_WPC");
+    const int n = v == nullptr ? 1 : std::atoi(v);
+    return n >= 1 && n <= 4 ? n : 1;
+  }();
+  return wpc;
+}
+
 // plan_w4a16_for_format for a kernel choice (kKernelDot2 is what the fused kernels need).
 ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int activation_dtype,
                                   int split_k_slices, int cu_count, int packet_format,
-                                  int kernel, bool allow_pair = true) {
+                                  int kernel, bool plain = true) {
   const fk::PacketFormat format = to_packet_format(packet_format, true);
   validate_dimensions(batch, n, k, group_size);
+  const bool cu_count_given = cu_count > 0;
   if (cu_count == 0) {
     cu_count = device_cu_count();
   }
@@ -295,13 +349,43 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
   // 7B gate_up (688 slices, 344 pairs) got 1 us slower, pairs that leave part of the chip idle
   // (70B o, 256 slices) 3 us slower, and with longer K, whose single-slice runs already stream
   // 135 KB, pairs gain nothing (70B qkv, K = 8192: 12.12 -> 12.20 us).
-  if (allow_pair && split_k_slices == 0 && per == num_groups && plan.m_tile == 1 &&
+  // The stream schedule (w4a16_gemv_stream.hip): one activation row, K staged whole in LDS, and
+  // the slices dividing evenly over one workgroup per CU, each workgroup streaming its share of
+  // whole slices as one contiguous range. The weights in flight per wave: 4 KB (32 KB per CU), or
+  // what FK_W4A16_STREAM_KB pins. Measured on MI355X (bench, Llama-70B bf16): o 8.07 -> 7.73 us,
+  // down 22.6 -> 21.3, gate_up 39.6 -> 39.8 (equal within the run-to-run spread); 8 and 16 KB
+  // per wave are slower (gate_up 39.9 and 41.5 us). Shapes whose slices do not divide evenly
+  // stay on the per-slice runs: cutting the remainder slices into K pieces finished by a
+  // cross-workgroup hand-off measured slower everywhere (8B down 8.7 -> 20.7 us, 7B o 4.6 -> 6.0).
+  if (plain && split_k_slices == 0 && batch == 1 && plan.m_tile == 1 &&
+      k <= fk::kStreamMaxK && stream_schedule_enabled()) {
+    const std::size_t lds =
+        fk::stream_lds_bytes(group_size, num_groups + 1) + fk::kStreamStaticLdsBytes;
+    const std::size_t lds_limit = cu_count_given ? kGfx950LdsBytes : device_lds_per_block();
+    const int kb = stream_kb_override() != 0 ? stream_kb_override() : 4;
+    const int depth = fk::stream_depth_for_kb(group_size, kb);
+    const int quantum = fk::kStreamWaves * depth;
+    const long long grid = static_cast<long long>(cu_count) * stream_workgroups_per_cu();
+    if (num_groups % quantum == 0 && lds <= lds_limit && slices >= grid && slices % grid == 0) {
+      plan.schedule = kScheduleStream;
+      plan.slice_cols = fk::kSliceCols;
+      plan.workgroups = static_cast<int>(grid);
+      plan.stream_depth = depth;
+      plan.stream_whole = static_cast<int>(slices / grid);
+      plan.groups_per_workgroup = plan.stream_whole * num_groups;
+      plan.max_tile_contributors = 1;
+      plan.workspace_bytes = 0;
+      return plan;
+    }
+  }
+  if (plain && split_k_slices == 0 && per == num_groups && plan.m_tile == 1 &&
       k <= kMaxPairK) {
     const long long rounds = (slices + cu_count - 1) / cu_count;
     const long long pair_rounds = (slices / 2 + cu_count - 1) / cu_count;
     if (rounds >= 2 * pair_rounds) {
       finish_plan(plan, fk::gemv_tiles(n, batch, plan.m_tile), fk::kSlicesPerTile / 2,
                   num_groups, per, n, batch);
+      plan.schedule = kSchedulePairs;
       return plan;
     }
   }
@@ -385,12 +469,26 @@ void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::u
   l.units_per_workgroup = plan.groups_per_workgroup;
   l.max_contributors = plan.max_tile_contributors;
   l.slice_cols = plan.slice_cols;
-  if (format != fk::PacketFormat::kArc && plan.m_tile != fk::kMfmaRows &&
-      plan.slice_cols == 2 * fk::kSliceCols) {
-    // Native slice pairs: the kernel counts its units in 32-column slices.
+  if (plan.schedule == kSchedulePairs) {
+    // Native slice pairs: the kernel counts its units in 32-column slices, and every run is a
+    // whole pair over all of K.
+    if (format == fk::PacketFormat::kArc || plan.m_tile != 1 ||
+        plan.slice_cols != 2 * fk::kSliceCols || plan.groups_per_workgroup != k / group_size) {
+      throw std::logic_error("slice-pair schedule on a plan that is not one row of whole pairs");
+    }
     l.slice_cols = fk::kSliceCols;
     l.slice_pair = true;
     l.units_per_workgroup = 2 * plan.groups_per_workgroup;
+  } else if (plan.schedule == kScheduleStream) {
+    if (format == fk::PacketFormat::kArc || batch != 1 || plan.slice_cols != fk::kSliceCols ||
+        fuse != fk::GemvFuse::kNone) {
+      throw std::logic_error("stream schedule on a plan that is not one unfused native row");
+    }
+    l.stream = true;
+    l.stream_waves = fk::kStreamWaves;
+    l.stream_depth = plan.stream_depth;
+    l.stream_grid = plan.workgroups;
+    l.stream_whole = plan.stream_whole;
   }
   l.format = format;
   l.fuse = fuse;
@@ -853,7 +951,7 @@ ArcW4A16Plan plan_w4a16_rmsnorm(int batch, int n, int k, int group_size, int act
                                 int split_k_slices, int cu_count, int packet_format) {
   to_packet_format(packet_format, false);
   return plan_for_format_impl(batch, n, k, group_size, activation_dtype, split_k_slices, cu_count,
-                              packet_format, kKernelDot2, /*allow_pair=*/false);
+                              packet_format, kKernelDot2, /*plain=*/false);
 }
 
 void arc_w4a16_forward_silu_mul(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,

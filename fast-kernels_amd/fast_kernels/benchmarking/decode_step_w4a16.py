@@ -80,6 +80,25 @@ def run_decode_step_w4a16_suite(suite: BenchmarkSuite) -> tuple[list[BenchmarkCa
     return cases, notes
 
 
+def layer_weights(torch: Any, device: Any, n: int, k: int, group_size: int, layer: int) -> tuple:
+    """One projection's int4 weights in one layer of the stack: (q_u8 [n, k/2], alpha fp16
+    [n, k/G], beta = -8 alpha fp16), drawn on the device from a generator seeded by the case seed
+    and the layer index, so that every layer is distinct and any layer can be rebuilt alone."""
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed_for_case(1, n, k, group_size) * 131 + layer)
+    q = torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device=device, generator=gen)
+    alpha = torch.empty((n, k // group_size), device=device).uniform_(0.001, 0.02, generator=gen).half()
+    beta = (alpha.float() * -8.0).half()
+    return q, alpha, beta
+
+
+def step_activations(torch: Any, device: Any, ks: list[int], act_dtype: Any) -> dict[int, Any]:
+    """The step's activation rows, one per distinct K, x ~ N(0, 1) in the activation dtype."""
+    gen = torch.Generator(device=device)
+    gen.manual_seed(12345)
+    return {k: torch.randn((1, k), device=device, generator=gen).to(act_dtype) for k in sorted(set(ks))}
+
+
 LAYER_UNFUSED = "decode_step_layers_unfused"
 LAYER_FUSED = "decode_step_layers_fused"
 
@@ -183,21 +202,13 @@ def _run_stack(torch: Any, suite: BenchmarkSuite, dtype: str, layout: str, layer
         keep_raw = {0, layers - 1}
         for layer in range(layers):
             for name, n, k, _ in shapes:
-                gen = torch.Generator(device=device)
-                gen.manual_seed(seed_for_case(1, n, k, group_size) * 131 + layer)
-                q = torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device=device, generator=gen)
-                alpha = torch.empty((n, k // group_size), device=device).uniform_(
-                    0.001, 0.02, generator=gen).half()
-                beta = (alpha.float() * -8.0).half()
+                q, alpha, beta = layer_weights(torch, device, n, k, group_size, layer)
                 packets = pack_arc_w4a16_packets(q, alpha, beta, group_size=group_size)
                 weights[(layer, name)] = (packets, q, alpha, beta) if layer in keep_raw else (packets, None, None, None)
                 if native_id is not None:
                     slabs[(layer, name)] = convert_arc_to_native_packets(
                         packets, n=n, k=k, group_size=group_size, packet_format="native_sym")
-        gen = torch.Generator(device=device)
-        gen.manual_seed(12345)
-        xs = {k: torch.randn((1, k), device=device, generator=gen).to(act_dtype)
-              for k in sorted({k for _, _, k, _ in shapes})}
+        xs = step_activations(torch, device, [k for _, _, k, _ in shapes], act_dtype)
         outs = {(layer, name): torch.empty((1, n), device=device, dtype=act_dtype)
                 for layer in range(layers) for name, n, _, _ in shapes}
         stream = torch.cuda.Stream()

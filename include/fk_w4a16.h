@@ -107,7 +107,17 @@ typedef struct fk_arc_w4a16_plan {
   int max_tile_contributors; /* workgroups that can share one slice (1 = none shared) */
   size_t workspace_bytes;    /* workspace fk_arc_w4a16_forward_ex needs */
   int slice_cols;            /* columns of a tile per workgroup slice: 128, 64 or 32 */
+  int schedule;              /* FK_SCHEDULE_*: how the workgroups walk their units */
 } fk_arc_w4a16_plan;
+
+/* Plan schedules. FK_SCHEDULE_RUNS: each workgroup streams runs of one slice (or tile) at a time.
+ * FK_SCHEDULE_PAIRS: one-row native plans, each workgroup streams two adjacent whole 32-column
+ * slices at once (slice_cols 64). FK_SCHEDULE_STREAM: one-row native plans on a persistent grid
+ * (workgroups = CUs): each workgroup streams one contiguous range of groups_per_workgroup slabs
+ * across slice boundaries, with the whole activation row staged in LDS (K <= 32768). */
+#define FK_SCHEDULE_RUNS 0
+#define FK_SCHEDULE_PAIRS 1
+#define FK_SCHEDULE_STREAM 2
 
 /* Launch plan for a shape. split_k_slices = 0 selects the built-in policy (one resident round of
  * equal runs); S > 0 gives every workgroup ceil(K/G/S) groups. cu_count = 0 queries the current

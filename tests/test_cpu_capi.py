@@ -54,6 +54,7 @@ class Plan(ctypes.Structure):
         ("max_tile_contributors", ctypes.c_int),
         ("workspace_bytes", ctypes.c_size_t),
         ("slice_cols", ctypes.c_int),
+        ("schedule", ctypes.c_int),
     ]
 
 
@@ -210,31 +211,34 @@ def test_native_format_validation_without_gpu(lib: ctypes.CDLL) -> None:
 @pytest.mark.parametrize(
     "shape,want",
     [
-        # (batch, n, k, G) -> (slice_cols, groups per workgroup, workgroups) on 256 CUs
-        ((1, 8192, 8192, 128), (32, 64, 256)),      # 256 slices, each over all of K
-        ((1, 10240, 8192, 128), (32, 64, 320)),     # pairs would fill as evenly, but K is long
-        ((1, 10240, 4096, 128), (64, 32, 160)),     # 320 slices in 160 pairs
-        ((1, 12288, 4096, 128), (64, 32, 192)),     # 7B qkv: 384 slices in 192 pairs
-        ((1, 28672, 4096, 128), (64, 32, 448)),     # 8B gate_up: 896 slices in 448 pairs
-        ((1, 22016, 4096, 128), (32, 32, 688)),     # 7B gate_up: 344 pairs would fill 2 rounds unevenly
-        ((2, 12288, 4096, 128), (32, 32, 384)),     # pairs for one row only
-        ((1, 57344, 8192, 128), (32, 64, 1792)),    # more slices than resident workgroups
-        ((1, 8192, 28672, 128), (32, 112, 512)),    # long K: two runs of 112, two per CU
-        ((1, 4096, 4096, 128), (32, 32, 128)),      # half the CUs idle, but K is short
-        ((1, 4096, 14336, 128), (32, 56, 256)),     # 128 slices, 112 groups: two runs of 56
-        ((4, 14336, 4096, 64), (32, 64, 448)),      # four rows share a slice's runs
-        ((16, 14336, 4096, 64), (128, 16, 448)),    # matrix cores: the reference-format plan
+        # (batch, n, k, G) -> (slice_cols, groups per workgroup, workgroups, schedule) on 256 CUs
+        # schedule 0: per-slice runs, 1: slice pairs, 2: stream (whole slices per CU, one range)
+        ((1, 8192, 8192, 128), (32, 64, 256, 2)),      # 256 slices: one per CU, streamed
+        ((1, 10240, 8192, 128), (32, 64, 320, 0)),     # 320 slices do not divide over 256 CUs
+        ((1, 10240, 4096, 128), (64, 32, 160, 1)),     # 320 slices in 160 pairs
+        ((1, 12288, 4096, 128), (64, 32, 192, 1)),     # 7B qkv: 384 slices in 192 pairs
+        ((1, 28672, 4096, 128), (64, 32, 448, 1)),     # 8B gate_up: 896 slices in 448 pairs
+        ((1, 22016, 4096, 128), (32, 32, 688, 0)),     # 7B gate_up: 344 pairs would fill 2 rounds unevenly
+        ((2, 12288, 4096, 128), (32, 32, 384, 0)),     # pairs for one row only
+        ((1, 57344, 8192, 128), (32, 448, 256, 2)),    # 70B gate_up: 7 whole slices per CU
+        ((1, 8192, 28672, 128), (32, 224, 256, 2)),    # 70B down: one slice of 224 groups per CU
+        ((1, 8192, 28672 + 128, 128), (32, 113, 510, 0)),  # 225 groups: not a multiple of 16
+        ((1, 4096, 4096, 128), (32, 32, 128, 0)),      # half the CUs idle, but K is short
+        ((1, 4096, 14336, 128), (32, 56, 256, 0)),     # 128 slices, 112 groups: two runs of 56
+        ((4, 14336, 4096, 64), (32, 64, 448, 0)),      # four rows share a slice's runs
+        ((16, 14336, 4096, 64), (128, 16, 448, 0)),    # matrix cores: the reference-format plan
     ],
 )
 def test_native_plan_policy_without_gpu(lib: ctypes.CDLL, shape, want) -> None:
     batch, n, k, g = shape
     p = Plan()
     assert lib.fk_w4a16_plan_for_format(batch, n, k, g, 0, 0, 256, 1, ctypes.byref(p)) == 0
-    assert (p.slice_cols, p.groups_per_workgroup, p.workgroups) == want
+    assert (p.slice_cols, p.groups_per_workgroup, p.workgroups, p.schedule) == want
     arc = Plan()
     assert lib.fk_w4a16_plan_for_format(batch, n, k, g, 0, 0, 256, 0, ctypes.byref(arc)) == 0
     rc, ref = _plan(lib, batch, n, k, g)
     assert rc == 0 and (arc.slice_cols, arc.workgroups) == (ref.slice_cols, ref.workgroups)
+    assert arc.schedule == 0
     # a fix-up needs a workspace exactly when runs do not cover whole slices
     assert (p.workspace_bytes > 0) == (p.groups_per_workgroup % (k // g) != 0)
 

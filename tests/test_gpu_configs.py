@@ -1,0 +1,199 @@
+"""GPU parity at the benchmark configurations' exact shapes, against the CPU oracle.
+
+  * configuration 2 (Llama-70B layer, M = 1, bf16): the four projections over native symmetric
+    slabs with the automatic plan, i.e. exactly the launches bench.py times (the stream schedule
+    for o, gate_up and down, per-slice runs for qkv), and over the reference packets;
+  * configuration 3 (N = 14336, K = 4096, G = 64, asymmetric, fp16, M = 2, 4, 8, 16): the
+    automatic dispatch and both forced kernels (dot2 loop, matrix cores), over the reference
+    packets and the native asymmetric slabs, every output against the oracle;
+  * configuration 4 (the 32-layer Llama-8B decode step, bf16): the stack built as the
+    decode-step runner builds it (distinct seeded weights per layer, native slabs), all 128
+    GEMVs captured in one HIP graph and replayed twice, the outputs of layers 0, 15 and 31 of
+    every projection against the oracle.
+
+Like the reference's suite runner (decode_linear_w4a16.py:497-521), which gates every shape on
+the explicit formula before timing it. Bar: the GEMV bar of the other parity tests
+(rel 1e-2, abs 1e-2 * sqrt(K) * max|alpha|, test_gpu_w4a16_parity._assert_gemv_close).
+"""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+
+from conftest import gpu_available
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not gpu_available(), reason="needs a GPU"),
+]
+
+torch = pytest.importorskip("torch")
+
+from fast_kernels.benchmarking.decode_step_w4a16 import layer_weights, step_activations  # noqa: E402
+from fast_kernels.benchmarking.inputs import make_case  # noqa: E402
+from fast_kernels.native import native_module  # noqa: E402
+from fast_kernels.ops import (  # noqa: E402
+    arc_w4a16_forward_native,
+    arc_w4a16_plan,
+    convert_arc_to_native_packets,
+    pack_arc_w4a16_packets,
+)
+from oracle import oracle  # noqa: E402
+from test_gpu_w4a16_parity import _assert_gemv_close, _bits, _upload  # noqa: E402
+
+DEV = "cuda"
+
+LLAMA70B = [("qkv", 10240, 8192), ("o", 8192, 8192), ("gate_up", 57344, 8192),
+            ("down", 8192, 28672)]
+LLAMA8B = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096),
+           ("down", 4096, 14336)]
+
+
+def _rows(n: int) -> np.ndarray:
+    """Every row up to 10240; for the larger shapes the first and last 1024 rows and 2048 spread
+    between (each 32-column slice of a stream workgroup's range is covered at both ends)."""
+    if n <= 10240:
+        return np.arange(n)
+    mid = np.linspace(1024, n - 1025, 2048).astype(int)
+    return np.unique(np.concatenate([np.arange(1024), mid, np.arange(n - 1024, n)]))
+
+
+def _oracle_rows(case, rows: np.ndarray, act: str) -> np.ndarray:
+    ref, _ = oracle.gemv(case.x, np.ascontiguousarray(case.q_u8[rows]),
+                         np.ascontiguousarray(case.alpha[rows]),
+                         np.ascontiguousarray(case.beta[rows]), case.group_size, act)
+    return ref
+
+
+@pytest.mark.parametrize("packets", ["native_sym", "arc"])
+@pytest.mark.parametrize("name,n,k", LLAMA70B)
+def test_config2_llama70b_bf16_as_benchmarked(name: str, n: int, k: int, packets: str) -> None:
+    case = make_case(1, n, k, 128, act="bf16")
+    x, q, a, b = _upload(case)
+    arc = pack_arc_w4a16_packets(q, a, b, group_size=128)
+    code = 1 if packets == "native_sym" else 0
+    slabs = arc if code == 0 else convert_arc_to_native_packets(arc, n=n, k=k, group_size=128)
+    plan = arc_w4a16_plan(batch=1, n=n, k=k, group_size=128, activation_dtype=torch.bfloat16,
+                          packet_format=code)
+    if code == 1 and torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert plan["schedule"] == (0 if name == "qkv" else 2), plan
+    y = arc_w4a16_forward_native(x, slabs, n=n, k=k, group_size=128, packet_format=packets)
+    torch.cuda.synchronize()
+    rows = _rows(n)
+    _assert_gemv_close(_bits(y)[:, rows], _oracle_rows(case, rows, "bf16"), case,
+                       f"70B {name} {packets} plan={plan}")
+
+
+_CONFIG3_REF: dict[int, tuple] = {}
+
+
+def _config3_case(batch: int):
+    if batch not in _CONFIG3_REF:
+        case = make_case(batch, 14336, 4096, 64, act="f16", asymmetric=True)
+        ref, _ = oracle.gemv(case.x, case.q_u8, case.alpha, case.beta, 64, "f16")
+        _CONFIG3_REF.clear()
+        _CONFIG3_REF[batch] = (case, ref)
+    return _CONFIG3_REF[batch]
+
+
+@pytest.mark.parametrize("batch", [2, 4, 8, 16])
+@pytest.mark.parametrize("kernel", [0, 1, 2])  # automatic, dot2 loop, matrix cores
+@pytest.mark.parametrize("packets", ["native_asym", "arc"])
+def test_config3_small_batch_every_kernel(batch: int, kernel: int, packets: str) -> None:
+    case, ref = _config3_case(batch)
+    n, k, g = 14336, 4096, 64
+    x, q, a, b = _upload(case)
+    arc = pack_arc_w4a16_packets(q, a, b, group_size=g)
+    code = 2 if packets == "native_asym" else 0
+    slabs = arc if code == 0 else convert_arc_to_native_packets(arc, n=n, k=k, group_size=g,
+                                                                packet_format="native_asym")
+    plan = arc_w4a16_plan(batch=batch, n=n, k=k, group_size=g, activation_dtype=torch.float16,
+                          packet_format=code, kernel=kernel)
+    ws = torch.zeros(max(1, plan["workspace_bytes"]) + 256, device=DEV, dtype=torch.uint8)
+    y = torch.empty((batch, n), device=DEV, dtype=torch.float16)
+    native_module().w4a16_forward_kernel(
+        x.data_ptr(), slabs.data_ptr(), y.data_ptr(), ws.data_ptr(), ws.numel(), batch, n, k, g,
+        code, 0, 0, kernel, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    _assert_gemv_close(_bits(y), ref, case, f"config 3 M={batch} kernel={kernel} {packets}")
+
+
+def test_config4_llama8b_decode_step_graph() -> None:
+    layers, g = 32, 128
+    dev = torch.device(DEV)
+    checked = (0, 15, 31)
+    slabs, host = {}, {}
+    for layer in range(layers):
+        for name, n, k in LLAMA8B:
+            q, alpha, beta = layer_weights(torch, dev, n, k, g, layer)
+            arc = pack_arc_w4a16_packets(q, alpha, beta, group_size=g)
+            slabs[(layer, name)] = convert_arc_to_native_packets(arc, n=n, k=k, group_size=g)
+            if layer in checked:
+                host[(layer, name)] = (q.cpu().numpy(), alpha.cpu().view(torch.int16).numpy().view(np.uint16),
+                                       beta.cpu().view(torch.int16).numpy().view(np.uint16))
+            del arc, q, alpha, beta
+    xs = step_activations(torch, dev, [k for _, _, k in LLAMA8B], torch.bfloat16)
+    outs = {(layer, name): torch.empty((1, n), device=dev, dtype=torch.bfloat16)
+            for layer in range(layers) for name, n, _ in LLAMA8B}
+
+    def step() -> None:
+        for layer in range(layers):
+            for name, n, k in LLAMA8B:
+                arc_w4a16_forward_native(xs[k], slabs[(layer, name)], n=n, k=k, group_size=g,
+                                         packet_format="native_sym", output=outs[(layer, name)])
+
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        step()  # eager warm-up: plans and workspaces exist before capture
+    torch.cuda.synchronize()
+    eager = {key: _bits(outs[key]) for key in host}
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        step()
+    for replay in range(2):
+        for o in outs.values():
+            o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for (layer, name), (q, alpha, beta) in host.items():
+            n, k = next((n, k) for nm, n, k in LLAMA8B if nm == name)
+            x_bits = _bits(xs[k])
+            ref, _ = oracle.gemv(x_bits, q, alpha, beta, g, "bf16")
+            c = SimpleNamespace(act="bf16", k=k, alpha=alpha)  # the fields the GEMV bar reads
+            got = _bits(outs[(layer, name)])
+            _assert_gemv_close(got, ref, c, f"8B step replay {replay} layer {layer} {name}")
+            np.testing.assert_array_equal(got, eager[(layer, name)])
+
+
+@pytest.mark.parametrize(
+    "n,k,g,act,asym",
+    [
+        (8192, 2048, 128, "f16", False),    # 16 groups: one block of 8 waves x 2 slabs per slice
+        (8192, 4096, 64, "f16", True),      # G = 64: 4 slabs in flight per wave, two blocks
+        (16384, 8192, 128, "bf16", True),   # two whole slices per workgroup, asymmetric
+        (8192, 32768, 128, "bf16", False),  # the longest K the stream schedule stages
+        (8192, 32768, 64, "f16", False),    # 512 groups at G = 64
+    ],
+)
+def test_stream_schedule_variants(n: int, k: int, g: int, act: str, asym: bool) -> None:
+    """The stream schedule (slices dividing over one workgroup per CU) at both group sizes, both
+    activation dtypes, both native formats and the staging slot counts; plus determinism."""
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the shapes are chosen for 256 CUs")
+    case = make_case(1, n, k, g, act=act, asymmetric=asym, seed=n + k + g)
+    x, q, a, b = _upload(case)
+    fmt = "native_asym" if asym else "native_sym"
+    slabs = convert_arc_to_native_packets(pack_arc_w4a16_packets(q, a, b, group_size=g), n=n, k=k,
+                                          group_size=g, packet_format=fmt)
+    plan = arc_w4a16_plan(batch=1, n=n, k=k, group_size=g,
+                          activation_dtype=x.dtype, packet_format=2 if asym else 1)
+    assert plan["schedule"] == 2, plan
+    ys = [_bits(arc_w4a16_forward_native(x, slabs, n=n, k=k, group_size=g, packet_format=fmt))
+          for _ in range(2)]
+    np.testing.assert_array_equal(ys[0], ys[1])
+    rows = _rows(n)
+    _assert_gemv_close(ys[0][:, rows], _oracle_rows(case, rows, act), case, f"stream {plan}")
