@@ -33,6 +33,7 @@ LIB_SOURCES = [
     CSRC / "kernels" / "decode_quant_linear" / "w4a16_gemm_mfma.hip",
     CSRC / "kernels" / "decode_quant_linear" / "w4a16_aux.hip",
     CSRC / "ops" / "decode_quant_linear" / "arc_w4a16_ops.cpp",
+    CSRC / "ops" / "decode_quant_linear" / "w4a16_scratch.hip",
     CSRC / "capi" / "fk_w4a16_capi.cpp",
 ]
 

@@ -255,6 +255,15 @@ int fk_arc_w4a16_forward_native(const void* activations, const void* packets, vo
   });
 }
 
+int fk_w4a16_forward_noalloc(const void* activations, const void* packets, void* output, int batch,
+                             int n, int k, int group_size, int packet_format,
+                             int activation_dtype, void* stream) {
+  return guarded([&] {
+    ops::w4a16_forward_noalloc(P(activations), P(packets), P(output), batch, n, k, group_size,
+                               packet_format, activation_dtype, P(stream));
+  });
+}
+
 int fk_w4a16_plan_rmsnorm(int batch, int n, int k, int group_size, int activation_dtype,
                           int split_k_slices, int cu_count, int packet_format,
                           fk_arc_w4a16_plan* plan) {

@@ -186,4 +186,12 @@ void w4a16_forward_kernel(std::uintptr_t activations_ptr, std::uintptr_t packets
                           int packet_format, int activation_dtype, int split_k_slices, int kernel,
                           std::uintptr_t stream_ptr);
 
+// arc_w4a16_forward_native (automatic plan) with no workspace argument and no allocation: the
+// fix-up scratch is a fixed per-device array (w4a16_scratch.hip), so launches whose plan needs
+// more than kNoAllocScratchBytes are rejected (std::invalid_argument), and calls that overlap on
+// one device race on it.
+void w4a16_forward_noalloc(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
+                           std::uintptr_t output_ptr, int batch, int n, int k, int group_size,
+                           int packet_format, int activation_dtype, std::uintptr_t stream_ptr);
+
 }  // namespace fast_kernels::decode_quant_linear

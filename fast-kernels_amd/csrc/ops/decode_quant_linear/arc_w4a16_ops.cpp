@@ -21,6 +21,7 @@
 
 #include "kernels/decode_quant_linear/w4a16_aux.h"
 #include "kernels/decode_quant_linear/w4a16_gemv.h"
+#include "ops/decode_quant_linear/w4a16_scratch.h"
 
 namespace fast_kernels::decode_quant_linear {
 namespace {
@@ -913,6 +914,30 @@ void w4a16_forward_kernel(std::uintptr_t activations_ptr, std::uintptr_t packets
   forward_with_format(activations_ptr, packets_ptr, output_ptr, workspace_ptr, workspace_bytes,
                       batch, n, k, group_size, to_packet_format(packet_format, true),
                       activation_dtype, split_k_slices, stream_ptr, kernel);
+}
+
+void w4a16_forward_noalloc(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr,
+                           std::uintptr_t output_ptr, int batch, int n, int k, int group_size,
+                           int packet_format, int activation_dtype, std::uintptr_t stream_ptr) {
+  validate_dimensions(batch, n, k, group_size);
+  const fk::PacketFormat format = to_packet_format(packet_format, true);
+  validate_activation_dtype(activation_dtype);
+  validate_forward_buffers(activations_ptr, packets_ptr, output_ptr);
+  const auto stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  // The plan of arc_w4a16_forward_native, checked against the scratch size before any device
+  // work; then the set-up on the first call on a device (address lookup, counter clear), and the
+  // launch with the scratch array standing in for the workspace.
+  const ArcW4A16Plan plan = plan_w4a16_for_kernel(batch, n, k, group_size, activation_dtype, 0,
+                                                  device_cu_count(), packet_format, kKernelAuto);
+  if (plan.workspace_bytes > kNoAllocScratchBytes) {
+    std::ostringstream oss;
+    oss << "this launch needs " << plan.workspace_bytes << " bytes of fix-up scratch; the "
+        << "no-allocation entry point holds " << kNoAllocScratchBytes << " per device";
+    throw_invalid(oss.str());
+  }
+  void* scratch = noalloc_scratch(kCounterRegionBytes, stream);
+  run_gemv(activations_ptr, packets_ptr, output_ptr, scratch, plan, batch, n, k, group_size,
+           activation_dtype, stream, format);
 }
 
 void arc_w4a16_forward_rmsnorm(std::uintptr_t activations_ptr, std::uintptr_t norm_weight_ptr,

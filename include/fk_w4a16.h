@@ -189,6 +189,20 @@ int fk_arc_w4a16_forward_native(const void* activations, const void* packets, vo
                                 int group_size, int packet_format, int activation_dtype,
                                 int split_k_slices, void* stream);
 
+/* fk_arc_w4a16_forward_native with the automatic plan, for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. It takes no workspace and calls no hipMalloc / hipFree: the stream-K fix-up scratch
+ * is a file-scope device array of FK_NOALLOC_SCRATCH_BYTES that every GPU the library runs on
+ * holds until the process ends, set up on the first call on a device (address lookup and one
+ * clearing kernel on that call's stream). Launches whose plan needs more scratch than that fail
+ * with FK_ERR_INVALID_ARGUMENT before any device work. Every call on one GPU shares its array:
+ * calls that overlap on one GPU (different streams, graphs replayed concurrently) race; calls
+ * ordered on one stream do not. Results are those of fk_arc_w4a16_forward_native. */
+#define FK_NOALLOC_SCRATCH_BYTES (8388608 + 65536)
+int fk_w4a16_forward_noalloc(const void* activations, const void* packets, void* output, int batch,
+                             int n, int k, int group_size, int packet_format,
+                             int activation_dtype, void* stream);
+
 /* Kernel choice for fk_w4a16_plan_for_kernel / fk_w4a16_forward_kernel. No counterpart in the
  * reference; they succeed the reference's per-kernel suite ids (decode/w4a16_linear_scalar and the
  * tensor-core ids), so that the suites can time one kernel against another:
