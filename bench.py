@@ -12,14 +12,15 @@ as the drop-in entry points take them) is measured too and reported under "other
 whose total exceeds twice the 256 MiB Infinity Cache, and consecutive steps use different copies,
 so every launch streams its weights from HBM.
 
-Timing: the launches of R steps are captured once into a HIP graph (torch.cuda.CUDAGraph) and
-replayed; HIP events on the capture stream bracket the K timed steps. value = algorithmic bytes
+Timing: the launches of exactly K steps are captured into one HIP graph (torch.cuda.CUDAGraph;
+step s uses weight copy s mod R) and replayed once between HIP events on the capture stream,
+after a graph of the W warm-up steps. value = algorithmic bytes
 per step / time per step (int4 codes + fp16 scales + activations + outputs; the reference
 packets' fp16 beta, when measured, is read but not credited).
 
 Also reported: per-shape us/call and GB/s (each shape's own graph, events over >= 200 launches),
-a roofline object for the dominant kernel (gate_up), and the CPU oracle timed on the host cores
-on a bounded sample of the same workload.
+a roofline object for the dominant kernel (gate_up), and the reference's CPU arithmetic (fp32
+accumulation) timed on all of this process's host cores on a bounded sample of the workload.
 """
 
 from __future__ import annotations
@@ -66,7 +67,7 @@ def algorithmic_bytes(batch: int, n: int, k: int, g: int) -> int:
 def parse_args() -> argparse.Namespace:
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=1000)
+    p.add_argument("--steps", type=int, default=1000)  # 1000 steps of the 70B layer: 80 ms
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--workload", choices=sorted(WORKLOADS), default="llama70b_layer_m1_bf16")
     p.add_argument("--batch", type=int, default=1)
@@ -220,15 +221,15 @@ def measured_traffic(workload: str, shape: str, packets: str = "native_sym"):
 
 
 def cpu_baseline(workload: str, batch: int, seconds: float) -> dict:
-    """The CPU oracle (C, OpenMP) on the same shapes, host-generated inputs, timed until at least
-    `seconds` of work (whole passes over the four shapes)."""
-    import numpy as np  # noqa: F401
-
+    """The reference's CPU arithmetic (fp32 weights alpha*q + beta, fp32 accumulation, one cast:
+    decode_linear_w4a16.py:177-192 restated in oracle/w4a16_oracle.c fko_gemv_f32) on the same
+    shapes, host-generated inputs, OpenMP over every core this process may run on, timed over
+    whole passes of the four shapes until at least `seconds` have passed."""
     from fast_kernels.benchmarking.inputs import make_case
     from oracle import oracle
 
     act, g, shapes = WORKLOADS[workload]
-    threads = min(len(os.sched_getaffinity(0)), 16)
+    threads = len(os.sched_getaffinity(0))
     oracle.set_threads(threads)
     cases = [make_case(batch, n, k, g, act=act) for _, n, k in shapes]
     total_bytes = 0
@@ -236,7 +237,7 @@ def cpu_baseline(workload: str, batch: int, seconds: float) -> dict:
     passes = 0
     while True:
         for c in cases:
-            oracle.gemv(c.x, c.q_u8, c.alpha, c.beta, g, act)
+            oracle.gemv_f32(c.x, c.q_u8, c.alpha, c.beta, g, act)
             total_bytes += algorithmic_bytes(batch, c.n, c.k, g)
         passes += 1
         elapsed = time.perf_counter() - t0
@@ -248,8 +249,8 @@ def cpu_baseline(workload: str, batch: int, seconds: float) -> dict:
         "cores": threads,
         "kind": "port",
         "sample": f"{passes} full pass(es) over the {len(shapes)} {workload} GEMVs "
-        f"({elapsed:.1f} s, oracle/w4a16_oracle.c fko_gemv, OpenMP {threads} threads, "
-        f"fp64 accumulation)",
+        f"({elapsed:.1f} s, oracle/w4a16_oracle.c fko_gemv_f32: fp32 weights and fp32 "
+        f"accumulation as the reference computes them, OpenMP {threads} threads)",
     }
 
 
@@ -289,22 +290,25 @@ def measure(torch, native, args, act, g, shapes, packets):
             "slice_cols": b.plan["slice_cols"],
         }
 
-    # Whole step: R_max steps captured, each step = all shapes with that step's rotation.
+    # Whole step: exactly `steps` steps captured in one graph (step s launches every shape with
+    # rotation s mod R, so consecutive steps read different weight copies), replayed once between
+    # events; the `warmup` steps are a graph of their own, replayed before.
     R_step = max(len(b.packets) for b in bufs)
 
-    def one_cycle():
-        for r in range(R_step):
-            for b in bufs:
-                b.launch(native, torch, ws, r)
+    def steps_fn(count):
+        def fn():
+            for s_i in range(count):
+                for b in bufs:
+                    b.launch(native, torch, ws, s_i % R_step)
+        return fn
 
-    run = make_runner(torch, one_cycle, R_step * len(bufs), args.eager)
-    cycles_warm = max(1, math.ceil(args.warmup / R_step))
-    cycles = max(1, math.ceil(args.steps / R_step))
-    time_events(torch, run, cycles_warm)
+    if args.warmup > 0:
+        make_runner(torch, steps_fn(args.warmup), args.warmup * len(bufs), args.eager)(1)
+    run = make_runner(torch, steps_fn(args.steps), args.steps * len(bufs), args.eager)
     torch.cuda.synchronize()
-    ms = time_events(torch, run, cycles)
+    ms = time_events(torch, run, 1)
     torch.cuda.synchronize()
-    steps = cycles * R_step
+    steps = args.steps
     ms_per_step = ms / steps
     step_bytes = sum(b.bytes for b in bufs)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
@@ -314,7 +318,7 @@ def measure(torch, native, args, act, g, shapes, packets):
     del ws
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
-    return bufs, per_shape, value, ms_per_step, steps, cycles_warm, R_step
+    return bufs, per_shape, value, ms_per_step, steps, R_step
 
 
 def main() -> int:
@@ -346,7 +350,7 @@ def main() -> int:
     if not args.no_other_packets:
         other_format = "native_sym" if args.packets == "arc" else "arc"
         other = measure(torch, native, args, act, g, shapes, other_format)
-    bufs, per_shape, value, ms_per_step, steps, cycles_warm, R_step = first
+    bufs, per_shape, value, ms_per_step, steps, R_step = first
 
     dominant = max(bufs, key=lambda b: b.bytes)
     dom = per_shape[dominant.name]
@@ -357,7 +361,7 @@ def main() -> int:
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": cycles_warm * R_step,
+        "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -387,7 +391,7 @@ def main() -> int:
         },
     }
     if other is not None:
-        o_bufs, o_per_shape, o_value, o_ms, _, _, _ = other
+        o_bufs, o_per_shape, o_value, o_ms, _, _ = other
         result["other_packets"] = {
             "packets": "native_sym" if args.packets == "arc" else "arc",
             "value": round(o_value, 1),

@@ -12,12 +12,14 @@
 #include <algorithm>
 #include <array>
 #include <cstddef>
-#include <cstdlib>
 #include <cstdint>
+#include <cstdlib>
+#include <map>
 #include <mutex>
 #include <sstream>
 #include <stdexcept>
 #include <string>
+#include <utility>
 
 #include "kernels/decode_quant_linear/w4a16_aux.h"
 #include "kernels/decode_quant_linear/w4a16_gemv.h"
@@ -412,24 +414,25 @@ ArcW4A16Plan plan_w4a16_for_kernel(int batch, int n, int k, int group_size, int 
 
 namespace {
 
-// Library-owned fix-up workspace per device for the reference-signature forward, which has no
-// workspace argument. Grown on demand (so the first call for a larger shape allocates and must not
-// run under stream capture); the counter region is zeroed once, stream-ordered, at allocation and
-// the kernel leaves it zeroed. Calls on one device that run concurrently on different streams share
-// it and must not overlap (the reference's cached group_sums buffer has the same restriction,
-// decode_quant_linear.py:150-168).
-struct DeviceWorkspace {
+// Library-owned fix-up workspace for the reference-signature forward, which has no workspace
+// argument: one per (device, stream), so that calls on different streams never share counters or
+// partials. Grown on demand (so the first call for a larger shape on a stream allocates and must
+// not run under stream capture): the old buffer is freed after synchronising its stream, its only
+// user. The counter region is zeroed, stream-ordered, at allocation, and the kernel leaves it
+// zeroed. (The reference shares one cached group_sums buffer across streams instead,
+// decode_quant_linear.py:150-168.)
+struct StreamWorkspace {
   void* ptr = nullptr;
   std::size_t bytes = 0;
 };
 
 void* library_workspace(std::size_t bytes, hipStream_t stream) {
-  static std::array<DeviceWorkspace, kMaxDevices> spaces{};
+  static std::map<std::pair<int, hipStream_t>, StreamWorkspace> spaces;
   static std::mutex mutex;
   int device = 0;
   check_hip(hipGetDevice(&device), "hipGetDevice");
   std::lock_guard<std::mutex> lock(mutex);
-  DeviceWorkspace& ws = spaces[device];
+  StreamWorkspace& ws = spaces[{device, stream}];
   if (ws.bytes < bytes) {
     if (ws.ptr != nullptr) {
       check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");

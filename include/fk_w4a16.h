@@ -58,8 +58,9 @@ int fk_compute_arc_w4a16_group_sums(const void* activations, void* sums, int bat
 
 /* Reference: arc_w4a16_forward, arc_w4a16.h:15-17 / arc_w4a16.cu:687-707.
  * group_sums is accepted for signature compatibility and not read (may be NULL): the kernel forms
- * the activation sums it needs itself, in the same launch. Uses a library-owned per-device
- * split-K workspace; calls on one device must be stream-ordered with respect to each other. */
+ * the activation sums it needs itself, in the same launch. Uses a library-owned split-K workspace
+ * per (device, stream): calls on different streams never share one, and the first call of a
+ * larger shape on a stream allocates (so it must not be the first call under graph capture). */
 int fk_arc_w4a16_forward(const void* activations, const void* packets, const void* group_sums,
                          void* output, int batch, int n, int k, int group_size,
                          int packet_stride_bytes, void* stream);

@@ -42,6 +42,7 @@ def lib() -> ctypes.CDLL:
         L.fko_dequant_packets.argtypes = [P, P, I, I, I]
         L.fko_group_sums.argtypes = [P, P, I, I, I, I]
         L.fko_gemv.argtypes = [P, P, P, P, P, P, I, I, I, I, I]
+        L.fko_gemv_f32.argtypes = [P, P, P, P, P, I, I, I, I, I]
         L.fko_reduce_partials.argtypes = [P, P, I, I, I]
         L.fko_packet_stride_bytes.argtypes = [I]
         L.fko_packet_stride_bytes.restype = ctypes.c_size_t
@@ -127,6 +128,26 @@ def gemv(
         1 if act == "bf16" else 0,
     )
     return out, out32
+
+
+def gemv_f32(
+    x_bits: np.ndarray,
+    q_u8: np.ndarray,
+    alpha: np.ndarray,
+    beta: np.ndarray,
+    group_size: int,
+    act: str = "f16",
+) -> np.ndarray:
+    """gemv with fp32 accumulation (the reference's arithmetic; the CPU baseline). Returns the
+    output bits [M, N] in the activation dtype."""
+    batch, k = x_bits.shape
+    n = q_u8.shape[0]
+    out = np.empty((batch, n), dtype=np.uint16)
+    lib().fko_gemv_f32(
+        _ptr(np.ascontiguousarray(x_bits)), _ptr(q_u8), _ptr(alpha), _ptr(beta), _ptr(out), batch,
+        n, k, group_size, 1 if act == "bf16" else 0,
+    )
+    return out
 
 
 def reduce_partials(partials: np.ndarray) -> np.ndarray:

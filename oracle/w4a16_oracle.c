@@ -12,6 +12,8 @@
  *   fko_group_sums         arc_w4a16.cu:124-158 (compute_arc_group_sums_kernel)
  *   fko_gemv               decode_linear_w4a16.py:177-192 (_explicit_reference_output):
  *                          fp32 weights alpha*q + beta, matmul, cast to the activation dtype
+ *   fko_gemv_f32           the same with fp32 accumulation, as the reference computes it (the
+ *                          CPU baseline bench.py times)
  *   fko_reduce_partials    arc_w4a16.cu:388-402
  * Conversions (fko_f32_to_f16_bits, fko_f32_to_bf16_bits) are IEEE round-to-nearest-even,
  * written from the format definitions.
@@ -253,6 +255,40 @@ void fko_gemv(const uint16_t* x, const uint8_t* q, const uint16_t* alpha, const 
         if (out_f32 != NULL) {
           out_f32[(size_t)m * n + r] = (float)acc;
         }
+      }
+    }
+  }
+}
+
+/* fko_gemv with the reference's own arithmetic (decode_linear_w4a16.py:177-192: fp32 weights,
+ * fp32 matmul): the products accumulate in float, in k order, then one cast. The CPU baseline that
+ * bench.py times; the parity tests use fko_gemv. */
+void fko_gemv_f32(const uint16_t* x, const uint8_t* q, const uint16_t* alpha, const uint16_t* beta,
+                  uint16_t* out, int batch, int n, int k, int group_size, int act_bf16) {
+  const int ng = k / group_size;
+#pragma omp parallel
+  {
+    float xf[16384];
+#pragma omp for schedule(static)
+    for (int r = 0; r < n; ++r) {
+      const uint8_t* q_row = q + (size_t)r * (size_t)(k / 2);
+      for (int m = 0; m < batch; ++m) {
+        float acc = 0.0f;
+        for (int k0 = 0; k0 < k; k0 += 16384) {
+          const int kc = (k - k0) < 16384 ? (k - k0) : 16384;
+          for (int i = 0; i < kc; ++i) {
+            xf[i] = act_to_f32(x[(size_t)m * k + k0 + i], act_bf16);
+          }
+          for (int g0 = k0; g0 < k0 + kc; g0 += group_size) {
+            const int g = g0 / group_size;
+            const float a = fko_f16_bits_to_f32(alpha[(size_t)r * ng + g]);
+            const float b = fko_f16_bits_to_f32(beta[(size_t)r * ng + g]);
+            for (int i = 0; i < group_size; ++i) {
+              acc += weight_f32(a, b, code_at(q_row, g0 + i)) * xf[g0 + i - k0];
+            }
+          }
+        }
+        out[(size_t)m * n + r] = f32_to_act(acc, act_bf16);
       }
     }
   }

@@ -137,6 +137,19 @@ def test_gemv_vs_float64_matmul(act: str, group_size: int) -> None:
     np.testing.assert_array_equal(bits, round_fn(f32))
 
 
+@pytest.mark.parametrize("act", ["f16", "bf16"])
+def test_gemv_f32_is_the_float32_sequential_sum(act: str) -> None:
+    """The CPU baseline's fp32 accumulation: against numpy summing the same fp32 products in k
+    order in float32 (np.cumsum keeps float32 and is sequential), then one cast."""
+    case = make_case(2, 128, 1024, 128, act=act, asymmetric=True, seed=23)
+    bits = oracle.gemv_f32(case.x, case.q_u8, case.alpha, case.beta, 128, act)
+    w = _numpy_dequant(case, 128)  # float32 alpha * q + beta
+    prod = case.x_f32()[:, None, :].astype(np.float32) * w[None, :, :].astype(np.float32)
+    acc = np.cumsum(prod, axis=2, dtype=np.float32)[:, :, -1]
+    round_fn = (lambda v: v.astype(np.float16).view(np.uint16)) if act == "f16" else f32_to_bf16_bits
+    np.testing.assert_array_equal(bits, round_fn(acc))
+
+
 def test_gemv_one_hot_and_identity_scale() -> None:
     case = make_case(1, 128, 256, 64, seed=5)
     case.alpha[:] = np.float16(1.0).view(np.uint16)

@@ -401,3 +401,33 @@ def test_invalid_arguments_raise_value_error() -> None:
         arc_w4a16_forward(x, packets[:1], n=128, k=256, group_size=128)
     with pytest.raises(ValueError):
         arc_w4a16_forward(x, packets, n=128, k=256, group_size=128, split_k_slices=0)
+
+
+def test_reference_forward_on_two_streams_at_once() -> None:
+    """The reference-signature arc_w4a16_forward (library-owned fix-up workspace) on two streams
+    whose launches overlap: each stream has its own workspace, so both results match the oracle."""
+    shapes = [(1, 4096, 14336, 128), (1, 1024, 16384, 128)]
+    runs = []
+    for batch, n, k, g in shapes:
+        plan = arc_w4a16_plan(batch=batch, n=n, k=k, group_size=g)
+        assert plan["workspace_bytes"] > 0, plan
+        case = make_case(batch, n, k, g, seed=n + k)
+        x, q, a, b = _upload(case)
+        runs.append((case, x, pack_arc_w4a16_packets(q, a, b, group_size=g)))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    outs = []
+    for _ in range(3):  # the first round allocates each stream's workspace
+        outs = []
+        for (case, x, packets), s in zip(runs, streams):
+            y = torch.empty((1, case.n), device=DEV, dtype=torch.float16)
+            with torch.cuda.stream(s):
+                for _ in range(20):
+                    native_module().arc_w4a16_forward(
+                        x.data_ptr(), packets.data_ptr(), 0, y.data_ptr(), 1, case.n, case.k,
+                        case.group_size, arc_packet_stride_bytes(case.group_size), s.cuda_stream)
+            outs.append(y)
+        torch.cuda.synchronize()
+    for (case, _, _), y in zip(runs, outs):
+        ref, _ = oracle.gemv(case.x, case.q_u8, case.alpha, case.beta, case.group_size)
+        _assert_gemv_close(_bits(y), ref, case, f"two streams {case.n}x{case.k}")
