@@ -60,6 +60,16 @@ WORKLOADS = {
 }
 
 
+# Launch schedules of a plan (fk_arc_w4a16_plan.schedule) and the kernel each runs.
+SCHEDULES = {0: "runs", 1: "slice_pairs", 2: "stream"}
+
+
+def kernel_name(packets: str, schedule: int) -> str:
+    if packets == "arc":
+        return "w4a16_gemv_kernel"
+    return "w4a16_gemv_stream_kernel" if schedule == 2 else "w4a16_gemv_native_kernel"
+
+
 def algorithmic_bytes(batch: int, n: int, k: int, g: int) -> int:
     return n * k // 2 + n * (k // g) * 2 + batch * k * 2 + batch * n * 2
 
@@ -288,6 +298,8 @@ def measure(torch, native, args, act, g, shapes, packets):
             "groups_per_workgroup": b.plan["groups_per_workgroup"],
             "workgroups": b.plan["workgroups"],
             "slice_cols": b.plan["slice_cols"],
+            "schedule": SCHEDULES[b.plan.get("schedule", 0)],
+            "threads_per_workgroup": 512 if b.plan.get("schedule", 0) == 2 else 256,
         }
 
     # Whole step: exactly `steps` steps captured in one graph (step s launches every shape with
@@ -381,7 +393,7 @@ def main() -> int:
         "per_shape": per_shape,
         "roofline": {
             "bound": "hbm",
-            "kernel": ("w4a16_gemv_native_kernel" if args.packets != "arc" else "w4a16_gemv_kernel")
+            "kernel": kernel_name(args.packets, dominant.plan.get("schedule", 0))
             + f" ({dominant.name} {dominant.n}x{dominant.k})",
             "achieved": achieved,
             "peak": PEAK_HBM_GBS,

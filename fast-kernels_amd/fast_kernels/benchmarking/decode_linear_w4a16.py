@@ -408,3 +408,51 @@ def _run_shape(torch: Any, device: Any, suite: BenchmarkSuite, dtype: str, layou
             if c.status == "ok" and c.subject_id != vendor_id and c.device_latency_us_median:
                 c.speedup_vs = {vendor_id: latencies[vendor_id] / c.device_latency_us_median}
     return out
+
+
+def launch_kernel_case(suite: BenchmarkSuite, case_id: str, launches: int) -> str:
+    """Rebuild one kernel case of the suite (the timed run's inputs, packets and rotated weight
+    copies) and launch its kernel `launches` times, cycling through the copies, then synchronise.
+    For measuring the case under a profiler (``fk bench --counters``); returns the kernel id."""
+    import torch
+
+    from fast_kernels.ops import (
+        arc_w4a16_forward,
+        arc_w4a16_forward_native,
+        convert_arc_to_native_packets,
+        group_size_for_layout,
+        pack_arc_w4a16_packets,
+    )
+
+    recipe = str(suite.metadata.get("recipe", "reference"))
+    asymmetric = recipe == "reference" or suite.metadata.get("zero_point") == "asymmetric"
+    match = [(kid, dtype, layout, shape) for kid in suite.kernels.ids for dtype in suite.dtypes
+             for layout in suite.layouts for shape in suite.shapes
+             if _make_case_id("kernel", kid, dtype, layout, shape.name) == case_id]
+    if not match:
+        raise ValueError(f"no kernel case {case_id!r} in suite {suite.id!r}")
+    kernel_id, dtype, layout, shape = match[0]
+    impl = kernel_registry()[kernel_id].impl
+    group_size = group_size_for_layout(layout)
+    n, k = shape.require_dimension("n"), shape.require_dimension("k")
+    device = torch.device("cuda")
+    case = make_case(shape.batch, n, k, group_size, act=_DTYPES[dtype], asymmetric=asymmetric,
+                     recipe=recipe)
+    x, q, a, b = _upload(torch, case, device)
+    packets = pack_arc_w4a16_packets(q, a, b, group_size=group_size)
+    native_format = "native_asym" if asymmetric else "native_sym"
+    if impl == NATIVE_IMPL:
+        packets = convert_arc_to_native_packets(packets, n=n, k=k, group_size=group_size,
+                                                packet_format=native_format)
+    rotations = max(2, math.ceil(CACHE_BUST_BYTES / max(packets.numel(), 1)))
+    copies = [packets] + [packets.clone() for _ in range(rotations - 1)]
+    out = torch.empty((shape.batch, n), device=device, dtype=x.dtype)
+    for i in range(launches):
+        if impl == NATIVE_IMPL:
+            arc_w4a16_forward_native(x, copies[i % rotations], n=n, k=k, group_size=group_size,
+                                     packet_format=native_format, output=out)
+        else:
+            arc_w4a16_forward(x, copies[i % rotations], n=n, k=k, group_size=group_size,
+                              output=out, impl=impl)
+    torch.cuda.synchronize()
+    return kernel_id

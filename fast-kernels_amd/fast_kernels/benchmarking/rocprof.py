@@ -83,8 +83,10 @@ def kernel_trace_by_grid(directory: str | Path, name_filter: str = "") -> list[d
     return out
 
 
-def counter_by_grid(directory: str | Path, counter: str, name_filter: str = "") -> dict:
-    """Mean counter value per (kernel, grid) from a --pmc counter-collection CSV."""
+def counter_by_grid(directory: str | Path, counter: str, name_filter: str = "",
+                    with_counts: bool = False) -> dict:
+    """Mean counter value per (kernel, grid) from a --pmc counter-collection CSV (with_counts:
+    (mean, dispatches) per key)."""
     path = _find(directory, "_counter_collection.csv")
     groups: dict[tuple[str, int], list[float]] = defaultdict(list)
     with path.open(newline="") as fh:
@@ -95,6 +97,8 @@ def counter_by_grid(directory: str | Path, counter: str, name_filter: str = "") 
             if name_filter and name_filter not in name:
                 continue
             groups[(short_kernel_name(name), int(row["Grid_Size"]))].append(float(row["Counter_Value"]))
+    if with_counts:
+        return {k: (sum(v) / len(v), len(v)) for k, v in groups.items()}
     return {k: sum(v) / len(v) for k, v in groups.items()}
 
 
@@ -133,14 +137,18 @@ def traffic(
     return {"read_scale_bytes_per_kib": rs, "write_scale_bytes_per_kib": ws, "kernels": rows}
 
 
-def _shape_row(rows: dict, threads: int, slice_cols: int | None) -> tuple[str, dict] | None:
+def _shape_row(rows: dict, threads: int, slice_cols: int | None,
+               native: bool | None = None) -> tuple[str, dict] | None:
     """The kernel row of one bench shape: same grid and, when several kernels share the grid, the
-    slice width, which the reference-packet kernel's template arguments carry as
-    ", <cols>, (PacketFormat)" (the native-slab kernel always uses 32-column slices)."""
+    packet format (native-slab kernels, whatever their slice width: single slices, slice pairs
+    and the stream schedule all carry "native" or "stream" in their names) or, for the
+    reference-packet kernel, the slice width its template arguments carry as
+    ", <cols>, (PacketFormat)"."""
     hits = [(k, v) for k, v in rows.items() if k.endswith(f" grid={threads}")]
+    if len(hits) > 1 and native is not None:
+        hits = [(k, v) for k, v in hits if (("native" in k or "stream" in k) == native)]
     if len(hits) > 1 and slice_cols is not None:
-        hits = [(k, v) for k, v in hits
-                if f", {slice_cols}, (PacketFormat)" in k or ("native" in k and slice_cols == 32)]
+        hits = [(k, v) for k, v in hits if f", {slice_cols}, (PacketFormat)" in k]
     return hits[0] if len(hits) == 1 else None
 
 
@@ -148,12 +156,14 @@ def traffic_by_shape(result: dict, bench: dict) -> dict:
     """traffic() rows keyed by the bench line's shape names (per_shape workgroups x 256 threads,
     slice_cols), with the algorithmic bytes beside them."""
     out = {}
+    native = bench.get("config", {}).get("packets", "native_sym") != "arc"
     for name, shape in bench["per_shape"].items():
-        hit = _shape_row(result["kernels"], int(shape["workgroups"]) * 256, shape.get("slice_cols"))
+        threads = int(shape["workgroups"]) * int(shape.get("threads_per_workgroup", 256))
+        hit = _shape_row(result["kernels"], threads, shape.get("slice_cols"), native)
         if hit is None:
             continue
         kernel, row = hit
-        out[name] = dict(row, kernel=kernel, grid_threads=int(shape["workgroups"]) * 256,
+        out[name] = dict(row, kernel=kernel, grid_threads=threads,
                          algorithmic_bytes=int(shape["bytes"]),
                          traffic_over_algorithmic=round(row["hbm_bytes_per_launch"] / shape["bytes"], 4))
     return out
