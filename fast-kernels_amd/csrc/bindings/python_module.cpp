@@ -17,6 +17,11 @@
 
 namespace py = pybind11;
 
+// 1 when libfk_w4a16.so holds the HIP kernels, 0 for the host-only stub (FK_ENABLE_HIP=OFF).
+#ifndef FK_COMPILED_WITH_HIP
+#define FK_COMPILED_WITH_HIP 1
+#endif
+
 namespace {
 
 void check(int status) {
@@ -51,10 +56,10 @@ PYBIND11_MODULE(_native, m) {
     py::dict info;
     info["project_version"] = std::string("0.1.0");
     info["library"] = std::string(fk_build_info());
-    info["compiled_with_hip"] = true;
+    info["compiled_with_hip"] = FK_COMPILED_WITH_HIP != 0;
     info["compiled_with_cuda"] = false;
-    info["compiled_with_gpu"] = true;
-    info["hip_architectures"] = std::string("gfx950");
+    info["compiled_with_gpu"] = FK_COMPILED_WITH_HIP != 0;
+    info["hip_architectures"] = std::string(FK_COMPILED_WITH_HIP ? "gfx950" : "");
     info["cxx_compiler_id"] = std::string("GNU");
     info["cxx_compiler_version"] = std::string(__VERSION__);
     return info;
