@@ -50,7 +50,10 @@ def _rocprof() -> str | None:
 def _profile(rocprof: str, counter: str, child_args: list[str], out_dir: Path) -> Path:
     cmd = [rocprof, "--pmc", counter, "--output-format", "csv", "-d", str(out_dir), "-o", "run",
            "--", sys.executable, "-m", "fast_kernels.benchmarking.counters", *child_args]
-    env = dict(os.environ, TMPDIR=str(out_dir.parent))
+    # The child runs from the scratch directory, so it finds this package through PYTHONPATH.
+    pkg_parent = str(Path(__file__).resolve().parents[2])
+    path = os.pathsep.join(p for p in (pkg_parent, os.environ.get("PYTHONPATH", "")) if p)
+    env = dict(os.environ, TMPDIR=str(out_dir.parent), PYTHONPATH=path)
     proc = subprocess.run(cmd, capture_output=True, text=True, timeout=CHILD_TIMEOUT_S, env=env,
                           cwd=str(out_dir.parent))
     if proc.returncode != 0:
@@ -78,6 +81,7 @@ def add_traffic_metrics(suite_path: Path, cases: list[BenchmarkCase]) -> list[st
     notes for the run metadata (what was measured, or why nothing was)."""
     from fast_kernels.benchmarking.suites import load_suite
 
+    suite_path = Path(suite_path).resolve()
     suite = load_suite(suite_path)
     if suite.family != "decode_quant_linear":
         return [f"--counters: no traffic measurement for suite family {suite.family!r}."]
@@ -93,6 +97,8 @@ def add_traffic_metrics(suite_path: Path, cases: list[BenchmarkCase]) -> list[st
             d = _profile(rocprof, counter, ["copy"], root / f"copy-{counter}")
             scale[counter] = copy_scale(d, counter, COPY_CALIBRATION_BYTES)
         for i, case in enumerate(targets):
+            print(f"[fk bench --counters] {i + 1}/{len(targets)} {case.case_id}", file=sys.stderr,
+                  flush=True)
             raw = {}
             for counter in COUNTERS:
                 d = _profile(rocprof, counter, ["case", str(suite_path), case.case_id],

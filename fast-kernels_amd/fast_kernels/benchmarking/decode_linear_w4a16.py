@@ -22,6 +22,7 @@ kernel against the reference baseline, suite tolerances), then timed. Difference
 from __future__ import annotations
 
 import math
+import sys
 from statistics import median
 from time import perf_counter
 from typing import Any, Callable, Literal
@@ -219,6 +220,8 @@ def run_decode_linear_w4a16_suite(suite: BenchmarkSuite) -> tuple[list[Benchmark
     for dtype in suite.dtypes:
         for layout in suite.layouts:
             for shape in suite.shapes:
+                print(f"[fk bench] {suite.id}: {dtype} {layout} {shape.name}", file=sys.stderr,
+                      flush=True)
                 cases.extend(_run_shape(torch, device, suite, dtype, layout, shape, recipe,
                                         asymmetric, launches))
     return cases, notes
