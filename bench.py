@@ -74,6 +74,14 @@ def algorithmic_bytes(batch: int, n: int, k: int, g: int) -> int:
     return n * k // 2 + n * (k // g) * 2 + batch * k * 2 + batch * n * 2
 
 
+def _threads_per_workgroup(plan: dict, num_groups: int) -> int:
+    """Threads of one workgroup: 256 for the per-slice runs, 8 waves for the stream schedule and a
+    ninth (the control wave) when its workgroups also take a piece of a left-over slice."""
+    if plan.get("schedule", 0) != 2:
+        return 256
+    return 576 if plan["groups_per_workgroup"] % num_groups else 512
+
+
 def parse_args() -> argparse.Namespace:
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -299,7 +307,7 @@ def measure(torch, native, args, act, g, shapes, packets):
             "workgroups": b.plan["workgroups"],
             "slice_cols": b.plan["slice_cols"],
             "schedule": SCHEDULES[b.plan.get("schedule", 0)],
-            "threads_per_workgroup": 512 if b.plan.get("schedule", 0) == 2 else 256,
+            "threads_per_workgroup": _threads_per_workgroup(b.plan, b.k // b.g),
         }
 
     # Whole step: exactly `steps` steps captured in one graph (step s launches every shape with

@@ -51,6 +51,11 @@ struct GemvLaunch {
   int stream_depth = 0;   // stream schedule: units in flight per wave
   int stream_grid = 0;    // stream schedule: workgroups
   int stream_whole = 0;   // stream schedule: whole slices per workgroup
+  // Stream schedule with a tail: the slices past stream_grid * stream_whole are cut into
+  // stream_parts pieces of stream_tail groups, one per workgroup, finished through the
+  // workspace (counters: one per tail slice; partials: 32 floats per workgroup).
+  int stream_tail = 0;
+  int stream_parts = 0;
 };
 
 // Longest K the stream schedule stages (its LDS holds the whole activation row).

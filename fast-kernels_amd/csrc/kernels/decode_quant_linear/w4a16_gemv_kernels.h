@@ -112,6 +112,8 @@ struct GemvParams {
   int pair;                         // native slabs: each run streams two adjacent whole slices
   int stream_whole;                 // stream schedule (w4a16_gemv_stream.hip): whole slices
                                     // per workgroup
+  int stream_tail;                  // stream schedule: groups of the workgroup's tail piece
+  int stream_parts;                 // stream schedule: workgroups sharing one tail slice
 };
 
 template <int G, int MT, int CW>

@@ -84,6 +84,8 @@ struct ArcW4A16Plan {
   int schedule;                 // kSchedule*: how the workgroups walk their units
   int stream_depth;             // kScheduleStream: slabs in flight per wave
   int stream_whole;             // kScheduleStream: whole slices per workgroup
+  int stream_tail;              // kScheduleStream: groups of each workgroup's tail piece (0: none)
+  int stream_parts;             // kScheduleStream: workgroups sharing one tail slice
 };
 
 // Launch schedules of a plan. kScheduleRuns: workgroups stream runs of one slice (or tile) at a

@@ -286,6 +286,16 @@ bool stream_schedule_enabled() {
   return enabled;
 }
 
+// FK_W4A16_STREAM_TAIL=0 keeps shapes whose slices do not divide over the CUs off the stream
+// schedule (they then run per-slice runs).
+bool stream_tail_enabled() {
+  static const bool enabled = [] {
+    const char* v = std::getenv("FK_W4A16_STREAM_TAIL");
+    return v == nullptr || std::string(v) != "0";
+  }();
+  return enabled;
+}
+
 // FK_W4A16_STREAM_KB=4|8 pins the weights in flight per wave (else the plan's choice).
 int stream_kb_override() {
   static const int kb = [] {
@@ -369,15 +379,34 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
     const int depth = fk::stream_depth_for_kb(group_size, kb);
     const int quantum = fk::kStreamWaves * depth;
     const long long grid = static_cast<long long>(cu_count) * stream_workgroups_per_cu();
-    if (num_groups % quantum == 0 && lds <= lds_limit && slices >= grid && slices % grid == 0) {
+    // Slices left over past whole ones per workgroup are cut into one piece per workgroup when
+    // they divide the grid, the pieces are whole blocks of the waves and lie inside one staging
+    // pass of a wave's groups (w4a16_gemv_stream.hip), and every workgroup also has a whole
+    // slice to stream while its piece is handed off. Measured on MI355X (bench): 70B qkv
+    // 11.6 -> 9.8 us, 8B gate_up 14.2 -> 12.7 (pairs before), 7B qkv 7.4 -> 7.1; with no whole
+    // slice (8B o: half a slice per CU) the hand-off is the workgroup's last step and costs more
+    // than it saves (4.8 -> 5.7 us), so such shapes stay on the per-slice runs.
+    const long long rem = slices % grid;
+    const long long parts = rem == 0 ? 0 : grid / rem;
+    const int pass_groups = fk::kStreamWaves * (64 / (group_size / 8));
+    const bool tail_ok = rem != 0 && slices > grid && stream_tail_enabled() && grid % rem == 0 &&
+                         num_groups % parts == 0 && (num_groups / parts) % quantum == 0 &&
+                         pass_groups % (num_groups / parts) == 0;
+    if (num_groups % quantum == 0 && lds <= lds_limit &&
+        ((slices >= grid && rem == 0) || tail_ok)) {
       plan.schedule = kScheduleStream;
       plan.slice_cols = fk::kSliceCols;
       plan.workgroups = static_cast<int>(grid);
       plan.stream_depth = depth;
       plan.stream_whole = static_cast<int>(slices / grid);
-      plan.groups_per_workgroup = plan.stream_whole * num_groups;
-      plan.max_tile_contributors = 1;
-      plan.workspace_bytes = 0;
+      plan.stream_tail = rem == 0 ? 0 : static_cast<int>(num_groups / parts);
+      plan.stream_parts = rem == 0 ? 0 : static_cast<int>(parts);
+      plan.groups_per_workgroup = plan.stream_whole * num_groups + plan.stream_tail;
+      plan.max_tile_contributors = rem == 0 ? 1 : static_cast<int>(parts);
+      plan.workspace_bytes =
+          rem == 0 ? 0
+                   : kCounterRegionBytes + static_cast<std::size_t>(grid) * fk::kSliceCols *
+                                               sizeof(float);
       return plan;
     }
   }
@@ -493,6 +522,8 @@ void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::u
     l.stream_depth = plan.stream_depth;
     l.stream_grid = plan.workgroups;
     l.stream_whole = plan.stream_whole;
+    l.stream_tail = plan.stream_tail;
+    l.stream_parts = plan.stream_parts;
   }
   l.format = format;
   l.fuse = fuse;

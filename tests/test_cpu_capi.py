@@ -214,16 +214,16 @@ def test_native_format_validation_without_gpu(lib: ctypes.CDLL) -> None:
         # (batch, n, k, G) -> (slice_cols, groups per workgroup, workgroups, schedule) on 256 CUs
         # schedule 0: per-slice runs, 1: slice pairs, 2: stream (whole slices per CU, one range)
         ((1, 8192, 8192, 128), (32, 64, 256, 2)),      # 256 slices: one per CU, streamed
-        ((1, 10240, 8192, 128), (32, 64, 320, 0)),     # 320 slices do not divide over 256 CUs
+        ((1, 10240, 8192, 128), (32, 80, 256, 2)),     # 70B qkv: 1 slice + a quarter slice per CU
         ((1, 10240, 4096, 128), (64, 32, 160, 1)),     # 320 slices in 160 pairs
-        ((1, 12288, 4096, 128), (64, 32, 192, 1)),     # 7B qkv: 384 slices in 192 pairs
-        ((1, 28672, 4096, 128), (64, 32, 448, 1)),     # 8B gate_up: 896 slices in 448 pairs
+        ((1, 12288, 4096, 128), (32, 48, 256, 2)),     # 7B qkv: 1 slice + a half slice per CU
+        ((1, 28672, 4096, 128), (32, 112, 256, 2)),    # 8B gate_up: 3 slices + a half per CU
         ((1, 22016, 4096, 128), (32, 32, 688, 0)),     # 7B gate_up: 344 pairs would fill 2 rounds unevenly
         ((2, 12288, 4096, 128), (32, 32, 384, 0)),     # pairs for one row only
         ((1, 57344, 8192, 128), (32, 448, 256, 2)),    # 70B gate_up: 7 whole slices per CU
         ((1, 8192, 28672, 128), (32, 224, 256, 2)),    # 70B down: one slice of 224 groups per CU
         ((1, 8192, 28672 + 128, 128), (32, 113, 510, 0)),  # 225 groups: not a multiple of 16
-        ((1, 4096, 4096, 128), (32, 32, 128, 0)),      # half the CUs idle, but K is short
+        ((1, 4096, 4096, 128), (32, 32, 128, 0)),      # no whole slice per CU to hide a tail
         ((1, 4096, 14336, 128), (32, 56, 256, 0)),     # 128 slices, 112 groups: two runs of 56
         ((4, 14336, 4096, 64), (32, 64, 448, 0)),      # four rows share a slice's runs
         ((16, 14336, 4096, 64), (128, 16, 448, 0)),    # matrix cores: the reference-format plan

@@ -79,7 +79,7 @@ def test_config2_llama70b_bf16_as_benchmarked(name: str, n: int, k: int, packets
     plan = arc_w4a16_plan(batch=1, n=n, k=k, group_size=128, activation_dtype=torch.bfloat16,
                           packet_format=code)
     if code == 1 and torch.cuda.get_device_properties(0).multi_processor_count == 256:
-        assert plan["schedule"] == (0 if name == "qkv" else 2), plan
+        assert plan["schedule"] == 2, plan  # qkv: 320 slices, one and a quarter per CU
     y = arc_w4a16_forward_native(x, slabs, n=n, k=k, group_size=128, packet_format=packets)
     torch.cuda.synchronize()
     rows = _rows(n)
@@ -177,11 +177,18 @@ def test_config4_llama8b_decode_step_graph() -> None:
         (16384, 8192, 128, "bf16", True),   # two whole slices per workgroup, asymmetric
         (8192, 32768, 128, "bf16", False),  # the longest K the stream schedule stages
         (8192, 32768, 64, "f16", False),    # 512 groups at G = 64
+        # tail pieces (slices left over past whole ones per CU), finished through the workspace
+        (10240, 8192, 128, "bf16", False),  # 1 slice + a quarter of one per CU
+        (12288, 4096, 128, "bf16", True),   # 1 slice + a half
+        (28672, 4096, 128, "f16", False),   # 3 slices + a half
+        (12288, 4096, 64, "bf16", False),   # G = 64: halves of 64 groups
+        (10240, 16384, 64, "f16", True),    # G = 64: quarters of 256 groups
     ],
 )
 def test_stream_schedule_variants(n: int, k: int, g: int, act: str, asym: bool) -> None:
-    """The stream schedule (slices dividing over one workgroup per CU) at both group sizes, both
-    activation dtypes, both native formats and the staging slot counts; plus determinism."""
+    """The stream schedule (whole slices per CU, and tail pieces of the slices left over) at both
+    group sizes, both activation dtypes, both native formats and the staging slot counts; plus
+    determinism."""
     if torch.cuda.get_device_properties(0).multi_processor_count != 256:
         pytest.skip("the shapes are chosen for 256 CUs")
     case = make_case(1, n, k, g, act=act, asymmetric=asym, seed=n + k + g)
@@ -192,8 +199,11 @@ def test_stream_schedule_variants(n: int, k: int, g: int, act: str, asym: bool) 
     plan = arc_w4a16_plan(batch=1, n=n, k=k, group_size=g,
                           activation_dtype=x.dtype, packet_format=2 if asym else 1)
     assert plan["schedule"] == 2, plan
+    # three calls: the tail hand-off leaves its counters at zero, and adds the parts in a fixed
+    # order, so every call gives the same bits
     ys = [_bits(arc_w4a16_forward_native(x, slabs, n=n, k=k, group_size=g, packet_format=fmt))
-          for _ in range(2)]
+          for _ in range(3)]
     np.testing.assert_array_equal(ys[0], ys[1])
+    np.testing.assert_array_equal(ys[0], ys[2])
     rows = _rows(n)
     _assert_gemv_close(ys[0][:, rows], _oracle_rows(case, rows, act), case, f"stream {plan}")
