@@ -296,6 +296,15 @@ bool stream_tail_enabled() {
   return enabled;
 }
 
+// FK_W4A16_STREAM_SMALL=0 keeps shapes with fewer slices than CUs on the per-slice runs.
+bool stream_small_enabled() {
+  static const bool enabled = [] {
+    const char* v = std::getenv("FK_W4A16_STREAM_SMALL");
+    return v == nullptr || std::string(v) != "0";
+  }();
+  return enabled;
+}
+
 // FK_W4A16_STREAM_KB=4|8 pins the weights in flight per wave (else the plan's choice).
 int stream_kb_override() {
   static const int kb = [] {
@@ -378,7 +387,15 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
     const int kb = stream_kb_override() != 0 ? stream_kb_override() : 4;
     const int depth = fk::stream_depth_for_kb(group_size, kb);
     const int quantum = fk::kStreamWaves * depth;
-    const long long grid = static_cast<long long>(cu_count) * stream_workgroups_per_cu();
+    long long grid = static_cast<long long>(cu_count) * stream_workgroups_per_cu();
+    // Fewer slices than CUs and K too short to split (per == K/G): one whole slice per
+    // workgroup, streamed by eight waves with the row staged once. Measured on MI355X (bench):
+    // 8B qkv (192 slices) 5.16 -> 4.44 us, o (128) 4.79 -> 4.02, 7B o 4.67 -> 4.15; 8B down
+    // (128 slices of 112 groups), whose runs split K over 256 workgroups, gets slower (8.8 ->
+    // 10.0), so it keeps its runs.
+    if (slices < grid && per == num_groups && stream_small_enabled()) {
+      grid = slices;
+    }
     // Slices left over past whole ones per workgroup are cut into one piece per workgroup when
     // they divide the grid, the pieces are whole blocks of the waves and lie inside one staging
     // pass of a wave's groups (w4a16_gemv_stream.hip), and every workgroup also has a whole
