@@ -56,6 +56,9 @@ struct GemvLaunch {
   // workspace (counters: one per tail slice; partials: 32 floats per workgroup).
   int stream_tail = 0;
   int stream_parts = 0;
+  // Stream schedule over half-slices (G = 128): workgroup b streams the 16 columns 16 * (b & 1)
+  // .. of slice b / 2, reading half of every slab (stream_grid = 2 * slices, stream_whole = 1).
+  bool stream_half = false;
 };
 
 // Longest K the stream schedule stages (its LDS holds the whole activation row).

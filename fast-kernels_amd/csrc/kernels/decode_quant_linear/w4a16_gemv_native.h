@@ -215,6 +215,23 @@ __device__ __forceinline__ void native_load(NativeLoad<G>& ld, const uint8_t* sl
   }
 }
 
+// Half a G = 128 slab: the 1 KB of code words of columns 16 * half .. 16 * half + 15 (into
+// ld.w[0]) and the lane's record (both columns' scales; the kernel picks its half).
+template <int G, PacketFormat F>
+__device__ __forceinline__ void native_load_half(NativeLoad<G>& ld, const uint8_t* slab, int lane,
+                                                 int half) {
+  static_assert(G == 128, "half slabs need G = 128");
+  ld.w[0] = stream_load16(slab + half * 1024 + lane * 16);
+  const uint8_t* record = slab + native_record_offset(G) + native_record_bytes(F) * (lane % 16);
+  if constexpr (F == PacketFormat::kNativeAsym) {
+    const uint2 r = stream_load8(record);
+    ld.alpha = r.x;
+    ld.zp = r.y;
+  } else {
+    ld.alpha = stream_load4(record);
+  }
+}
+
 // Word j of the lane's unit of column n + 16 i.
 template <int G>
 __device__ __forceinline__ uint32_t unit_word(const NativeLoad<G>& ld, int i, int j) {
@@ -302,11 +319,14 @@ __device__ __forceinline__ void native_stage_store(NativeSmem<G, MT>& sm, StageR
   }
 }
 
-template <int G, Act A, int MT, PacketFormat F, class S>
+// kCols = 2: the lane's two columns n and n + 16 (ld holds both halves of the slab). kCols = 1
+// (G = 128, native_load_half): column n + 16 * half only, its words in ld.w[0]; y[m][0] gets it.
+template <int G, Act A, int MT, PacketFormat F, class S, int kCols = 2>
 __device__ __forceinline__ void native_compute_group(const S& sm,
                                                      const NativeLoad<G>& ld, int gl, int t,
                                                      uint32_t mask_lo, uint32_t mask_hi,
-                                                     float (&y)[MT][2]) {
+                                                     float (&y)[MT][2], int half = 0) {
+  static_assert(kCols == 2 || G == 128, "half slabs need G = 128");
   constexpr int U = native_unit_words(G);
   // One accumulator per (row, column): with the odd nibbles unpacked as 64 + q both nibble
   // positions add into it. A single row keeps a second one so that the dependent dot2 chains are
@@ -318,7 +338,7 @@ __device__ __forceinline__ void native_compute_group(const S& sm,
     // The offset term divided by alpha seeds the accumulator (see native_stage_store).
     const float seed = sm.sums_at(m, gl, t).x;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kCols; ++i) {
       acc[m][i][0] = seed;
       if constexpr (kAcc == 2) {
         acc[m][i][kAcc - 1] = 0.0f;
@@ -329,7 +349,7 @@ __device__ __forceinline__ void native_compute_group(const S& sm,
   for (int j = 0; j < U; ++j) {
     uint32_t e0[2], o0[2], e1[2], o1[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kCols; ++i) {
       const uint32_t wv = unit_word<G>(ld, i, j);
       const uint32_t w8 = wv >> 8;
       e0[i] = (wv & mask_lo) | kBiasLow;   // 1024+q for k0,k4
@@ -341,7 +361,7 @@ __device__ __forceinline__ void native_compute_group(const S& sm,
     for (int m = 0; m < MT; ++m) {
       const uint4 xp = sm.x_at(m, gl, U * t + j);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < kCols; ++i) {
         float& a0 = acc[m][i][0];
         float& a1 = acc[m][i][kAcc - 1];
         a0 = dot2<Act::kF16>(e0[i], xp.x, a0);
@@ -359,9 +379,10 @@ __device__ __forceinline__ void native_compute_group(const S& sm,
         uint32_t, __builtin_bit_cast(half2_t, ld.alpha) * __builtin_bit_cast(half2_t, ld.zp));
   }
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const float a = half_bits_to_float(static_cast<uint16_t>(ld.alpha >> (16 * i)));
-    const float b = half_bits_to_float(static_cast<uint16_t>(beta_pair >> (16 * i)));
+  for (int i = 0; i < kCols; ++i) {
+    const int sh = 16 * (kCols == 2 ? i : half);
+    const float a = half_bits_to_float(static_cast<uint16_t>(ld.alpha >> sh));
+    const float b = half_bits_to_float(static_cast<uint16_t>(beta_pair >> sh));
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       float sum = acc[m][i][0];

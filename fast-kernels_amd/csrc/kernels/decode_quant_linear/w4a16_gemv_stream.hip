@@ -67,7 +67,7 @@ struct StreamLds {
 // kW waves per workgroup, D register buffers (slabs in flight) per wave: kW * D slabs of 2 KB
 // (G = 128) or 1 KB (G = 64) in flight per workgroup, one workgroup per CU. kStageSlots passes
 // of 64 / (G / 8) groups per wave stage K <= kStageSlots * 64 * kW * 8 activations.
-template <int G, Act A, PacketFormat F, int kStageSlots, int kW, int D, bool kTail>
+template <int G, Act A, PacketFormat F, int kStageSlots, int kW, int D, bool kTail, bool kHalf>
 __global__ void __launch_bounds__(64 * (kW + (kTail ? 1 : 0)), 1)
     w4a16_gemv_stream_kernel(GemvParams p) {
   extern __shared__ uint4 stream_lds[];
@@ -152,7 +152,10 @@ __global__ void __launch_bounds__(64 * (kW + (kTail ? 1 : 0)), 1)
 
   // This wave's slabs: u0 + wave + kW j, j < n_w. Past its last slab a wave re-reads that slab,
   // so every buffer slot is loaded unconditionally (and never past the range).
-  const uint32_t u0 = static_cast<uint32_t>(b) * static_cast<uint32_t>(whole) * ng;
+  // kHalf: workgroup b streams half (b & 1) of slice b / 2 (one half-slice per workgroup).
+  const int half = kHalf ? (b & 1) : 0;
+  const uint32_t u0 = (kHalf ? static_cast<uint32_t>(b >> 1)
+                             : static_cast<uint32_t>(b) * static_cast<uint32_t>(whole)) * ng;
   const int n_blk = static_cast<int>(ng) / (kW * D);  // blocks of D slabs per wave and slice
   const int n_t = kTail ? p.stream_tail / kW : 0;     // the wave's slabs of the tail piece
   const int n_w = n_t + whole * n_blk * D;
@@ -170,6 +173,13 @@ __global__ void __launch_bounds__(64 * (kW + (kTail ? 1 : 0)), 1)
                      : base + static_cast<size_t>(c - n_t) * step;
     } else {
       return base + static_cast<size_t>(c) * step;
+    }
+  };
+  auto load_slab = [&](NativeLoad<G>& ld, const uint8_t* ptr) {
+    if constexpr (kHalf) {
+      native_load_half<G, F>(ld, ptr, lane, half);
+    } else {
+      native_load<G, F>(ld, ptr, lane);
     }
   };
 
@@ -202,7 +212,7 @@ __global__ void __launch_bounds__(64 * (kW + (kTail ? 1 : 0)), 1)
   NativeLoad<G> buf[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
-    native_load<G, F>(buf[d], slab(d), lane);
+    load_slab(buf[d], slab(d));
     __builtin_amdgcn_sched_barrier(0);  // the same issue order as the refills in the loop
   }
   int staged = 0;
@@ -233,8 +243,9 @@ __global__ void __launch_bounds__(64 * (kW + (kTail ? 1 : 0)), 1)
   auto block = [&](int gl0) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      native_compute_group<G, A, 1, F>(sm, buf[d], gl0 + kW * d, t, mask_lo, mask_hi, y);
-      native_load<G, F>(buf[d], slab(j + d + D), lane);
+      native_compute_group<G, A, 1, F, StreamLds<G>, kHalf ? 1 : 2>(sm, buf[d], gl0 + kW * d, t,
+                                                                    mask_lo, mask_hi, y, half);
+      load_slab(buf[d], slab(j + d + D));
       // Issue the refill here, not after the block's later slabs: the scheduler would otherwise
       // sink every load below the block's arithmetic and drain the pipeline once per block.
       __builtin_amdgcn_sched_barrier(0);
@@ -247,14 +258,18 @@ __global__ void __launch_bounds__(64 * (kW + (kTail ? 1 : 0)), 1)
     float y0 = y[0][0];
     float y1 = y[0][1];
     y0 += __shfl_xor(y0, 16);
-    y1 += __shfl_xor(y1, 16);
     y0 += __shfl_xor(y0, 32);
-    y1 += __shfl_xor(y1, 32);
+    if constexpr (!kHalf) {
+      y1 += __shfl_xor(y1, 16);
+      y1 += __shfl_xor(y1, 32);
+    }
     y[0][0] = 0.0f;
     y[0][1] = 0.0f;
     if (lane < 16) {
       red[slot][wave][lane] = y0;
-      red[slot][wave][lane + 16] = y1;
+      if constexpr (!kHalf) {
+        red[slot][wave][lane + 16] = y1;
+      }
     }
     lds_barrier();
   };
@@ -291,14 +306,16 @@ __global__ void __launch_bounds__(64 * (kW + (kTail ? 1 : 0)), 1)
     const int slot = (r + (kTail ? 1 : 0)) & 1;
     reduce_slice(slot);
     // One wave, rotating with the slice, writes it.
-    if (wave == (r & (kW - 1)) && lane < kSliceCols) {
+    constexpr int kCols = kHalf ? kSliceCols / 2 : kSliceCols;
+    if (wave == (r & (kW - 1)) && lane < kCols) {
       float v = red[slot][0][lane];
 #pragma unroll
       for (int w = 1; w < kW; ++w) {
         v += red[slot][w][lane];
       }
-      const size_t slice = static_cast<size_t>(b) * whole + r;
-      p.out[slice * kSliceCols + lane] = float_to_act_bits<A>(v);
+      const size_t col = kHalf ? static_cast<size_t>(b >> 1) * kSliceCols + 16 * half + lane
+                               : (static_cast<size_t>(b) * whole + r) * kSliceCols + lane;
+      p.out[col] = float_to_act_bits<A>(v);
     }
   }
   // Retire the loads of re-read tail slots before the workgroup ends.
@@ -317,10 +334,17 @@ hipError_t launch_stream_t(const GemvLaunch& l, hipStream_t stream) {
   p.xcd_remap = grid % 8 == 0 ? 1 : 0;
   const size_t lds = stream_lds_bytes(G, l.K / G + 1);
   if (l.stream_tail > 0) {
-    hipLaunchKernelGGL((w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, true>), dim3(grid),
-                       dim3(64 * (kW + 1)), lds, stream, p);
+    hipLaunchKernelGGL((w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, true, false>),
+                       dim3(grid), dim3(64 * (kW + 1)), lds, stream, p);
+  } else if (l.stream_half) {
+    if constexpr (G == 128) {
+      hipLaunchKernelGGL((w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, false, true>),
+                         dim3(grid), dim3(64 * kW), lds, stream, p);
+    } else {
+      return hipErrorInvalidValue;
+    }
   } else {
-    hipLaunchKernelGGL((w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, false>),
+    hipLaunchKernelGGL((w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, false, false>),
                        dim3(grid), dim3(64 * kW), lds, stream, p);
   }
   return hipGetLastError();
@@ -381,7 +405,13 @@ hipError_t launch_w4a16_gemv_stream(const GemvLaunch& l, hipStream_t stream) {
   }
   const long long slices = l.N / kSliceCols;
   const long long whole_slices = static_cast<long long>(l.stream_whole) * l.stream_grid;
-  if (l.stream_tail == 0) {
+  if (l.stream_half) {
+    // one half-slice (16 columns of a G = 128 slice) per workgroup
+    if (l.group_size != 128 || l.stream_tail != 0 || l.stream_whole != 1 ||
+        l.stream_grid != 2 * slices) {
+      return hipErrorInvalidValue;
+    }
+  } else if (l.stream_tail == 0) {
     if (l.stream_whole == 0 || whole_slices != slices) {
       return hipErrorInvalidValue;
     }

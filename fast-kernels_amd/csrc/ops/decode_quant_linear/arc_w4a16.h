@@ -80,12 +80,13 @@ struct ArcW4A16Plan {
   int groups_per_workgroup;     // stream-K run length in (tile, group) units
   int max_tile_contributors;    // workgroups that can share one slice
   std::size_t workspace_bytes;  // caller workspace needed by arc_w4a16_forward_ex
-  int slice_cols;               // columns per workgroup slice of a tile (128, 64 or 32)
+  int slice_cols;               // columns per workgroup slice of a tile (128, 64, 32 or 16)
   int schedule;                 // kSchedule*: how the workgroups walk their units
   int stream_depth;             // kScheduleStream: slabs in flight per wave
   int stream_whole;             // kScheduleStream: whole slices per workgroup
   int stream_tail;              // kScheduleStream: groups of each workgroup's tail piece (0: none)
   int stream_parts;             // kScheduleStream: workgroups sharing one tail slice
+  int stream_half;              // kScheduleStream: one half-slice (16 columns) per workgroup
 };
 
 // Launch schedules of a plan. kScheduleRuns: workgroups stream runs of one slice (or tile) at a

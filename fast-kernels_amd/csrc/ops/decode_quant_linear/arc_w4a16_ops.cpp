@@ -296,6 +296,15 @@ bool stream_tail_enabled() {
   return enabled;
 }
 
+// FK_W4A16_STREAM_HALF=0 keeps shapes with at most half as many slices as CUs off half-slices.
+bool stream_half_enabled() {
+  static const bool enabled = [] {
+    const char* v = std::getenv("FK_W4A16_STREAM_HALF");
+    return v == nullptr || std::string(v) != "0";
+  }();
+  return enabled;
+}
+
 // FK_W4A16_STREAM_SMALL=0 keeps shapes with fewer slices than CUs on the per-slice runs.
 bool stream_small_enabled() {
   static const bool enabled = [] {
@@ -396,6 +405,16 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
     if (slices < grid && per == num_groups && stream_small_enabled()) {
       grid = slices;
     }
+    // At most half as many slices as CUs (G = 128): one half-slice (16 columns, the first or
+    // second 1 KB of every slab) per workgroup, so every CU streams and no slice is split over
+    // K. Measured on MI355X (bench): 8B o (128 slices) 4.0 -> ? us, down (128 x 112 groups)
+    // 8.8 -> ? us.
+    const bool half = group_size == 128 && 2 * slices <= static_cast<long long>(cu_count) *
+                                                            stream_workgroups_per_cu() &&
+                      stream_half_enabled();
+    if (half) {
+      grid = 2 * slices;
+    }
     // Slices left over past whole ones per workgroup are cut into one piece per workgroup when
     // they divide the grid, the pieces are whole blocks of the waves and lie inside one staging
     // pass of a wave's groups (w4a16_gemv_stream.hip), and every workgroup also has a whole
@@ -409,7 +428,19 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
     const bool tail_ok = rem != 0 && slices > grid && stream_tail_enabled() && grid % rem == 0 &&
                          num_groups % parts == 0 && (num_groups / parts) % quantum == 0 &&
                          pass_groups % (num_groups / parts) == 0;
-    if (num_groups % quantum == 0 && lds <= lds_limit &&
+    if (half && num_groups % quantum == 0 && lds <= lds_limit) {
+      plan.schedule = kScheduleStream;
+      plan.slice_cols = fk::kSliceCols / 2;
+      plan.workgroups = static_cast<int>(grid);
+      plan.stream_depth = depth;
+      plan.stream_whole = 1;
+      plan.stream_half = 1;
+      plan.groups_per_workgroup = num_groups;
+      plan.max_tile_contributors = 1;
+      plan.workspace_bytes = 0;
+      return plan;
+    }
+    if (!half && num_groups % quantum == 0 && lds <= lds_limit &&
         ((slices >= grid && rem == 0) || tail_ok)) {
       plan.schedule = kScheduleStream;
       plan.slice_cols = fk::kSliceCols;
@@ -530,11 +561,14 @@ void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::u
     l.slice_pair = true;
     l.units_per_workgroup = 2 * plan.groups_per_workgroup;
   } else if (plan.schedule == kScheduleStream) {
-    if (format == fk::PacketFormat::kArc || batch != 1 || plan.slice_cols != fk::kSliceCols ||
+    const int cols = plan.stream_half ? fk::kSliceCols / 2 : fk::kSliceCols;
+    if (format == fk::PacketFormat::kArc || batch != 1 || plan.slice_cols != cols ||
         fuse != fk::GemvFuse::kNone) {
       throw std::logic_error("stream schedule on a plan that is not one unfused native row");
     }
     l.stream = true;
+    l.slice_cols = fk::kSliceCols;
+    l.stream_half = plan.stream_half != 0;
     l.stream_waves = fk::kStreamWaves;
     l.stream_depth = plan.stream_depth;
     l.stream_grid = plan.workgroups;

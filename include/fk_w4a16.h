@@ -107,15 +107,18 @@ typedef struct fk_arc_w4a16_plan {
   int groups_per_workgroup;  /* run of (tile, group) units each workgroup streams */
   int max_tile_contributors; /* workgroups that can share one slice (1 = none shared) */
   size_t workspace_bytes;    /* workspace fk_arc_w4a16_forward_ex needs */
-  int slice_cols;            /* columns of a tile per workgroup slice: 128, 64 or 32 */
+  int slice_cols;            /* columns of a tile per workgroup slice: 128, 64, 32 or 16 */
   int schedule;              /* FK_SCHEDULE_*: how the workgroups walk their units */
 } fk_arc_w4a16_plan;
 
 /* Plan schedules. FK_SCHEDULE_RUNS: each workgroup streams runs of one slice (or tile) at a time.
  * FK_SCHEDULE_PAIRS: one-row native plans, each workgroup streams two adjacent whole 32-column
- * slices at once (slice_cols 64). FK_SCHEDULE_STREAM: one-row native plans on a persistent grid
- * (workgroups = CUs): each workgroup streams one contiguous range of groups_per_workgroup slabs
- * across slice boundaries, with the whole activation row staged in LDS (K <= 32768). */
+ * slices at once (slice_cols 64). FK_SCHEDULE_STREAM: one-row native plans, the whole activation
+ * row staged in LDS (K <= 32768), one workgroup per CU or per slice: each workgroup streams its
+ * whole slices as one contiguous range across slice boundaries, plus, when the slices do not
+ * divide over the CUs, one piece of a left-over slice (groups_per_workgroup is then not a
+ * multiple of K/G; the pieces are finished through the workspace). With at most half as many
+ * 32-column slices as CUs (G = 128) a workgroup streams half a slice (slice_cols 16). */
 #define FK_SCHEDULE_RUNS 0
 #define FK_SCHEDULE_PAIRS 1
 #define FK_SCHEDULE_STREAM 2
@@ -178,7 +181,8 @@ int fk_convert_native_to_arc_packets(const void* native_packets, void* arc_packe
 
 /* Launch plan of fk_arc_w4a16_forward_native for a packet format (arguments as
  * fk_arc_w4a16_plan_for). For the native formats below 16 activation rows slice_cols is 32, or
- * 64 for one activation row when a workgroup streams two adjacent 32-column slabs at once. */
+ * for one activation row 64 when a workgroup streams two adjacent 32-column slabs at once and 16
+ * when it streams half of each slab. */
 int fk_w4a16_plan_for_format(int batch, int n, int k, int group_size, int activation_dtype,
                              int split_k_slices, int cu_count, int packet_format,
                              fk_arc_w4a16_plan* plan);

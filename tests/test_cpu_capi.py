@@ -223,8 +223,8 @@ def test_native_format_validation_without_gpu(lib: ctypes.CDLL) -> None:
         ((1, 57344, 8192, 128), (32, 448, 256, 2)),    # 70B gate_up: 7 whole slices per CU
         ((1, 8192, 28672, 128), (32, 224, 256, 2)),    # 70B down: one slice of 224 groups per CU
         ((1, 8192, 28672 + 128, 128), (32, 113, 510, 0)),  # 225 groups: not a multiple of 16
-        ((1, 4096, 4096, 128), (32, 32, 128, 2)),      # 128 slices, K short: streamed, one per workgroup
-        ((1, 4096, 14336, 128), (32, 56, 256, 0)),     # 128 slices, 112 groups: two runs of 56
+        ((1, 4096, 4096, 128), (16, 32, 256, 2)),      # 128 slices: a half slice per CU
+        ((1, 4096, 14336, 128), (16, 112, 256, 2)),    # 128 slices of 112 groups: halves, whole K
         ((4, 14336, 4096, 64), (32, 64, 448, 0)),      # four rows share a slice's runs
         ((16, 14336, 4096, 64), (128, 16, 448, 0)),    # matrix cores: the reference-format plan
     ],

@@ -183,6 +183,10 @@ def test_config4_llama8b_decode_step_graph() -> None:
         (28672, 4096, 128, "f16", False),   # 3 slices + a half
         (12288, 4096, 64, "bf16", False),   # G = 64: halves of 64 groups
         (10240, 16384, 64, "f16", True),    # G = 64: quarters of 256 groups
+        # half slices (G = 128, at most half as many slices as CUs)
+        (4096, 4096, 128, "bf16", False),   # 8B o
+        (4096, 14336, 128, "f16", True),    # 8B down, asymmetric
+        (1024, 2048, 128, "bf16", True),    # 64 workgroups
     ],
 )
 def test_stream_schedule_variants(n: int, k: int, g: int, act: str, asym: bool) -> None:
