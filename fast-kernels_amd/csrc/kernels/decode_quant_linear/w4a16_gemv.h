@@ -44,20 +44,18 @@ struct GemvLaunch {
   // once (two waves per slice), which needs units_per_workgroup to be a multiple of 2 K/G.
   bool slice_pair = false;
   // Native formats, one activation row, unfused: the persistent stream schedule
-  // (w4a16_gemv_stream.hip): each workgroup streams one contiguous run of units_per_workgroup
-  // slabs with the whole activation row staged in LDS.
+  // (w4a16_gemv_stream.hip), the activation row staged whole in LDS.
   bool stream = false;
-  int stream_waves = 0;   // stream schedule: waves per workgroup (kStreamWaves)
+  int stream_waves = 0;   // stream schedule: streaming waves per workgroup (kStreamWaves)
   int stream_depth = 0;   // stream schedule: units in flight per wave
   int stream_grid = 0;    // stream schedule: workgroups
-  int stream_whole = 0;   // stream schedule: whole slices per workgroup
-  // Stream schedule with a tail: the slices past stream_grid * stream_whole are cut into
-  // stream_parts pieces of stream_tail groups, one per workgroup, finished through the
-  // workspace (counters: one per tail slice; partials: 32 floats per workgroup).
-  int stream_tail = 0;
-  int stream_parts = 0;
-  // Stream schedule over half-slices (G = 128): workgroup b streams the 16 columns 16 * (b & 1)
-  // .. of slice b / 2, reading half of every slab (stream_grid = 2 * slices, stream_whole = 1).
+  int stream_whole = 0;   // stream schedule: whole slices per workgroup (1 for half slices)
+  // The slices left over past stream_grid * stream_whole (fewer than the workgroups) are dealt
+  // as equal block ranges, a head and a tail piece per workgroup, finished through the
+  // workspace: counters, one per slice; partials, 2 * 32 floats per workgroup.
+  bool stream_pieces = false;
+  // Half-slices (G = 128, one row): workgroup b streams the 16 columns 16 * (b & 1) .. of slice
+  // b / 2, reading half of every slab (stream_grid = 2 * slices).
   bool stream_half = false;
 };
 
@@ -69,13 +67,21 @@ constexpr int kStreamMaxK = 32768;
 inline size_t stream_lds_bytes(int group_size, int num_groups) {
   return static_cast<size_t>(num_groups) * (static_cast<size_t>(group_size / 8) * 16 + 32 + 4);
 }
-// Waves per workgroup of the stream schedule, and the units (slabs) in flight per wave it may
-// use: 4 or 8 KB of weights per wave (a G = 128 slab is 2 KB, a G = 64 slab 1 KB). K/G and
-// units_per_workgroup must be multiples of kStreamWaves * depth.
+// Streaming waves per workgroup of the stream schedule and the weights in flight per wave (4 KB:
+// two G = 128 slabs of 2 KB or four G = 64 slabs of 1 KB). K/G must be a multiple of
+// kStreamWaves * depth (a block).
 constexpr int kStreamWaves = 8;
+constexpr int kStreamKB = 4;
 constexpr int stream_depth_for_kb(int group_size, int kb) { return kb / (group_size == 128 ? 2 : 1); }
-// Static LDS of the stream kernel besides the dynamic part (two reduction slots, up to 8 waves).
+// Most 32-column slices a stream launch with pieces may have (one arrival counter each).
+constexpr int kStreamMaxSlices = 16384;
+// Static LDS of the stream kernel besides the dynamic part: two reduction slots of 8 waves x
+// rows x 32 floats, per activation row.
 constexpr size_t kStreamStaticLdsBytes = 2 * 8 * 32 * sizeof(float);
+// Workspace floats of a stream launch with pieces: two partial slots of rows x 32 per workgroup.
+inline size_t stream_partial_floats(int grid, int rows) {
+  return static_cast<size_t>(grid) * 2 * rows * kSliceCols;
+}
 
 // Activation rows per m-tile for a batch: 1, 2, 4, 8 on the dot2 GEMV kernel, kMfmaRows (from
 // kMfmaMinBatch rows) on the matrix-core kernel.

@@ -110,10 +110,7 @@ struct GemvParams {
   const uint16_t* norm_weight;      // RMSNorm prologue: gamma [K] (activation dtype), else null
   float eps;                        // RMSNorm prologue: epsilon
   int pair;                         // native slabs: each run streams two adjacent whole slices
-  int stream_whole;                 // stream schedule (w4a16_gemv_stream.hip): whole slices
-                                    // per workgroup
-  int stream_tail;                  // stream schedule: groups of the workgroup's tail piece
-  int stream_parts;                 // stream schedule: workgroups sharing one tail slice
+  int stream_whole;                 // stream schedule: whole slices per workgroup
 };
 
 template <int G, int MT, int CW>

@@ -1,44 +1,45 @@
 // W4A16 GEMV over native slabs for one activation row: the persistent "stream" schedule.
 //
-// The native slabs of a buffer are laid out [slice][group] (w4a16_device.h), so the slices
-// b * whole .. (b + 1) * whole - 1 are one contiguous byte range. When the 32-column slices divide
-// evenly over one workgroup per CU (Llama-70B o, gate_up and down: 256, 1792 and 256 slices on
-// 256 CUs), workgroup b streams that range without a break:
+// The native slabs of a buffer are laid out [slice][group] (w4a16_device.h), so a run of slices is
+// one contiguous byte range. With one workgroup per CU, workgroup b streams the stream_whole
+// slices b * stream_whole .. as one range. The slices left over when they do not divide evenly
+// (fewer than the workgroups) are cut into blocks of kW * D groups (one slab in each of a wave's D
+// register buffers) and dealt to the workgroups as equal contiguous block ranges ("stream-K"), so
+// every CU streams the same number of bytes whatever the shape. Such a range is shorter than a
+// slice: at most a head piece (the end of a slice an earlier workgroup starts) and a tail piece
+// (the start of a slice a later workgroup finishes).
 //
-//  * The whole activation row is staged in LDS once per workgroup (dynamic LDS: K/G groups of
-//    re-paired fp16 values and per-quarter sums, as native_stage_unit writes them) instead of
-//    once per slice and chunk. Wave w only ever computes groups g = w (mod 8), so each wave
-//    stages its own groups and no workgroup barrier separates staging from streaming. Staging
-//    is spread over the first slice: one pass of the wave's groups before its first block, one
-//    more after each block, so that the first weights are consumed as soon as they arrive.
-//  * The staging loads are issued before the first weight loads, so the conversion overlaps
-//    the weights' HBM latency (the load counter retires in order, so waiting for the activations
-//    does not wait for the weights behind them).
-//  * Wave w takes slabs w, w + 8, w + 16, ... of the range through D register buffers, and the
-//    pipeline runs across slice boundaries: the loads of the next slice's first slabs are in
-//    flight while a slice is reduced, so the stream does not drain at each slice as it does when
-//    every slice is its own workgroup run.
-//  * At a slice boundary each wave folds its lane partials over the column's four quarters,
-//    writes them to one of two LDS slots and meets the others at a barrier (its loads stay in
-//    flight); one wave, rotating with the slice, adds the eight waves' totals in wave order and
-//    writes the 32 outputs. No slice is shared, so there is no fix-up and no workspace.
-//
-// Slices that do not divide evenly (Llama-70B qkv: 320 slices on 256 CUs) leave stream_grid *
-// stream_whole slices to the whole ranges and cut each remaining "tail" slice into stream_parts
-// pieces of stream_tail groups, one piece per workgroup (kTail): 1.25 slices per CU instead of
-// one round of 256 slices and a second of 64. A workgroup streams its piece first, then its whole
-// slices, so the hand-off of the piece is off the critical path:
-//
-//  * The piece's activations are staged first (one extra pass; the piece lies inside one pass).
-//  * After the piece, the eight streaming waves write their totals to LDS and meet a ninth,
-//    control wave at the barrier, and go on streaming. The control wave adds the totals, stores
-//    the piece's 32 partial sums to the workspace, and bumps the tail slice's arrival counter
-//    once they are acknowledged (agent scope); the workgroup that arrives last adds the parts' partials
-//    in part order, so the result does not depend on arrival order, writes the 32 outputs and
-//    resets the counter to zero for the next call. The control wave's waits (the store, the
-//    counter's return, the partials' loads) stall no weight stream.
-//  * With the logical-to-hardware workgroup remap the parts of one tail slice run on one XCD,
-//    whose L2 then holds the partials the last part reads.
+//  * The activation rows are staged in LDS once per workgroup (dynamic LDS: K/G groups of
+//    re-paired fp16 values and per-quarter sums per row, as native_stage_unit writes them). Wave w
+//    only ever computes groups g = w (mod kW), so each wave stages its own groups and no
+//    workgroup barrier separates staging from streaming. Without pieces the staging is spread
+//    over the first slice (one pass of the wave's groups before its first block, one more after
+//    each block), so that the first weights are consumed as soon as they arrive; with pieces all
+//    passes are staged first (a piece may start anywhere in K).
+//  * The staging loads are issued before the first weight loads, so the conversion overlaps the
+//    weights' HBM latency (the load counter retires in order, so waiting for the activations does
+//    not wait for the weights behind them).
+//  * Wave w takes slabs w, w + kW, w + 2 kW, ... of each part (pieces first, then the whole
+//    slices) through D register buffers, and the pipeline runs across part and slice boundaries: the loads of the next slabs are in flight
+//    while a slice is reduced, so the stream never drains before the workgroup's last slab. The
+//    slab address is a uniform select between the three parts' bases, so the pipelined loops have
+//    no branch.
+//  * At the end of a slice or piece each wave folds its lane partials over the column's four
+//    quarters, writes them to one of two LDS slots and meets the others at a barrier (its loads
+//    stay in flight). A whole slice is then written by one streaming wave, rotating with the
+//    slice, which adds the waves' totals in wave order.
+//  * The pieces are streamed first (head, then tail) and handed to a ninth, control wave (kPieces)
+//    so that their hand-off is off the critical path: the control wave adds the waves' totals,
+//    stores the piece's partial sums to the workspace (one slot per workgroup and piece) and
+//    bumps the slice's arrival counter once they are acknowledged; the workgroup that arrives
+//    last adds the slice's parts in workgroup order, so the result does not depend on arrival
+//    order, writes the outputs and resets the counter for the next call. The streaming waves go
+//    on meanwhile; the control wave meets them at every later barrier (s_barrier counts waves).
+//  * With the logical-to-hardware workgroup remap consecutive ranges, and so the parts of a split
+//    slice, run on one XCD, whose L2 then serves the partials the last part reads.
+//  * kHalf (one row, G = 128, at most half as many slices as CUs): workgroup b streams 16 columns,
+//    the first or second KB of every slab of slice b / 2, so that every CU streams and no slice
+//    is split over K.
 //
 // Math per group is native_compute_group's (w4a16_gemv_native.h); results equal the per-slice
 // kernel's up to fp32 summation order across waves.
@@ -47,31 +48,72 @@
 namespace fk {
 namespace {
 
-// LDS view of a whole staged activation row: xs [NG][G/8] re-paired fp16 words, sums [NG][4]
-// per-quarter offset terms, scale [NG] bf16 staging scales (the layout of NativeSmem for one row
-// and every group of K).
+// LDS view of the staged activation rows: xs [MT][NG + 1][G/8] re-paired fp16 words, sums
+// [MT][NG + 1][4] per-quarter offset terms, scale [MT][NG + 1] bf16 staging scales (the layout of
+// NativeSmem for every group of K, plus a spare group slot per row for branch-free staging).
 template <int G>
 struct StreamLds {
   uint4* xs;
   float2* sums;
   float* scale;
+  int slots;  // NG + 1
 
-  __device__ uint4 x_at(int, int gl, int i) const { return xs[gl * (G / 8) + i]; }
-  __device__ float2 sums_at(int, int gl, int t) const { return sums[gl * 4 + t]; }
-  __device__ float scale_at(int, int gl) const { return scale[gl]; }
-  __device__ void set_x(int, int gl, int i, uint4 v) { xs[gl * (G / 8) + i] = v; }
-  __device__ void set_sums(int, int gl, int t, float2 v) { sums[gl * 4 + t] = v; }
-  __device__ void set_scale(int, int gl, float v) { scale[gl] = v; }
+  __device__ int at(int m, int gl) const { return m * slots + gl; }
+  __device__ uint4 x_at(int m, int gl, int i) const { return xs[at(m, gl) * (G / 8) + i]; }
+  __device__ float2 sums_at(int m, int gl, int t) const { return sums[at(m, gl) * 4 + t]; }
+  __device__ float scale_at(int m, int gl) const { return scale[at(m, gl)]; }
+  __device__ void set_x(int m, int gl, int i, uint4 v) { xs[at(m, gl) * (G / 8) + i] = v; }
+  __device__ void set_sums(int m, int gl, int t, float2 v) { sums[at(m, gl) * 4 + t] = v; }
+  __device__ void set_scale(int m, int gl, float v) { scale[at(m, gl)] = v; }
 };
 
-// kW waves per workgroup, D register buffers (slabs in flight) per wave: kW * D slabs of 2 KB
-// (G = 128) or 1 KB (G = 64) in flight per workgroup, one workgroup per CU. kStageSlots passes
-// of 64 / (G / 8) groups per wave stage K <= kStageSlots * 64 * kW * 8 activations.
-template <int G, Act A, PacketFormat F, int kStageSlots, int kW, int D, bool kTail, bool kHalf>
-__global__ void __launch_bounds__(64 * (kW + (kTail ? 1 : 0)), 1)
+// A workgroup's parts: stream_whole whole slices, and (with pieces) its share of the slices left
+// over past grid * stream_whole of them, as an equal contiguous range of blocks (kW * D groups;
+// nbs blocks a slice) of fewer blocks than a slice: a head piece (the end of a slice an earlier
+// workgroup starts) and a tail piece (the start of a slice a later workgroup finishes).
+struct StreamRange {
+  int head_slice, head_blk0, head_len;  // head piece: blocks head_blk0 .. of head_slice
+  int tail_slice, tail_len;             // tail piece: the first tail_len blocks of tail_slice
+  int whole_slice0, whole;              // whole slices whole_slice0 ..
+};
+
+// First left-over block of workgroup b (left-over blocks numbered from 0). 32-bit arithmetic: the
+// host bounds grid * total below 2^31 (a 64-bit division costs hundreds of instructions).
+__device__ __forceinline__ int range_start(int b, int total, int grid) {
+  return static_cast<int>(static_cast<uint32_t>(b * total) / static_cast<uint32_t>(grid));
+}
+
+// Workgroup owning left-over block x: the last b with range_start(b) <= x.
+__device__ __forceinline__ int range_owner(int x, int total, int grid) {
+  return static_cast<int>(static_cast<uint32_t>((x + 1) * grid - 1) / static_cast<uint32_t>(total));
+}
+
+// The pieces of workgroup b's left-over range; slice s0 is the first left-over slice.
+__device__ __forceinline__ void stream_pieces(StreamRange& r, int b, int total, int grid, int nbs,
+                                              int s0) {
+  const int blk0 = range_start(b, total, grid);
+  const int blk1 = range_start(b + 1, total, grid);
+  const int q0 = blk0 / nbs;
+  const int off0 = blk0 - q0 * nbs;
+  r.head_slice = s0 + q0;
+  r.head_blk0 = off0;
+  r.head_len = off0 != 0 ? min(blk1, blk0 - off0 + nbs) - blk0 : 0;
+  const int c = blk0 + r.head_len;  // a slice start, or blk1
+  // the range is shorter than a slice, so what follows the head piece is the start of one slice
+  r.tail_slice = s0 + c / nbs;
+  r.tail_len = blk1 - c;
+}
+
+// kW streaming waves per workgroup (plus the control wave with kPieces), D register buffers
+// (slabs in flight) per wave, MT activation rows; one workgroup per CU. kStageSlots passes of
+// 64 / (G / 8) groups per wave stage K <= kStageSlots * 64 * kW * 8 activations.
+template <int G, Act A, PacketFormat F, int kStageSlots, int kW, int D, int MT, bool kPieces,
+          bool kHalf>
+__global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     w4a16_gemv_stream_kernel(GemvParams p) {
+  static_assert(!kHalf || (MT == 1 && !kPieces && G == 128), "half slices: one row, no pieces");
   extern __shared__ uint4 stream_lds[];
-  __shared__ float red[2][kW][kSliceCols];
+  __shared__ float red[2][kW][MT * kSliceCols];
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -85,59 +127,127 @@ __global__ void __launch_bounds__(64 * (kW + (kTail ? 1 : 0)), 1)
   if (p.xcd_remap) {
     b = (b & 7) * (grid >> 3) + (b >> 3);
   }
-  const uint32_t ng = static_cast<uint32_t>(p.NG);
-  const int whole = p.stream_whole;
-  // The tail piece: groups gt0 .. gt0 + stream_tail - 1 of tail slice `tail_slice`.
-  const int parts = kTail ? p.stream_parts : 1;
-  const int tail_local = b / parts;
-  const int part = b - tail_local * parts;
-  const int tail_slice = grid * whole + tail_local;
-  const int gt0 = part * p.stream_tail;
-  if constexpr (kTail) {
+  const int ng = p.NG;
+  constexpr int Q = kW * D;  // groups per block
+  const int nbs = ng / Q;    // blocks per slice
+  constexpr int kOut = MT * kSliceCols;  // outputs of a slice
+  constexpr int kOutPerLane = (kOut + 63) / 64;
+
+  StreamRange rg;
+  rg.head_slice = 0;
+  rg.head_blk0 = 0;
+  rg.head_len = 0;
+  rg.tail_slice = 0;
+  rg.tail_len = 0;
+  int half = 0;
+  // Left-over slices (pieces): the first, and their blocks.
+  const int s_left = grid * p.stream_whole;
+  const int left_blocks = (p.N / kSliceCols - s_left) * nbs;
+  if constexpr (kHalf) {
+    half = b & 1;
+    rg.whole_slice0 = b >> 1;
+    rg.whole = 1;
+  } else {
+    rg.whole_slice0 = b * p.stream_whole;
+    rg.whole = p.stream_whole;
+    if constexpr (kPieces) {
+      stream_pieces(rg, b, left_blocks, grid, nbs, s_left);
+    }
+  }
+
+  if constexpr (kPieces) {
     if (wave == kW) {
-      // Control wave: finishes the tail piece, then meets the streaming waves at every slice's
-      // barrier (s_barrier counts waves, not code locations).
-      lds_barrier();
-      if (lane < kSliceCols) {
-        float v = red[0][0][lane];
+      // Control wave. Totals of the pieces first (a barrier each), then their hand-offs, then the
+      // whole slices' barriers.
+      float v[2][kOutPerLane];
+      int slot = 0;
+      const bool has[2] = {rg.head_len > 0, rg.tail_len > 0};
 #pragma unroll
-        for (int w = 1; w < kW; ++w) {
-          v += red[0][w][lane];
-        }
-        float* ws = p.partials + static_cast<size_t>(tail_local) * parts * kSliceCols;
-        __hip_atomic_store(&ws[part * kSliceCols + lane], v, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      }
-      // Hand-off without cache-wide fences (an agent-scope release writes back the whole L2 and
-      // costs microseconds): the partials are agent-scope stores, which gfx950 writes through the
-      // XCD's L2 to the memory-side coherence point; s_waitcnt vmcnt(0) holds the wave until all
-      // of them are acknowledged there, and only then is the counter bumped. The last part's
-      // loads are agent-scope too, so they miss the L2 and read the coherence point, after its
-      // counter bump has returned the final count. Every part does the same, so whichever
-      // arrives last sees all parts' partials.
-      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-      uint32_t prev = 0;
-      if (lane == 0) {
-        prev = __hip_atomic_fetch_add(&p.counters[tail_local], 1u, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-      }
-      prev = __builtin_amdgcn_readfirstlane(prev);
-      if (prev == static_cast<uint32_t>(parts - 1)) {
-        if (lane < kSliceCols) {
-          const float* ws = p.partials + static_cast<size_t>(tail_local) * parts * kSliceCols;
-          float v = 0.0f;
-          for (int q = 0; q < parts; ++q) {
-            v += __hip_atomic_load(&ws[q * kSliceCols + lane], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+      for (int pc = 0; pc < 2; ++pc) {
+        if (has[pc]) {
+          lds_barrier();
+#pragma unroll
+          for (int i = 0; i < kOutPerLane; ++i) {
+            const int o = lane + 64 * i;
+            float s = 0.0f;
+            if (o < kOut) {
+#pragma unroll
+              for (int w = 0; w < kW; ++w) {
+                s += red[slot][w][o];
+              }
+            }
+            v[pc][i] = s;
           }
-          p.out[static_cast<size_t>(tail_slice) * kSliceCols + lane] = float_to_act_bits<A>(v);
-        }
-        if (lane == 0) {
-          __hip_atomic_store(&p.counters[tail_local], 0u, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+          slot ^= 1;
         }
       }
-      for (int r = 0; r < whole; ++r) {
+#pragma unroll
+      for (int pc = 0; pc < 2; ++pc) {
+        if (!has[pc]) {
+          continue;
+        }
+        const int slice = pc == 0 ? rg.head_slice : rg.tail_slice;
+        // This workgroup's slot: piece pc of workgroup b.
+        float* mine = p.partials + (static_cast<size_t>(b) * 2 + pc) * kOut;
+#pragma unroll
+        for (int i = 0; i < kOutPerLane; ++i) {
+          const int o = lane + 64 * i;
+          if (o < kOut) {
+            __hip_atomic_store(&mine[o], v[pc][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+        // Hand-off without cache-wide fences (an agent-scope release writes back the whole L2
+        // and costs microseconds): the partials are agent-scope stores, which gfx950 writes
+        // through the XCD's L2 to the memory-side coherence point; s_waitcnt vmcnt(0) holds the
+        // wave until all of them are acknowledged there, and only then is the counter bumped. The
+        // last part's loads are agent-scope too, so they miss the L2 and read the coherence
+        // point, after its counter bump has returned the final count. Every part does the same,
+        // so whichever arrives last sees all parts' partials.
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        // Parts of the slice: the workgroups owning its first and last block.
+        const int s0 = (slice - s_left) * nbs;
+        const int b_first = range_owner(s0, left_blocks, grid);
+        const int b_last = range_owner(s0 + nbs - 1, left_blocks, grid);
+        uint32_t prev = 0;
+        if (lane == 0) {
+          prev = __hip_atomic_fetch_add(&p.counters[slice], 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+        }
+        prev = __builtin_amdgcn_readfirstlane(prev);
+        if (prev == static_cast<uint32_t>(b_last - b_first)) {
+          float acc[kOutPerLane];
+#pragma unroll
+          for (int i = 0; i < kOutPerLane; ++i) {
+            acc[i] = 0.0f;
+          }
+          for (int bb = b_first; bb <= b_last; ++bb) {
+            // The slice is the head piece of a workgroup whose range starts inside it.
+            const int pp = range_start(bb, left_blocks, grid) > s0 ? 0 : 1;
+            const float* part = p.partials + (static_cast<size_t>(bb) * 2 + pp) * kOut;
+#pragma unroll
+            for (int i = 0; i < kOutPerLane; ++i) {
+              const int o = lane + 64 * i;
+              if (o < kOut) {
+                acc[i] += __hip_atomic_load(&part[o], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              }
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < kOutPerLane; ++i) {
+            const int o = lane + 64 * i;
+            const int m = o / kSliceCols;
+            if (o < kOut && m < p.M) {
+              p.out[static_cast<size_t>(m) * p.N + static_cast<size_t>(slice) * kSliceCols +
+                    o % kSliceCols] = float_to_act_bits<A>(acc[i]);
+            }
+          }
+          if (lane == 0) {
+            __hip_atomic_store(&p.counters[slice], 0u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+      }
+      for (int r = 0; r < rg.whole; ++r) {
         lds_barrier();
       }
       return;
@@ -145,35 +255,36 @@ __global__ void __launch_bounds__(64 * (kW + (kTail ? 1 : 0)), 1)
   }
 
   StreamLds<G> sm;
+  sm.slots = ng + 1;
   sm.xs = stream_lds;
-  // K/G groups and one spare group slot (stage_one)
-  sm.sums = reinterpret_cast<float2*>(stream_lds + static_cast<size_t>(p.NG + 1) * (G / 8));
-  sm.scale = reinterpret_cast<float*>(sm.sums + static_cast<size_t>(p.NG + 1) * 4);
+  sm.sums = reinterpret_cast<float2*>(stream_lds + static_cast<size_t>(MT) * sm.slots * (G / 8));
+  sm.scale = reinterpret_cast<float*>(sm.sums + static_cast<size_t>(MT) * sm.slots * 4);
 
-  // This wave's slabs: u0 + wave + kW j, j < n_w. Past its last slab a wave re-reads that slab,
-  // so every buffer slot is loaded unconditionally (and never past the range).
-  // kHalf: workgroup b streams half (b & 1) of slice b / 2 (one half-slice per workgroup).
-  const int half = kHalf ? (b & 1) : 0;
-  const uint32_t u0 = (kHalf ? static_cast<uint32_t>(b >> 1)
-                             : static_cast<uint32_t>(b) * static_cast<uint32_t>(whole)) * ng;
-  const int n_blk = static_cast<int>(ng) / (kW * D);  // blocks of D slabs per wave and slice
-  const int n_t = kTail ? p.stream_tail / kW : 0;     // the wave's slabs of the tail piece
-  const int n_w = n_t + whole * n_blk * D;
+  // The wave's slabs, in order: the head piece's, the tail piece's, then the whole slices' (one
+  // contiguous range). Past its last slab a wave re-reads that slab, so every buffer slot is
+  // loaded unconditionally (and never past the buffer).
+  const int n_h = rg.head_len * D;
+  const int n_t = rg.tail_len * D;
+  const int n_w = n_h + n_t + rg.whole * nbs * D;
   const int j_last = n_w - 1;
-  const uint8_t* base = p.packets + static_cast<size_t>(u0 + wave) * stride;
-  const uint8_t* tail_base =
-      p.packets + (static_cast<size_t>(tail_slice) * ng + gt0 + wave) * stride;
-  const size_t step = static_cast<size_t>(kW) * stride;
-  // The wave's slab i (clamped to its last): the tail piece's first, then the whole range. The
-  // choice is uniform (a scalar select), so the pipeline has no branch.
+  // Slab index of the wave's i-th slab: i * kW plus a per-part offset (uniform 32-bit arithmetic;
+  // selects of 64-bit addresses compile to branches).
+  const int off_w = rg.whole_slice0 * ng + wave - (n_h + n_t) * kW;
+  const int off_t = rg.tail_slice * ng + wave - n_h * kW;
+  const int off_h = rg.head_slice * ng + rg.head_blk0 * Q + wave;
   auto slab = [&](int i) -> const uint8_t* {
     const int c = min(i, j_last);
-    if constexpr (kTail) {
-      return c < n_t ? tail_base + static_cast<size_t>(c) * step
-                     : base + static_cast<size_t>(c - n_t) * step;
-    } else {
-      return base + static_cast<size_t>(c) * step;
+    int off = off_w;
+    if constexpr (kPieces) {
+      // 0/1 flags made opaque to the compiler (readfirstlane), which otherwise turns the choice
+      // into a lookup table in scratch memory
+      int in_t = c < n_h + n_t ? 1 : 0;
+      int in_h = c < n_h ? 1 : 0;
+      in_t = __builtin_amdgcn_readfirstlane(in_t);
+      in_h = __builtin_amdgcn_readfirstlane(in_h);
+      off += in_t * (off_t - off_w) + in_h * (off_h - off_t);
     }
+    return p.packets + static_cast<size_t>(static_cast<uint32_t>(c * kW + off)) * stride;
   };
   auto load_slab = [&](NativeLoad<G>& ld, const uint8_t* ptr) {
     if constexpr (kHalf) {
@@ -184,29 +295,21 @@ __global__ void __launch_bounds__(64 * (kW + (kTail ? 1 : 0)), 1)
   };
 
   // Activations: every pass's loads first. Pass i stages groups wave + kW (i * 64 / WR + l / WR)
-  // (lane l, word row l % WR); pass 0 before the first block, one more after each block of the
-  // first slice (pass i covers the wave's slabs 64 / WR * i .. of a slice, and a block needs D of
-  // them), and any left after it.
+  // (lane l, word row l % WR) of every row.
   constexpr int WR = G / 8;
   constexpr int kGroupsPerPass = 64 / WR;
-  const int n_pass = (p.NG / kW + kGroupsPerPass - 1) / kGroupsPerPass;
-  uint4 raw[kStageSlots];
+  const int n_pass = (ng / kW + kGroupsPerPass - 1) / kGroupsPerPass;
+  uint4 raw[kStageSlots][MT];
 #pragma unroll
   for (int i = 0; i < kStageSlots; ++i) {
     // clamped and unconditional (a load under a branch waits for the one before it); slots past
     // the wave's passes and groups past the row are never staged
-    const int g = min(wave + kW * (i * kGroupsPerPass + lane / WR), p.NG - 1);
-    raw[i] = *reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(g) * G + (lane % WR) * 8);
-  }
-  // The pass holding the tail piece's groups, loaded once more into a register of its own (picking
-  // it out of raw[] by a runtime index would put raw[] in scratch memory).
-  uint4 raw_tail = make_uint4(0u, 0u, 0u, 0u);
-  int g_tail = 0;
-  if constexpr (kTail) {
-    const int q = (gt0 / kW) / kGroupsPerPass;
-    g_tail = min(wave + kW * (q * kGroupsPerPass + lane / WR), p.NG);
-    raw_tail = *reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(min(g_tail, p.NG - 1)) * G +
-                                               (lane % WR) * 8);
+    const int g = min(wave + kW * (i * kGroupsPerPass + lane / WR), ng - 1);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      raw[i][m] = *reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * p.K +
+                                                  static_cast<size_t>(g) * G + (lane % WR) * 8);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   NativeLoad<G> buf[D];
@@ -219,13 +322,19 @@ __global__ void __launch_bounds__(64 * (kW + (kTail ? 1 : 0)), 1)
   // Stages the next pass from raw[0] and shifts the slots down (register moves; a runtime slot
   // index would put the slots in scratch memory).
   auto stage_one = [&]() {
-    // Groups past the row (the wave's last pass may be partial) are staged into a spare group
+    // Groups past the row (the wave's last pass may be partial) are staged into the spare group
     // slot past the row's, so the staging has no branch.
-    const int g = min(wave + kW * (staged * kGroupsPerPass + lane / WR), p.NG);
-    native_stage_unit<G, A, F>(sm, raw[0], 0, g, lane % WR);
+    const int g = min(wave + kW * (staged * kGroupsPerPass + lane / WR), ng);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      native_stage_unit<G, A, F>(sm, raw[0][m], m, g, lane % WR);
+    }
 #pragma unroll
     for (int i = 0; i + 1 < kStageSlots; ++i) {
-      raw[i] = raw[i + 1];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        raw[i][m] = raw[i + 1][m];
+      }
     }
     ++staged;
     // The wave reads back only what it wrote: its LDS accesses complete in order, so a
@@ -233,18 +342,29 @@ __global__ void __launch_bounds__(64 * (kW + (kTail ? 1 : 0)), 1)
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
+  stage_one();
+  if constexpr (kPieces) {
+    while (staged < n_pass) {
+      stage_one();
+    }
+  }
 
-  float y[1][2] = {{0.0f, 0.0f}};
+  float y[MT][2];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    y[m][0] = 0.0f;
+    y[m][1] = 0.0f;
+  }
   int j = 0;  // the wave's next slab to compute
-  // A block of D slabs of slice-local groups gl0 .., kW apart. Each slice gives every wave n_blk
-  // whole blocks (the host plans K/G as a multiple of kW * D), so the block loops have no branch:
-  // the compiler's wait for a buffer is then the in-order count of the loads issued after it,
-  // not a drain of the pipeline.
+  // A block of D slabs of slice-local groups gl0 .., kW apart. Every part is whole blocks (the
+  // host plans K/G as a multiple of kW * D), so the block loops have no branch: the compiler's
+  // wait for a buffer is then the in-order count of the loads issued after it, not a drain of the
+  // pipeline.
   auto block = [&](int gl0) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      native_compute_group<G, A, 1, F, StreamLds<G>, kHalf ? 1 : 2>(sm, buf[d], gl0 + kW * d, t,
-                                                                    mask_lo, mask_hi, y, half);
+      native_compute_group<G, A, MT, F, StreamLds<G>, kHalf ? 1 : 2>(sm, buf[d], gl0 + kW * d, t,
+                                                                     mask_lo, mask_hi, y, half);
       load_slab(buf[d], slab(j + d + D));
       // Issue the refill here, not after the block's later slabs: the scheduler would otherwise
       // sink every load below the block's arithmetic and drain the pipeline once per block.
@@ -252,178 +372,194 @@ __global__ void __launch_bounds__(64 * (kW + (kTail ? 1 : 0)), 1)
     }
     j += D;
   };
-  // Folds the lane partials over the column's four quarters (lanes n, n+16, n+32, n+48) into LDS
-  // slot `slot` and meets the other waves; the loads of the next slabs stay in flight.
-  auto reduce_slice = [&](int slot) {
-    float y0 = y[0][0];
-    float y1 = y[0][1];
-    y0 += __shfl_xor(y0, 16);
-    y0 += __shfl_xor(y0, 32);
-    if constexpr (!kHalf) {
-      y1 += __shfl_xor(y1, 16);
-      y1 += __shfl_xor(y1, 32);
-    }
-    y[0][0] = 0.0f;
-    y[0][1] = 0.0f;
-    if (lane < 16) {
-      red[slot][wave][lane] = y0;
+  int n_red = 0;  // reductions so far: their LDS slot alternates
+  // Folds the lane partials over the column's four quarters (lanes n, n+16, n+32, n+48) into the
+  // next LDS slot and meets the other waves; the loads of the next slabs stay in flight. Slot
+  // reuse is safe: a slot is written again only after the next barrier, which the wave reading it
+  // (the rotating writer, or the control wave) reaches after reading.
+  auto reduce = [&]() -> int {
+    const int slot = n_red & 1;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      float y0 = y[m][0];
+      float y1 = y[m][1];
+      y0 += __shfl_xor(y0, 16);
+      y0 += __shfl_xor(y0, 32);
       if constexpr (!kHalf) {
-        red[slot][wave][lane + 16] = y1;
+        y1 += __shfl_xor(y1, 16);
+        y1 += __shfl_xor(y1, 32);
+      }
+      y[m][0] = 0.0f;
+      y[m][1] = 0.0f;
+      if (lane < 16) {
+        red[slot][wave][m * kSliceCols + lane] = y0;
+        if constexpr (!kHalf) {
+          red[slot][wave][m * kSliceCols + lane + 16] = y1;
+        }
       }
     }
     lds_barrier();
+    ++n_red;
+    return slot;
   };
-  if constexpr (kTail) {
-    // Stage the pass holding the piece's groups, stream the piece, hand its totals to the control
-    // wave. The regular passes later stage this one again, with the same values.
-    native_stage_unit<G, A, F>(sm, raw_tail, 0, g_tail, lane % WR);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    for (int blk = 0; blk < n_t / D; ++blk) {
-      block(gt0 + wave + kW * D * blk);
-    }
-    reduce_slice(0);
-  }
-  stage_one();
-  for (int r = 0; r < whole; ++r) {
-    // Blocks that each stage one more pass, then blocks that do not: two loops, no branch in
-    // either.
-    const int n_staging = min(n_blk, n_pass - staged);
-    int blk = 0;
-    for (; blk < n_staging; ++blk) {
-      block(wave + kW * D * blk);
-      stage_one();
-    }
-    for (; blk < n_blk; ++blk) {
-      block(wave + kW * D * blk);
-    }
-    while (staged < n_pass) {
-      stage_one();
-    }
 
-    // Slot reuse is safe: a slot is written again only after the next slice's barrier, which the
-    // wave reading it (below, or the control wave for the tail piece) reaches after reading.
-    const int slot = (r + (kTail ? 1 : 0)) & 1;
-    reduce_slice(slot);
+  if constexpr (kPieces) {
+    for (int blk = 0; blk < rg.head_len; ++blk) {
+      block((rg.head_blk0 + blk) * Q + wave);
+    }
+    if (rg.head_len > 0) {
+      reduce();
+    }
+    for (int blk = 0; blk < rg.tail_len; ++blk) {
+      block(blk * Q + wave);
+    }
+    if (rg.tail_len > 0) {
+      reduce();
+    }
+  }
+  for (int r = 0; r < rg.whole; ++r) {
+    // Without pieces: blocks that each stage one more pass, then blocks that do not: two loops,
+    // no branch in either.
+    int blk = 0;
+    if constexpr (!kPieces) {
+      const int n_staging = min(nbs, n_pass - staged);
+      for (; blk < n_staging; ++blk) {
+        block(blk * Q + wave);
+        stage_one();
+      }
+    }
+    for (; blk < nbs; ++blk) {
+      block(blk * Q + wave);
+    }
+    if constexpr (!kPieces) {
+      while (staged < n_pass) {
+        stage_one();
+      }
+    }
+    const int slot = reduce();
     // One wave, rotating with the slice, writes it.
     constexpr int kCols = kHalf ? kSliceCols / 2 : kSliceCols;
-    if (wave == (r & (kW - 1)) && lane < kCols) {
-      float v = red[slot][0][lane];
+    const size_t slice = static_cast<size_t>(rg.whole_slice0) + r;
+    if (wave == (r & (kW - 1))) {
 #pragma unroll
-      for (int w = 1; w < kW; ++w) {
-        v += red[slot][w][lane];
+      for (int i = 0; i < (MT * kCols + 63) / 64; ++i) {
+        const int o = lane + 64 * i;
+        const int m = o / kCols;
+        const int c = o % kCols;
+        if (o < MT * kCols && m < p.M) {
+          float v = red[slot][0][m * kSliceCols + c];
+#pragma unroll
+          for (int w = 1; w < kW; ++w) {
+            v += red[slot][w][m * kSliceCols + c];
+          }
+          p.out[static_cast<size_t>(m) * p.N + slice * kSliceCols + 16 * half + c] =
+              float_to_act_bits<A>(v);
+        }
       }
-      const size_t col = kHalf ? static_cast<size_t>(b >> 1) * kSliceCols + 16 * half + lane
-                               : (static_cast<size_t>(b) * whole + r) * kSliceCols + lane;
-      p.out[col] = float_to_act_bits<A>(v);
     }
   }
   // Retire the loads of re-read tail slots before the workgroup ends.
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
 }
 
-template <int G, Act A, PacketFormat F, int kStageSlots, int kW, int D>
+template <int G, Act A, PacketFormat F, int kStageSlots, int kW, int D, int MT>
 hipError_t launch_stream_t(const GemvLaunch& l, hipStream_t stream) {
   int grid = 0;
-  GemvParams p = native_params<G, 1>(l, &grid);
+  GemvParams p = native_params<G, MT>(l, &grid);
   p.pair = 0;
-  p.stream_whole = l.stream_whole;
-  p.stream_tail = l.stream_tail;
-  p.stream_parts = l.stream_parts;
   grid = l.stream_grid;
+  p.stream_whole = l.stream_whole;
   p.xcd_remap = grid % 8 == 0 ? 1 : 0;
-  const size_t lds = stream_lds_bytes(G, l.K / G + 1);
-  if (l.stream_tail > 0) {
-    hipLaunchKernelGGL((w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, true, false>),
+  const size_t lds = static_cast<size_t>(MT) * stream_lds_bytes(G, l.K / G + 1);
+  if (l.stream_pieces) {
+    hipLaunchKernelGGL((w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, MT, true, false>),
                        dim3(grid), dim3(64 * (kW + 1)), lds, stream, p);
   } else if (l.stream_half) {
-    if constexpr (G == 128) {
-      hipLaunchKernelGGL((w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, false, true>),
+    if constexpr (G == 128 && MT == 1) {
+      hipLaunchKernelGGL((w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, 1, false, true>),
                          dim3(grid), dim3(64 * kW), lds, stream, p);
     } else {
       return hipErrorInvalidValue;
     }
   } else {
-    hipLaunchKernelGGL((w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, false, false>),
+    hipLaunchKernelGGL((w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, MT, false, false>),
                        dim3(grid), dim3(64 * kW), lds, stream, p);
   }
   return hipGetLastError();
 }
 
-template <int G, Act A, PacketFormat F, int kW, int D>
+template <int G, Act A, PacketFormat F, int kW, int D, int MT>
 hipError_t stream_dispatch_slots(const GemvLaunch& l, hipStream_t stream) {
   constexpr int kPerPass = 64 * kW * 8;  // activations staged per slot
   if (l.K <= kPerPass * (16 / kW)) {
-    return launch_stream_t<G, A, F, 16 / kW, kW, D>(l, stream);
+    return launch_stream_t<G, A, F, 16 / kW, kW, D, MT>(l, stream);
   }
   if (l.K <= kPerPass * (64 / kW)) {
-    return launch_stream_t<G, A, F, 64 / kW, kW, D>(l, stream);
+    return launch_stream_t<G, A, F, 64 / kW, kW, D, MT>(l, stream);
   }
   return hipErrorInvalidValue;
 }
 
-// Waves and depth: units_per_workgroup and K / G are multiples of stream_waves * stream_depth
-// (the host plans them so).
 template <int G, Act A, PacketFormat F>
-hipError_t stream_dispatch_waves(const GemvLaunch& l, hipStream_t stream) {
-  constexpr int kUnitKB = G == 128 ? 2 : 1;
-  if (l.stream_waves != kStreamWaves) {
+hipError_t stream_dispatch_rows(const GemvLaunch& l, hipStream_t stream) {
+  constexpr int D = stream_depth_for_kb(G, kStreamKB);
+  if (l.stream_waves != kStreamWaves || l.stream_depth != D) {
     return hipErrorInvalidValue;
   }
-  switch (l.stream_depth * kUnitKB) {
-    case 4: return stream_dispatch_slots<G, A, F, kStreamWaves, 4 / kUnitKB>(l, stream);
-    case 8: return stream_dispatch_slots<G, A, F, kStreamWaves, 8 / kUnitKB>(l, stream);
-    default: return hipErrorInvalidValue;
+  // MT > 1 (several rows per slab) builds, but measured slower than the per-slice runs on MI355X
+  // (benchmark configuration 3, 14336 x 4096, G = 64: two rows 9.7 -> 10.5 us, four rows 12.9 ->
+  // 13.7 us; the dot2 arithmetic of four rows per slab at two waves per SIMD does not keep up),
+  // so only one row is dispatched.
+  if (l.M != 1) {
+    return hipErrorInvalidValue;
   }
+  return stream_dispatch_slots<G, A, F, kStreamWaves, D, 1>(l, stream);
 }
 
 template <PacketFormat F>
 hipError_t stream_dispatch(const GemvLaunch& l, hipStream_t stream) {
   if (l.group_size == 64) {
-    return l.act == Act::kF16 ? stream_dispatch_waves<64, Act::kF16, F>(l, stream)
-                              : stream_dispatch_waves<64, Act::kBF16, F>(l, stream);
+    return l.act == Act::kF16 ? stream_dispatch_rows<64, Act::kF16, F>(l, stream)
+                              : stream_dispatch_rows<64, Act::kBF16, F>(l, stream);
   }
-  return l.act == Act::kF16 ? stream_dispatch_waves<128, Act::kF16, F>(l, stream)
-                            : stream_dispatch_waves<128, Act::kBF16, F>(l, stream);
+  return l.act == Act::kF16 ? stream_dispatch_rows<128, Act::kF16, F>(l, stream)
+                            : stream_dispatch_rows<128, Act::kBF16, F>(l, stream);
 }
 
 }  // namespace
 
 hipError_t launch_w4a16_gemv_stream(const GemvLaunch& l, hipStream_t stream) {
-  if (l.mode != GemvMode::kStreamK || l.m_tile != 1 || l.M != 1 || l.fuse != GemvFuse::kNone ||
+  if (l.mode != GemvMode::kStreamK || l.m_tile != l.M || l.fuse != GemvFuse::kNone ||
       l.slice_cols != kSliceCols || l.slice_pair || l.K > kStreamMaxK || l.stream_depth <= 0 ||
       l.stream_grid <= 0) {
     return hipErrorInvalidValue;
   }
-  // Whole slices, the same count per workgroup, in blocks of waves * depth units; with a tail,
-  // one piece per workgroup of the slices left over, lying inside one staging pass of the wave's
-  // groups (64 / (G / 8) of them), with the workspace to finish them.
+  // Blocks of waves * depth groups. Half slices: G = 128, one row, two workgroups per slice.
+  // Pieces: the workspace to finish the split slices. Else whole slices, the same count per
+  // workgroup.
   const int ng = l.K / l.group_size;
   const int quantum = l.stream_waves * l.stream_depth;
-  if (l.stream_whole < 0 || ng % quantum != 0) {
+  if (ng % quantum != 0) {
     return hipErrorInvalidValue;
   }
   const long long slices = l.N / kSliceCols;
-  const long long whole_slices = static_cast<long long>(l.stream_whole) * l.stream_grid;
   if (l.stream_half) {
-    // one half-slice (16 columns of a G = 128 slice) per workgroup
-    if (l.group_size != 128 || l.stream_tail != 0 || l.stream_whole != 1 ||
-        l.stream_grid != 2 * slices) {
+    if (l.group_size != 128 || l.M != 1 || l.stream_pieces || l.stream_grid != 2 * slices) {
       return hipErrorInvalidValue;
     }
-  } else if (l.stream_tail == 0) {
-    if (l.stream_whole == 0 || whole_slices != slices) {
+  } else if (l.stream_pieces) {
+    // left-over slices fewer than the workgroups (so a range is shorter than a slice), and at
+    // least one left-over block per workgroup
+    const long long left = slices - static_cast<long long>(l.stream_grid) * l.stream_whole;
+    if (l.counters == nullptr || l.partials == nullptr || slices > kStreamMaxSlices ||
+        l.stream_whole < 0 || left <= 0 || left >= l.stream_grid ||
+        left * (ng / quantum) < l.stream_grid ||
+        left * (ng / quantum) * l.stream_grid >= (1LL << 31)) {
       return hipErrorInvalidValue;
     }
-  } else {
-    const int pass_groups = l.stream_waves * (64 / (l.group_size / 8));
-    if (l.stream_parts <= 0 || l.stream_grid % l.stream_parts != 0 ||
-        l.stream_tail * l.stream_parts != ng || l.stream_tail % quantum != 0 ||
-        pass_groups % l.stream_tail != 0 ||
-        whole_slices + l.stream_grid / l.stream_parts != slices || l.counters == nullptr ||
-        l.partials == nullptr) {
-      return hipErrorInvalidValue;
-    }
+  } else if (l.stream_whole <= 0 ||
+             static_cast<long long>(l.stream_whole) * l.stream_grid != slices) {
+    return hipErrorInvalidValue;
   }
   switch (l.format) {
     case PacketFormat::kNativeSym: return stream_dispatch<PacketFormat::kNativeSym>(l, stream);

@@ -84,8 +84,7 @@ struct ArcW4A16Plan {
   int schedule;                 // kSchedule*: how the workgroups walk their units
   int stream_depth;             // kScheduleStream: slabs in flight per wave
   int stream_whole;             // kScheduleStream: whole slices per workgroup
-  int stream_tail;              // kScheduleStream: groups of each workgroup's tail piece (0: none)
-  int stream_parts;             // kScheduleStream: workgroups sharing one tail slice
+  int stream_pieces;            // kScheduleStream: left-over slices dealt as pieces
   int stream_half;              // kScheduleStream: one half-slice (16 columns) per workgroup
 };
 

@@ -286,15 +286,17 @@ bool stream_schedule_enabled() {
   return enabled;
 }
 
-// FK_W4A16_STREAM_TAIL=0 keeps shapes whose slices do not divide over the CUs off the stream
-// schedule (they then run per-slice runs).
-bool stream_tail_enabled() {
-  static const bool enabled = [] {
-    const char* v = std::getenv("FK_W4A16_STREAM_TAIL");
-    return v == nullptr || std::string(v) != "0";
-  }();
+// FK_W4A16_STREAM_PIECES=0 keeps shapes whose slices do not divide over the CUs off the stream
+// schedule.
+bool env_enabled(const char* name) {
+  const char* v = std::getenv(name);
+  return v == nullptr || std::string(v) != "0";
+}
+bool stream_pieces_enabled() {
+  static const bool enabled = env_enabled("FK_W4A16_STREAM_PIECES");
   return enabled;
 }
+
 
 // FK_W4A16_STREAM_HALF=0 keeps shapes with at most half as many slices as CUs off half-slices.
 bool stream_half_enabled() {
@@ -312,16 +314,6 @@ bool stream_small_enabled() {
     return v == nullptr || std::string(v) != "0";
   }();
   return enabled;
-}
-
-// FK_W4A16_STREAM_KB=4|8 pins the weights in flight per wave (else the plan's choice).
-int stream_kb_override() {
-  static const int kb = [] {
-    const char* v = std::getenv("FK_W4A16_STREAM_KB");
-    const int n = v == nullptr ? 0 : std::atoi(v);
-    return n == 4 || n == 8 ? n : 0;
-  }();
-  return kb;
 }
 
 int stream_workgroups_per_cu() {
@@ -380,82 +372,75 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
   // 7B gate_up (688 slices, 344 pairs) got 1 us slower, pairs that leave part of the chip idle
   // (70B o, 256 slices) 3 us slower, and with longer K, whose single-slice runs already stream
   // 135 KB, pairs gain nothing (70B qkv, K = 8192: 12.12 -> 12.20 us).
-  // The stream schedule (w4a16_gemv_stream.hip): one activation row, K staged whole in LDS, and
-  // the slices dividing evenly over one workgroup per CU, each workgroup streaming its share of
-  // whole slices as one contiguous range. The weights in flight per wave: 4 KB (32 KB per CU), or
-  // what FK_W4A16_STREAM_KB pins. Measured on MI355X (bench, Llama-70B bf16): o 8.07 -> 7.73 us,
-  // down 22.6 -> 21.3, gate_up 39.6 -> 39.8 (equal within the run-to-run spread); 8 and 16 KB
-  // per wave are slower (gate_up 39.9 and 41.5 us). Shapes whose slices do not divide evenly
-  // stay on the per-slice runs: cutting the remainder slices into K pieces finished by a
-  // cross-workgroup hand-off measured slower everywhere (8B down 8.7 -> 20.7 us, 7B o 4.6 -> 6.0).
+  // The stream schedule (w4a16_gemv_stream.hip): one activation row staged whole in LDS, one
+  // workgroup per CU streaming its share of whole slices as one contiguous range, with
+  // 4 KB of weights in flight per wave. Measured on MI355X (bench, Llama-70B bf16): o 8.07 ->
+  // 7.73 us, down 22.6 -> 21.3, gate_up 39.6 -> 39.8 (equal within the run-to-run spread); 8 and
+  // 16 KB per wave are slower (gate_up 39.9 and 41.5 us). Slices that do not divide evenly:
+  //  * more slices than CUs and long K: the left-over slices are dealt as equal block ranges
+  //    (pieces) on top of the whole slices, and handed off while the whole slices stream;
+  //  * at most half as many slices as CUs (G = 128, one row): a half-slice (16 columns, the first
+  //    or second KB of every slab) per workgroup, so every CU streams and no slice is split over
+  //    K (8B o 4.0 -> 3.9 us, 8B down 8.8 -> 8.0);
+  //  * otherwise fewer slices than CUs and K too short to split (per == K/G): one whole slice per
+  //    workgroup (8B qkv 5.16 -> 4.44 us, 7B o 4.67 -> 4.15). Pieces with no whole slice to hide
+  //    their hand-off behind cost more than they save (8B o 4.8 -> 5.7 us), and 8B down as whole
+  //    slices on 128 workgroups is slower than its runs split over K (8.8 -> 10.0 us).
+  // Pieces only for long K: measured on MI355X (bench, alternating runs on one GPU), 70B qkv
+  // (K/G = 64) 11.9 -> 10.6 us, but 8B gate_up (K/G = 32) 12.6 -> 13.2 us against slice pairs and
+  // 7B gate_up 10.5 -> 11.9 us against per-slice runs.
+  constexpr int kMinPieceGroups = 64;
   if (plain && split_k_slices == 0 && batch == 1 && plan.m_tile == 1 &&
       k <= fk::kStreamMaxK && stream_schedule_enabled()) {
     const std::size_t lds =
         fk::stream_lds_bytes(group_size, num_groups + 1) + fk::kStreamStaticLdsBytes;
     const std::size_t lds_limit = cu_count_given ? kGfx950LdsBytes : device_lds_per_block();
-    const int kb = stream_kb_override() != 0 ? stream_kb_override() : 4;
-    const int depth = fk::stream_depth_for_kb(group_size, kb);
-    const int quantum = fk::kStreamWaves * depth;
-    long long grid = static_cast<long long>(cu_count) * stream_workgroups_per_cu();
-    // Fewer slices than CUs and K too short to split (per == K/G): one whole slice per
-    // workgroup, streamed by eight waves with the row staged once. Measured on MI355X (bench):
-    // 8B qkv (192 slices) 5.16 -> 4.44 us, o (128) 4.79 -> 4.02, 7B o 4.67 -> 4.15; 8B down
-    // (128 slices of 112 groups), whose runs split K over 256 workgroups, gets slower (8.8 ->
-    // 10.0), so it keeps its runs.
-    if (slices < grid && per == num_groups && stream_small_enabled()) {
-      grid = slices;
-    }
-    // At most half as many slices as CUs (G = 128): one half-slice (16 columns, the first or
-    // second 1 KB of every slab) per workgroup, so every CU streams and no slice is split over
-    // K. Measured on MI355X (bench): 8B o (128 slices) 4.0 -> ? us, down (128 x 112 groups)
-    // 8.8 -> ? us.
-    const bool half = group_size == 128 && 2 * slices <= static_cast<long long>(cu_count) *
-                                                            stream_workgroups_per_cu() &&
-                      stream_half_enabled();
-    if (half) {
-      grid = 2 * slices;
-    }
-    // Slices left over past whole ones per workgroup are cut into one piece per workgroup when
-    // they divide the grid, the pieces are whole blocks of the waves and lie inside one staging
-    // pass of a wave's groups (w4a16_gemv_stream.hip), and every workgroup also has a whole
-    // slice to stream while its piece is handed off. Measured on MI355X (bench): 70B qkv
-    // 11.6 -> 9.8 us, 8B gate_up 14.2 -> 12.7 (pairs before), 7B qkv 7.4 -> 7.1; with no whole
-    // slice (8B o: half a slice per CU) the hand-off is the workgroup's last step and costs more
-    // than it saves (4.8 -> 5.7 us), so such shapes stay on the per-slice runs.
-    const long long rem = slices % grid;
-    const long long parts = rem == 0 ? 0 : grid / rem;
-    const int pass_groups = fk::kStreamWaves * (64 / (group_size / 8));
-    const bool tail_ok = rem != 0 && slices > grid && stream_tail_enabled() && grid % rem == 0 &&
-                         num_groups % parts == 0 && (num_groups / parts) % quantum == 0 &&
-                         pass_groups % (num_groups / parts) == 0;
-    if (half && num_groups % quantum == 0 && lds <= lds_limit) {
-      plan.schedule = kScheduleStream;
-      plan.slice_cols = fk::kSliceCols / 2;
-      plan.workgroups = static_cast<int>(grid);
-      plan.stream_depth = depth;
-      plan.stream_whole = 1;
-      plan.stream_half = 1;
-      plan.groups_per_workgroup = num_groups;
-      plan.max_tile_contributors = 1;
-      plan.workspace_bytes = 0;
-      return plan;
-    }
-    if (!half && num_groups % quantum == 0 && lds <= lds_limit &&
-        ((slices >= grid && rem == 0) || tail_ok)) {
-      plan.schedule = kScheduleStream;
-      plan.slice_cols = fk::kSliceCols;
-      plan.workgroups = static_cast<int>(grid);
-      plan.stream_depth = depth;
-      plan.stream_whole = static_cast<int>(slices / grid);
-      plan.stream_tail = rem == 0 ? 0 : static_cast<int>(num_groups / parts);
-      plan.stream_parts = rem == 0 ? 0 : static_cast<int>(parts);
-      plan.groups_per_workgroup = plan.stream_whole * num_groups + plan.stream_tail;
-      plan.max_tile_contributors = rem == 0 ? 1 : static_cast<int>(parts);
-      plan.workspace_bytes =
-          rem == 0 ? 0
-                   : kCounterRegionBytes + static_cast<std::size_t>(grid) * fk::kSliceCols *
-                                               sizeof(float);
-      return plan;
+    const int depth = fk::stream_depth_for_kb(group_size, fk::kStreamKB);
+    const int nbs = num_groups / (fk::kStreamWaves * depth);  // blocks per slice
+    const long long cus = static_cast<long long>(cu_count) * stream_workgroups_per_cu();
+    if (num_groups % (fk::kStreamWaves * depth) == 0 && lds <= lds_limit) {
+      long long grid = 0;
+      int whole = 0;
+      bool pieces = false;
+      bool half = false;
+      const long long left = slices % cus;
+      if (slices >= cus && left == 0) {
+        grid = cus;
+        whole = static_cast<int>(slices / cus);
+      } else if (slices > cus && left * nbs >= cus && num_groups >= kMinPieceGroups &&
+                 slices <= fk::kStreamMaxSlices && stream_pieces_enabled()) {
+        grid = cus;
+        whole = static_cast<int>(slices / cus);
+        pieces = true;
+      } else if (batch == 1 && group_size == 128 && 2 * slices <= cus && stream_half_enabled()) {
+        grid = 2 * slices;
+        whole = 1;
+        half = true;
+      } else if (slices < cus && per == num_groups && stream_small_enabled()) {
+        grid = slices;
+        whole = 1;
+      }
+      if (grid > 0) {
+        plan.schedule = kScheduleStream;
+        plan.slice_cols = half ? fk::kSliceCols / 2 : fk::kSliceCols;
+        plan.workgroups = static_cast<int>(grid);
+        plan.stream_depth = depth;
+        plan.stream_whole = whole;
+        plan.stream_pieces = pieces ? 1 : 0;
+        plan.stream_half = half ? 1 : 0;
+        // groups a workgroup streams (the most, with pieces)
+        const long long left_blocks = (slices - grid * whole) * nbs;
+        const long long piece_blocks = pieces ? (left_blocks + grid - 1) / grid : 0;
+        plan.groups_per_workgroup = static_cast<int>(
+            whole * num_groups + piece_blocks * fk::kStreamWaves * depth);
+        plan.max_tile_contributors =
+            pieces ? static_cast<int>((nbs * grid + left_blocks - 1) / left_blocks + 1) : 1;
+        plan.workspace_bytes =
+            pieces ? kCounterRegionBytes +
+                         fk::stream_partial_floats(static_cast<int>(grid), 1) * sizeof(float)
+                   : 0;
+        return plan;
+      }
     }
   }
   if (plain && split_k_slices == 0 && per == num_groups && plan.m_tile == 1 &&
@@ -562,19 +547,18 @@ void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::u
     l.units_per_workgroup = 2 * plan.groups_per_workgroup;
   } else if (plan.schedule == kScheduleStream) {
     const int cols = plan.stream_half ? fk::kSliceCols / 2 : fk::kSliceCols;
-    if (format == fk::PacketFormat::kArc || batch != 1 || plan.slice_cols != cols ||
+    if (format == fk::PacketFormat::kArc || plan.m_tile != batch || plan.slice_cols != cols ||
         fuse != fk::GemvFuse::kNone) {
       throw std::logic_error("stream schedule on a plan that is not one unfused native row");
     }
     l.stream = true;
     l.slice_cols = fk::kSliceCols;
-    l.stream_half = plan.stream_half != 0;
     l.stream_waves = fk::kStreamWaves;
     l.stream_depth = plan.stream_depth;
     l.stream_grid = plan.workgroups;
     l.stream_whole = plan.stream_whole;
-    l.stream_tail = plan.stream_tail;
-    l.stream_parts = plan.stream_parts;
+    l.stream_pieces = plan.stream_pieces != 0;
+    l.stream_half = plan.stream_half != 0;
   }
   l.format = format;
   l.fuse = fuse;

@@ -216,10 +216,11 @@ def test_native_format_validation_without_gpu(lib: ctypes.CDLL) -> None:
         ((1, 8192, 8192, 128), (32, 64, 256, 2)),      # 256 slices: one per CU, streamed
         ((1, 10240, 8192, 128), (32, 80, 256, 2)),     # 70B qkv: 1 slice + a quarter slice per CU
         ((1, 10240, 4096, 128), (64, 32, 160, 1)),     # 320 slices in 160 pairs
-        ((1, 12288, 4096, 128), (32, 48, 256, 2)),     # 7B qkv: 1 slice + a half slice per CU
-        ((1, 28672, 4096, 128), (32, 112, 256, 2)),    # 8B gate_up: 3 slices + a half per CU
+        ((1, 12288, 4096, 128), (64, 32, 192, 1)),     # 7B qkv: 384 slices in 192 pairs (K short for pieces)
+        ((1, 28672, 4096, 128), (64, 32, 448, 1)),     # 8B gate_up: 896 slices in 448 pairs
+        ((1, 12288, 8192, 128), (32, 96, 256, 2)),     # 1 slice + pieces of the 128 left over
         ((1, 22016, 4096, 128), (32, 32, 688, 0)),     # 7B gate_up: 344 pairs would fill 2 rounds unevenly
-        ((2, 12288, 4096, 128), (32, 32, 384, 0)),     # pairs for one row only
+        ((2, 12288, 4096, 128), (32, 32, 384, 0)),     # pairs and stream for one row only
         ((1, 57344, 8192, 128), (32, 448, 256, 2)),    # 70B gate_up: 7 whole slices per CU
         ((1, 8192, 28672, 128), (32, 224, 256, 2)),    # 70B down: one slice of 224 groups per CU
         ((1, 8192, 28672 + 128, 128), (32, 113, 510, 0)),  # 225 groups: not a multiple of 16
@@ -239,8 +240,9 @@ def test_native_plan_policy_without_gpu(lib: ctypes.CDLL, shape, want) -> None:
     rc, ref = _plan(lib, batch, n, k, g)
     assert rc == 0 and (arc.slice_cols, arc.workgroups) == (ref.slice_cols, ref.workgroups)
     assert arc.schedule == 0
-    # a fix-up needs a workspace exactly when runs do not cover whole slices
-    assert (p.workspace_bytes > 0) == (p.groups_per_workgroup % (k // g) != 0)
+    # a fix-up needs a workspace exactly when slices are shared (runs that do not cover whole
+    # slices, or stream pieces)
+    assert (p.workspace_bytes > 0) == (p.max_tile_contributors > 1)
 
 
 def test_fused_entry_points_validate_without_gpu(lib: ctypes.CDLL) -> None:

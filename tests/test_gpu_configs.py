@@ -169,41 +169,87 @@ def test_config4_llama8b_decode_step_graph() -> None:
             np.testing.assert_array_equal(got, eager[(layer, name)])
 
 
+def test_config2_layer_graph_replays_match_eager() -> None:
+    """The 70B layer (its qkv takes pieces with a counter hand-off, the other three whole slices)
+    captured in one HIP graph: four replays, with eager work and synchronisations between them,
+    each bit-identical to the eager call (the counters the pieces leave behind are zero)."""
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the plans are chosen for 256 CUs")
+    dev = torch.device(DEV)
+    slabs, xs, outs = {}, {}, {}
+    for name, n, k in LLAMA70B:
+        q, alpha, beta = layer_weights(torch, dev, n, k, 128, 7)
+        arc = pack_arc_w4a16_packets(q, alpha, beta, group_size=128)
+        slabs[name] = convert_arc_to_native_packets(arc, n=n, k=k, group_size=128)
+        del arc, q, alpha, beta
+        xs[name] = torch.randn((1, k), device=dev).to(torch.bfloat16)
+        outs[name] = torch.empty((1, n), device=dev, dtype=torch.bfloat16)
+    plan = arc_w4a16_plan(batch=1, n=10240, k=8192, group_size=128,
+                          activation_dtype=torch.bfloat16, packet_format=1)
+    assert plan["schedule"] == 2 and plan["workspace_bytes"] > 0, plan
+
+    def layer() -> None:
+        for name, n, k in LLAMA70B:
+            arc_w4a16_forward_native(xs[name], slabs[name], n=n, k=k, group_size=128,
+                                     packet_format="native_sym", output=outs[name])
+
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        layer()
+    torch.cuda.synchronize()
+    eager = {name: _bits(o) for name, o in outs.items()}
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        layer()
+    for replay in range(4):
+        for o in outs.values():
+            o.fill_(float("nan"))
+        scratch = torch.randn(1 << 20, device=dev).sum()  # eager work between the replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        del scratch
+        for name, o in outs.items():
+            np.testing.assert_array_equal(_bits(o), eager[name], err_msg=f"replay {replay} {name}")
+
+
 @pytest.mark.parametrize(
-    "n,k,g,act,asym",
+    "n,k,g,act,asym,m",
     [
-        (8192, 2048, 128, "f16", False),    # 16 groups: one block of 8 waves x 2 slabs per slice
-        (8192, 4096, 64, "f16", True),      # G = 64: 4 slabs in flight per wave, two blocks
-        (16384, 8192, 128, "bf16", True),   # two whole slices per workgroup, asymmetric
-        (8192, 32768, 128, "bf16", False),  # the longest K the stream schedule stages
-        (8192, 32768, 64, "f16", False),    # 512 groups at G = 64
-        # tail pieces (slices left over past whole ones per CU), finished through the workspace
-        (10240, 8192, 128, "bf16", False),  # 1 slice + a quarter of one per CU
-        (12288, 4096, 128, "bf16", True),   # 1 slice + a half
-        (28672, 4096, 128, "f16", False),   # 3 slices + a half
-        (12288, 4096, 64, "bf16", False),   # G = 64: halves of 64 groups
-        (10240, 16384, 64, "f16", True),    # G = 64: quarters of 256 groups
+        (8192, 2048, 128, "f16", False, 1),  # 16 groups: one block of 8 waves x 2 slabs per slice
+        (8192, 4096, 64, "f16", True, 1),      # G = 64: 4 slabs in flight per wave, two blocks
+        (16384, 8192, 128, "bf16", True, 1),   # two whole slices per workgroup, asymmetric
+        (8192, 32768, 128, "bf16", False, 1),  # the longest K the stream schedule stages
+        (8192, 32768, 64, "f16", False, 1),    # 512 groups at G = 64
+        # pieces of the slices left over past whole ones per CU, finished through the workspace
+        (10240, 8192, 128, "bf16", False, 1),  # 1 slice + a quarter of one per CU
+        (12288, 8192, 128, "f16", True, 1),    # 1 slice + a head and a tail piece (1.5 blocks)
+        (28672, 8192, 128, "bf16", False, 1),  # 3 slices + a half
+        (12288, 4096, 64, "bf16", False, 1),   # G = 64: halves of 64 groups
+        (10240, 16384, 64, "f16", True, 1),    # G = 64: quarters of 256 groups
+        (22016, 8192, 128, "f16", True, 1),    # ranges of 1 or 2 blocks over 176 slices
         # half slices (G = 128, at most half as many slices as CUs)
-        (4096, 4096, 128, "bf16", False),   # 8B o
-        (4096, 14336, 128, "f16", True),    # 8B down, asymmetric
-        (1024, 2048, 128, "bf16", True),    # 64 workgroups
+        (4096, 4096, 128, "bf16", False, 1),   # 8B o
+        (4096, 14336, 128, "f16", True, 1),    # 8B down, asymmetric
+        (1024, 2048, 128, "bf16", True, 1),    # 64 workgroups
+        (6144, 4096, 128, "f16", False, 1),  # one slice per workgroup, 192 workgroups
     ],
 )
-def test_stream_schedule_variants(n: int, k: int, g: int, act: str, asym: bool) -> None:
-    """The stream schedule (whole slices per CU, and tail pieces of the slices left over) at both
-    group sizes, both activation dtypes, both native formats and the staging slot counts; plus
-    determinism."""
+def test_stream_schedule_variants(n: int, k: int, g: int, act: str, asym: bool, m: int) -> None:
+    """The stream schedule (whole slices per CU, pieces of the slices left over, half slices, one
+    slice per workgroup) at both group sizes, both activation dtypes, both native formats and the
+    staging slot counts; plus determinism."""
     if torch.cuda.get_device_properties(0).multi_processor_count != 256:
         pytest.skip("the shapes are chosen for 256 CUs")
-    case = make_case(1, n, k, g, act=act, asymmetric=asym, seed=n + k + g)
+    case = make_case(m, n, k, g, act=act, asymmetric=asym, seed=n + k + g + m)
     x, q, a, b = _upload(case)
     fmt = "native_asym" if asym else "native_sym"
     slabs = convert_arc_to_native_packets(pack_arc_w4a16_packets(q, a, b, group_size=g), n=n, k=k,
                                           group_size=g, packet_format=fmt)
-    plan = arc_w4a16_plan(batch=1, n=n, k=k, group_size=g,
+    plan = arc_w4a16_plan(batch=m, n=n, k=k, group_size=g,
                           activation_dtype=x.dtype, packet_format=2 if asym else 1)
     assert plan["schedule"] == 2, plan
-    # three calls: the tail hand-off leaves its counters at zero, and adds the parts in a fixed
+    # three calls: the pieces' hand-off leaves its counters at zero, and adds the parts in a fixed
     # order, so every call gives the same bits
     ys = [_bits(arc_w4a16_forward_native(x, slabs, n=n, k=k, group_size=g, packet_format=fmt))
           for _ in range(3)]
