@@ -31,6 +31,7 @@ LIB_SOURCES = [
     CSRC / "kernels" / "decode_quant_linear" / "w4a16_gemv_stream.hip",
     CSRC / "kernels" / "decode_quant_linear" / "w4a16_gemv_fused.hip",
     CSRC / "kernels" / "decode_quant_linear" / "w4a16_gemm_mfma.hip",
+    CSRC / "kernels" / "decode_quant_linear" / "w4a16_gemm_mfma_stream.hip",
     CSRC / "kernels" / "decode_quant_linear" / "w4a16_aux.hip",
     CSRC / "ops" / "decode_quant_linear" / "arc_w4a16_ops.cpp",
     CSRC / "ops" / "decode_quant_linear" / "w4a16_scratch.hip",

@@ -1,0 +1,473 @@
+// W4A16 small-batch GEMM (2-16 activation rows) over native slabs on the gfx950 matrix cores, on
+// the persistent stream schedule.
+//
+// The work split is the one-row stream kernel's (w4a16_stream_common.h): one workgroup per CU
+// streams its whole 32-column slices as one contiguous range, plus pieces of the slices left
+// over, handed off by a control wave. What changes is the arithmetic per slab:
+//
+//  * One v_mfma_f32_16x16x32_f16 multiplies A = 16 activation rows x 32 k by B = 32 k x 16
+//    columns. A slab gives lane l = 16 t + n the U = G/32 code words of quarter t of columns n
+//    and n + 16; MFMA window j takes word j of every lane (k-chunks {j, U + j, 2U + j, 3U + j}
+//    of the group), so a slab is 2 U MFMAs: two 16-column halves times U windows, the halves
+//    sharing each window's A operand. B is the unpacked words, 1024 + q (even k) and 64 + q (odd
+//    k) in the slot order (0,4)(1,5)(2,6)(3,7); A is the activations paired in that order.
+//  * The activation rows are staged once per workgroup in LDS (MT rows of K, MT = 4, 8 or 16;
+//    rows past the batch are zeros), each wave staging the groups it computes (g = w mod 8), so no
+//    barrier separates staging from streaming. All of a wave's staging loads are issued before
+//    its first weight loads, and converted while those are in flight. The A operand of a window
+//    is one ds_read_b128 per lane for all 16 rows, whatever the batch: the LDS traffic per slab is
+//    U KB per wave (the dot2 kernel reads the activations once per row).
+//  * Every MFMA chain starts from the group's seed, C = -1024 S_e - 64 S_o (kNativeSym: minus
+//    8 (S_e + S_o) more, folding beta = -8 alpha), which cancels the unpack bias; the epilogue is
+//    y += alpha D (+ beta S for kNativeAsym), with the bf16 staging scale where it applies. The
+//    16 x 16 D tile gives lane l rows 4 t .. 4 t + 3 of column n of its half.
+//  * At the end of a slice or piece each wave writes its partial tile (rows < M) to LDS and meets
+//    the others; one wave (rotating with the slice, or the control wave for pieces) adds the
+//    eight partials in wave order and writes the slice, and a second barrier frees the one LDS
+//    slot (the activations of 16 rows leave no room for a second).
+#include "w4a16_gemv_native.h"
+#include "w4a16_stream_common.h"
+
+namespace fk {
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+// LDS of the MFMA stream kernel: xs [NG][G/8][MT] paired activation words (row fastest),
+// sums [NG][MT] {-1024 S_e - 64 S_o, S_e + S_o}, scale [NG][MT] bf16 staging scales, then the
+// reduction slot red [kW][MT][32].
+template <int G, int MT>
+struct MfmaStreamLds {
+  uint4* xs;
+  float2* sums;
+  float* scale;
+  float* red;
+};
+
+template <int G, int MT>
+__host__ __device__ constexpr size_t mfma_stream_lds_bytes(int ng, int waves) {
+  return static_cast<size_t>(ng) * MT * ((G / 8) * 16 + 8 + 4) +
+         static_cast<size_t>(waves) * MT * kSliceCols * 4;
+}
+
+// Code word -> 8 fp16 values in the slot order (k0,k4)(k1,k5)(k2,k6)(k3,k7): 1024 + q for even
+// k, 64 + q for odd k. One shift, four and-or.
+__device__ __forceinline__ half8_t unpack_word8(uint32_t w, uint32_t mask_lo, uint32_t mask_hi) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const uint32_t w8 = w >> 8;
+  u32x4 v;
+  v.x = (w & mask_lo) | kBiasLow;
+  v.y = (w & mask_hi) | kBiasHigh;
+  v.z = (w8 & mask_lo) | kBiasLow;
+  v.w = (w8 & mask_hi) | kBiasHigh;
+  return __builtin_bit_cast(half8_t, v);
+}
+
+// Word j of half i of the lane's unit (native_word_offset's layout).
+template <int G>
+__device__ __forceinline__ uint32_t slab_word(const NativeLoad<G>& ld, int i, int j) {
+  if constexpr (G == 128) {
+    const uint4 v = ld.w[i];
+    return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
+  } else {
+    const uint4 v = ld.w[0];
+    return i == 0 ? (j == 0 ? v.x : v.y) : (j == 0 ? v.z : v.w);
+  }
+}
+
+// Most staging loads per lane (a wave's groups x MT rows x G/8 word rows / 64 lanes): MT. The
+// host keeps launches within it.
+constexpr int max_stage_per_lane(int mt) { return mt; }
+
+template <int G, Act A, PacketFormat F, int kW, int D, int MT, bool kPieces>
+__global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
+    w4a16_gemm_mfma_stream_kernel(GemvParams p) {
+  extern __shared__ uint4 mfma_stream_lds[];
+  constexpr int WR = G / 8;
+  constexpr int U = native_unit_words(G);
+  constexpr int Q = kW * D;           // groups per block
+  constexpr int kOutMax = 16 * kSliceCols;
+  constexpr int kPer = MT * kSliceCols / 64;  // outputs per lane of a slice (MT rows)
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int t = lane / 16;
+  const int n = lane % 16;
+  const uint32_t mask_lo = vgpr_constant(0x000f000fu);
+  const uint32_t mask_hi = vgpr_constant(0x00f000f0u);
+  const size_t stride = static_cast<size_t>(format_packet_stride(G, F));
+  const int grid = static_cast<int>(gridDim.x);
+  int b = static_cast<int>(blockIdx.x);
+  if (p.xcd_remap) {
+    b = (b & 7) * (grid >> 3) + (b >> 3);
+  }
+  const int ng = p.NG;
+  const int nbs = ng / Q;
+  const int slices = p.N / kSliceCols;
+  const int rows = p.M;  // rows < MT are real, the rest zeros
+  const int n_out = rows * kSliceCols;
+  const StreamRange rg = stream_range(b, grid, p.stream_whole, slices, nbs, kPieces);
+
+  MfmaStreamLds<G, MT> sm;
+  sm.xs = mfma_stream_lds;
+  sm.sums = reinterpret_cast<float2*>(sm.xs + static_cast<size_t>(ng) * WR * MT);
+  sm.scale = reinterpret_cast<float*>(sm.sums + static_cast<size_t>(ng) * MT);
+  sm.red = sm.scale + static_cast<size_t>(ng) * MT;
+
+  // Adds the waves' partial tiles of output o in wave order.
+  auto total = [&](int o) {
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kW; ++w) {
+      s += sm.red[w * MT * kSliceCols + o];
+    }
+    return s;
+  };
+
+  if constexpr (kPieces) {
+    if (wave == kW) {
+      // Control wave: the pieces' totals first (two barriers each, the slot is then free), then
+      // their hand-offs, then the whole slices' barriers.
+      float v[2][kPer];
+      const bool has[2] = {rg.head_len > 0, rg.tail_len > 0};
+#pragma unroll
+      for (int pc = 0; pc < 2; ++pc) {
+        if (has[pc]) {
+          lds_barrier();
+#pragma unroll
+          for (int i = 0; i < kPer; ++i) {
+            const int o = lane + 64 * i;
+            v[pc][i] = o < n_out ? total(o) : 0.0f;
+          }
+          lds_barrier();
+        }
+      }
+      if (has[0]) {
+        stream_hand_off<A, kPer>(p, b, 0, rg.head_slice, grid, p.stream_whole, slices, nbs,
+                                 n_out, kOutMax, v[0], lane);
+      }
+      if (has[1]) {
+        stream_hand_off<A, kPer>(p, b, 1, rg.tail_slice, grid, p.stream_whole, slices, nbs,
+                                 n_out, kOutMax, v[1], lane);
+      }
+      for (int r = 0; r < rg.whole; ++r) {
+        lds_barrier();
+        lds_barrier();
+      }
+      return;
+    }
+  }
+
+  // The wave's slabs: the head piece's, the tail piece's, then the whole slices' range (as in the
+  // one-row stream kernel; re-reads past the last slab keep every load unconditional).
+  const int n_h = rg.head_len * D;
+  const int n_t = rg.tail_len * D;
+  const int n_w = n_h + n_t + rg.whole * nbs * D;
+  const int j_last = n_w - 1;
+  const int off_w = rg.whole_slice0 * ng + wave - (n_h + n_t) * kW;
+  const int off_t = rg.tail_slice * ng + wave - n_h * kW;
+  const int off_h = rg.head_slice * ng + rg.head_blk0 * Q + wave;
+  auto slab = [&](int i) -> const uint8_t* {
+    const int c = min(i, j_last);
+    int off = off_w;
+    if constexpr (kPieces) {
+      // 0/1 flags made opaque to the compiler (readfirstlane), which otherwise turns the choice
+      // into a lookup table in scratch memory
+      int in_t = c < n_h + n_t ? 1 : 0;
+      int in_h = c < n_h ? 1 : 0;
+      in_t = __builtin_amdgcn_readfirstlane(in_t);
+      in_h = __builtin_amdgcn_readfirstlane(in_h);
+      off += in_t * (off_t - off_w) + in_h * (off_h - off_t);
+    }
+    return p.packets + static_cast<size_t>(static_cast<uint32_t>(c * kW + off)) * stride;
+  };
+
+  // Staging: the wave's (group, row, word row) units, 64 a pass, groups g = wave + kW gi; a
+  // group's MT * WR units are P consecutive lanes' worth (row and word row fastest), so a group's
+  // WR word rows of one row are WR consecutive lanes (the per-(group, row) sums are xor-shuffles).
+  // With P >= 64 a pass lies inside one group and its group and first row are compile-time
+  // constants of the (unrolled) pass; with P = 32 a pass holds two groups, one per half-wave.
+  // Either way a unit's address is a lane constant plus a uniform offset (the general division
+  // form put some 600 instructions ahead of the first weight load).
+  constexpr int P = MT * WR;
+  constexpr int L = P < 64 ? P : 64;  // lanes per group in a pass
+  constexpr int kGroupsPerPass = 64 / L;
+  const int gsub = lane / L;
+  const int m_l = (lane % L) / WR;
+  const int wr = lane % WR;
+  const int g_last = ng / kW - 1;  // the wave's last group index
+  // Group index and row of this lane's unit in pass i (i a compile-time constant). Passes past
+  // the wave's last group stage that group again (the same values; the host bounds the passes).
+  auto pass_group = [&](int i) {
+    return P >= 64 ? min((i * 64) / P, g_last) : min(i * kGroupsPerPass + gsub, g_last);
+  };
+  auto pass_row = [&](int i) { return (P >= 64 ? ((i * 64) % P) / WR : 0) + m_l; };
+  constexpr int kStage = max_stage_per_lane(MT);
+  uint4 raw[kStage];
+#pragma unroll
+  for (int i = 0; i < kStage; ++i) {
+    // every pass loads (a load under a branch waits for the one before it, and an early exit
+    // spills raw[] to scratch)
+    const int g = wave + kW * pass_group(i);
+    const int m = min(pass_row(i), rows - 1);  // rows past the batch: read a real row, stage 0
+    raw[i] = *reinterpret_cast<const uint4*>(p.x + (m * p.K + g * G + wr * 8));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  NativeLoad<G> buf[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    native_load<G, F>(buf[d], slab(d), lane);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // Convert and store: rows past the batch stage zeros; a pass past the wave's last group stores
+  // that group's values again.
+#pragma unroll
+  for (int i = 0; i < kStage; ++i) {
+    const int g = wave + kW * pass_group(i);
+    const int m = pass_row(i);
+    uint4 v = m < rows ? raw[i] : make_uint4(0u, 0u, 0u, 0u);
+    float undo = 1.0f;
+    if constexpr (A == Act::kBF16) {
+      const uint32_t e = group_max<WR>(bf16_max_mag(v)) >> 7;
+      const int shift = bf16_stage_shift(e);
+      const float sc = __builtin_bit_cast(float, static_cast<uint32_t>(127 - shift) << 23);
+      undo = __builtin_bit_cast(float, static_cast<uint32_t>(127 + shift) << 23);
+      v.x = bf16_pair_to_half_pair(v.x, sc);
+      v.y = bf16_pair_to_half_pair(v.y, sc);
+      v.z = bf16_pair_to_half_pair(v.z, sc);
+      v.w = bf16_pair_to_half_pair(v.w, sc);
+    }
+    const uint4 xp = pair_activations(v);
+    // even k: x0 x2 x4 x6 (xp.x, xp.z), odd k: x1 x3 x5 x7 (xp.y, xp.w)
+    constexpr uint32_t kOnes = 0x3c003c00u;
+    float se = dot2<Act::kF16>(xp.z, kOnes, dot2<Act::kF16>(xp.x, kOnes, 0.0f));
+    float so = dot2<Act::kF16>(xp.w, kOnes, dot2<Act::kF16>(xp.y, kOnes, 0.0f));
+    se = group_sum<WR>(se);
+    so = group_sum<WR>(so);
+    sm.xs[(g * WR + wr) * MT + m] = xp;
+    // every lane of the (group, row) holds the same values and writes them (no branch)
+    sm.sums[g * MT + m] = make_float2(fmaf(-1024.0f, se, -64.0f * so), se + so);
+    sm.scale[g * MT + m] = undo;
+  }
+  // The wave reads back only what it wrote (its LDS accesses complete in order); the fences keep
+  // the compiler from hoisting the reads.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  float y[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      y[i][r] = 0.0f;
+    }
+  }
+  const int r0 = 4 * t;  // D rows of this lane
+  // Slab of slice-local group gl: 2 U MFMAs and the epilogue.
+  auto compute = [&](const NativeLoad<G>& ld, int gl) {
+    half8_t a[U];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const uint4 xv = sm.xs[(static_cast<size_t>(gl) * WR + U * t + j) * MT + min(n, MT - 1)];
+      a[j] = __builtin_bit_cast(half8_t, n < MT ? xv : make_uint4(0u, 0u, 0u, 0u));
+    }
+    float4_t seed;
+    float s[4];
+    float sc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = min(r0 + r, MT - 1);
+      const float2 v = sm.sums[gl * MT + row];
+      const bool live = r0 + r < MT;
+      s[r] = live ? v.y : 0.0f;
+      const float c = F == PacketFormat::kNativeSym ? fmaf(-8.0f, v.y, v.x) : v.x;
+      seed[r] = live ? c : 0.0f;
+      sc[r] = sm.scale[gl * MT + row];
+    }
+    uint32_t beta_pair = 0;
+    if constexpr (F == PacketFormat::kNativeAsym) {
+      beta_pair = __builtin_bit_cast(
+          uint32_t, __builtin_bit_cast(half2_t, ld.alpha) * __builtin_bit_cast(half2_t, ld.zp));
+    }
+    float4_t dd[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      dd[i] = seed;
+#pragma unroll
+      for (int j = 0; j < U; ++j) {
+        dd[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            a[j], unpack_word8(slab_word<G>(ld, i, j), mask_lo, mask_hi), dd[i], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float alpha = half_bits_to_float(static_cast<uint16_t>(ld.alpha >> (16 * i)));
+      const float beta = half_bits_to_float(static_cast<uint16_t>(beta_pair >> (16 * i)));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if constexpr (A == Act::kBF16) {
+          float tt = alpha * dd[i][r];
+          if constexpr (F == PacketFormat::kNativeAsym) {
+            tt = fmaf(beta, s[r], tt);
+          }
+          y[i][r] = fmaf(tt, sc[r], y[i][r]);
+        } else {
+          y[i][r] = fmaf(alpha, dd[i][r], y[i][r]);
+          if constexpr (F == PacketFormat::kNativeAsym) {
+            y[i][r] = fmaf(beta, s[r], y[i][r]);
+          }
+        }
+      }
+    }
+  };
+  int j = 0;
+  auto block = [&](int gl0) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      compute(buf[d], gl0 + kW * d);
+      native_load<G, F>(buf[d], slab(j + d + D), lane);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    j += D;
+  };
+  // The wave's partial tile (rows < M) into the slot, then the first barrier.
+  auto reduce = [&]() {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (r0 + r < MT) {
+          sm.red[(wave * MT + r0 + r) * kSliceCols + 16 * i + n] = y[i][r];
+        }
+        y[i][r] = 0.0f;
+      }
+    }
+    lds_barrier();
+  };
+
+  if constexpr (kPieces) {
+    for (int blk = 0; blk < rg.head_len; ++blk) {
+      block((rg.head_blk0 + blk) * Q + wave);
+    }
+    if (rg.head_len > 0) {
+      reduce();
+      lds_barrier();  // the control wave has read the slot
+    }
+    for (int blk = 0; blk < rg.tail_len; ++blk) {
+      block(blk * Q + wave);
+    }
+    if (rg.tail_len > 0) {
+      reduce();
+      lds_barrier();
+    }
+  }
+  for (int r = 0; r < rg.whole; ++r) {
+    for (int blk = 0; blk < nbs; ++blk) {
+      block(blk * Q + wave);
+    }
+    reduce();
+    if (wave == (r & (kW - 1))) {
+      const size_t slice = static_cast<size_t>(rg.whole_slice0) + r;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int o = lane + 64 * i;
+        if (o < n_out) {
+          p.out[static_cast<size_t>(o / kSliceCols) * p.N + slice * kSliceCols + o % kSliceCols] =
+              float_to_act_bits<A>(total(o));
+        }
+      }
+    }
+    lds_barrier();  // the slot is free again
+  }
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+}
+
+template <int G, Act A, PacketFormat F, int MT>
+hipError_t launch_mfma_stream_t(const GemvLaunch& l, hipStream_t stream) {
+  constexpr int D = stream_depth_for_kb(G, kStreamKB);
+  int grid = 0;
+  GemvParams p = native_params<G, 1>(l, &grid);
+  p.pair = 0;
+  p.stream_whole = l.stream_whole;
+  grid = l.stream_grid;
+  p.xcd_remap = grid % 8 == 0 ? 1 : 0;
+  const size_t lds = mfma_stream_lds_bytes<G, MT>(l.K / G, kStreamWaves);
+  if (l.stream_pieces) {
+    hipLaunchKernelGGL((w4a16_gemm_mfma_stream_kernel<G, A, F, kStreamWaves, D, MT, true>),
+                       dim3(grid), dim3(64 * (kStreamWaves + 1)), lds, stream, p);
+  } else {
+    hipLaunchKernelGGL((w4a16_gemm_mfma_stream_kernel<G, A, F, kStreamWaves, D, MT, false>),
+                       dim3(grid), dim3(64 * kStreamWaves), lds, stream, p);
+  }
+  return hipGetLastError();
+}
+
+template <int G, Act A, PacketFormat F>
+hipError_t mfma_stream_rows(const GemvLaunch& l, hipStream_t stream) {
+  if (l.M <= 4) return launch_mfma_stream_t<G, A, F, 4>(l, stream);
+  if (l.M <= 8) return launch_mfma_stream_t<G, A, F, 8>(l, stream);
+  return launch_mfma_stream_t<G, A, F, 16>(l, stream);
+}
+
+template <PacketFormat F>
+hipError_t mfma_stream_dispatch(const GemvLaunch& l, hipStream_t stream) {
+  if (l.group_size == 64) {
+    return l.act == Act::kF16 ? mfma_stream_rows<64, Act::kF16, F>(l, stream)
+                              : mfma_stream_rows<64, Act::kBF16, F>(l, stream);
+  }
+  return l.act == Act::kF16 ? mfma_stream_rows<128, Act::kF16, F>(l, stream)
+                            : mfma_stream_rows<128, Act::kBF16, F>(l, stream);
+}
+
+}  // namespace
+
+int mfma_stream_rows_for_batch(int batch) { return batch <= 4 ? 4 : batch <= 8 ? 8 : 16; }
+
+size_t mfma_stream_lds(int group_size, int k, int batch) {
+  const int mt = mfma_stream_rows_for_batch(batch);
+  const int ng = k / group_size;
+  const int wr = group_size / 8;
+  return static_cast<size_t>(ng) * mt * (wr * 16 + 8 + 4) +
+         static_cast<size_t>(kStreamWaves) * mt * kSliceCols * 4;
+}
+
+bool mfma_stream_fits(int group_size, int k, int batch) {
+  const int mt = mfma_stream_rows_for_batch(batch);
+  const int units_per_lane = ((k / group_size / kStreamWaves) * mt * (group_size / 8) + 63) / 64;
+  return (k / group_size) % kStreamWaves == 0 && units_per_lane <= max_stage_per_lane(mt);
+}
+
+hipError_t launch_w4a16_gemm_mfma_stream(const GemvLaunch& l, hipStream_t stream) {
+  if (l.mode != GemvMode::kStreamK || !l.stream || l.m_tile != kMfmaRows || l.M < 1 ||
+      l.M > kMfmaRows || l.fuse != GemvFuse::kNone || l.slice_cols != kSliceCols ||
+      l.stream_half || l.stream_grid <= 0 || !mfma_stream_fits(l.group_size, l.K, l.M)) {
+    return hipErrorInvalidValue;
+  }
+  const int ng = l.K / l.group_size;
+  const int quantum = l.stream_waves * l.stream_depth;
+  if (l.stream_waves != kStreamWaves ||
+      l.stream_depth != stream_depth_for_kb(l.group_size, kStreamKB) || ng % quantum != 0) {
+    return hipErrorInvalidValue;
+  }
+  const long long slices = l.N / kSliceCols;
+  if (l.stream_pieces) {
+    const long long left = slices - static_cast<long long>(l.stream_grid) * l.stream_whole;
+    if (l.counters == nullptr || l.partials == nullptr || slices > kStreamMaxSlices ||
+        l.stream_whole < 0 || left <= 0 || left >= l.stream_grid ||
+        left * (ng / quantum) < l.stream_grid ||
+        left * (ng / quantum) * l.stream_grid >= (1LL << 31)) {
+      return hipErrorInvalidValue;
+    }
+  } else if (l.stream_whole <= 0 ||
+             static_cast<long long>(l.stream_whole) * l.stream_grid != slices) {
+    return hipErrorInvalidValue;
+  }
+  switch (l.format) {
+    case PacketFormat::kNativeSym: return mfma_stream_dispatch<PacketFormat::kNativeSym>(l, stream);
+    case PacketFormat::kNativeAsym: return mfma_stream_dispatch<PacketFormat::kNativeAsym>(l, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace fk

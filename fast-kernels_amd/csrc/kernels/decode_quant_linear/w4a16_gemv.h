@@ -78,7 +78,8 @@ constexpr int kStreamMaxSlices = 16384;
 // Static LDS of the stream kernel besides the dynamic part: two reduction slots of 8 waves x
 // rows x 32 floats, per activation row.
 constexpr size_t kStreamStaticLdsBytes = 2 * 8 * 32 * sizeof(float);
-// Workspace floats of a stream launch with pieces: two partial slots of rows x 32 per workgroup.
+// Workspace floats of a stream launch with pieces: two partial slots of rows x 32 per workgroup
+// (the matrix-core stream kernel's slots hold 16 rows whatever the batch).
 inline size_t stream_partial_floats(int grid, int rows) {
   return static_cast<size_t>(grid) * 2 * rows * kSliceCols;
 }
@@ -108,5 +109,11 @@ hipError_t launch_w4a16_gemv(const GemvLaunch& launch, hipStream_t stream);
 hipError_t launch_w4a16_gemm_mfma(const GemvLaunch& launch, hipStream_t stream);
 hipError_t launch_w4a16_gemv_native(const GemvLaunch& launch, hipStream_t stream);
 hipError_t launch_w4a16_gemv_stream(const GemvLaunch& launch, hipStream_t stream);
+// Matrix-core kernel on the stream schedule (w4a16_gemm_mfma_stream.hip): native slabs, 1-16 rows
+// (m_tile == kMfmaRows), the rows staged whole in LDS. mfma_stream_fits: K/G a multiple of the
+// waves and a wave's staging within its registers; mfma_stream_lds: its dynamic LDS bytes.
+hipError_t launch_w4a16_gemm_mfma_stream(const GemvLaunch& launch, hipStream_t stream);
+bool mfma_stream_fits(int group_size, int k, int batch);
+size_t mfma_stream_lds(int group_size, int k, int batch);
 
 }  // namespace fk

@@ -1,7 +1,8 @@
 // W4A16 GEMV launch entry points. The kernels are in w4a16_gemv_kernels.h; this file instantiates
 // the reference packet format (kArc, stream-K and the reference split-K protocol) and routes every
-// launch: 16-row m-tiles to the matrix-core kernel (w4a16_gemm_mfma.hip), native packet formats
-// to w4a16_gemv_native.hip.
+// launch: 16-row m-tiles to the matrix-core kernels (w4a16_gemm_mfma.hip, or on the stream schedule
+// w4a16_gemm_mfma_stream.hip), native packet formats to w4a16_gemv_native.hip or, on the stream
+// schedule, w4a16_gemv_stream.hip.
 #include "w4a16_gemv_kernels.h"
 
 namespace fk {
@@ -23,7 +24,7 @@ hipError_t launch_w4a16_gemv(const GemvLaunch& l, hipStream_t stream) {
     return launch_w4a16_gemv_fused(l, stream);
   }
   if (l.m_tile == kMfmaRows) {
-    return launch_w4a16_gemm_mfma(l, stream);
+    return l.stream ? launch_w4a16_gemm_mfma_stream(l, stream) : launch_w4a16_gemm_mfma(l, stream);
   }
   if (l.stream) {
     return launch_w4a16_gemv_stream(l, stream);

@@ -44,6 +44,7 @@
 // Math per group is native_compute_group's (w4a16_gemv_native.h); results equal the per-slice
 // kernel's up to fp32 summation order across waves.
 #include "w4a16_gemv_native.h"
+#include "w4a16_stream_common.h"
 
 namespace fk {
 namespace {
@@ -66,43 +67,6 @@ struct StreamLds {
   __device__ void set_sums(int m, int gl, int t, float2 v) { sums[at(m, gl) * 4 + t] = v; }
   __device__ void set_scale(int m, int gl, float v) { scale[at(m, gl)] = v; }
 };
-
-// A workgroup's parts: stream_whole whole slices, and (with pieces) its share of the slices left
-// over past grid * stream_whole of them, as an equal contiguous range of blocks (kW * D groups;
-// nbs blocks a slice) of fewer blocks than a slice: a head piece (the end of a slice an earlier
-// workgroup starts) and a tail piece (the start of a slice a later workgroup finishes).
-struct StreamRange {
-  int head_slice, head_blk0, head_len;  // head piece: blocks head_blk0 .. of head_slice
-  int tail_slice, tail_len;             // tail piece: the first tail_len blocks of tail_slice
-  int whole_slice0, whole;              // whole slices whole_slice0 ..
-};
-
-// First left-over block of workgroup b (left-over blocks numbered from 0). 32-bit arithmetic: the
-// host bounds grid * total below 2^31 (a 64-bit division costs hundreds of instructions).
-__device__ __forceinline__ int range_start(int b, int total, int grid) {
-  return static_cast<int>(static_cast<uint32_t>(b * total) / static_cast<uint32_t>(grid));
-}
-
-// Workgroup owning left-over block x: the last b with range_start(b) <= x.
-__device__ __forceinline__ int range_owner(int x, int total, int grid) {
-  return static_cast<int>(static_cast<uint32_t>((x + 1) * grid - 1) / static_cast<uint32_t>(total));
-}
-
-// The pieces of workgroup b's left-over range; slice s0 is the first left-over slice.
-__device__ __forceinline__ void stream_pieces(StreamRange& r, int b, int total, int grid, int nbs,
-                                              int s0) {
-  const int blk0 = range_start(b, total, grid);
-  const int blk1 = range_start(b + 1, total, grid);
-  const int q0 = blk0 / nbs;
-  const int off0 = blk0 - q0 * nbs;
-  r.head_slice = s0 + q0;
-  r.head_blk0 = off0;
-  r.head_len = off0 != 0 ? min(blk1, blk0 - off0 + nbs) - blk0 : 0;
-  const int c = blk0 + r.head_len;  // a slice start, or blk1
-  // the range is shorter than a slice, so what follows the head piece is the start of one slice
-  r.tail_slice = s0 + c / nbs;
-  r.tail_len = blk1 - c;
-}
 
 // kW streaming waves per workgroup (plus the control wave with kPieces), D register buffers
 // (slabs in flight) per wave, MT activation rows; one workgroup per CU. kStageSlots passes of
@@ -133,26 +97,13 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   constexpr int kOut = MT * kSliceCols;  // outputs of a slice
   constexpr int kOutPerLane = (kOut + 63) / 64;
 
-  StreamRange rg;
-  rg.head_slice = 0;
-  rg.head_blk0 = 0;
-  rg.head_len = 0;
-  rg.tail_slice = 0;
-  rg.tail_len = 0;
+  const int slices = p.N / kSliceCols;
+  StreamRange rg = stream_range(b, grid, p.stream_whole, slices, nbs, kPieces);
   int half = 0;
-  // Left-over slices (pieces): the first, and their blocks.
-  const int s_left = grid * p.stream_whole;
-  const int left_blocks = (p.N / kSliceCols - s_left) * nbs;
   if constexpr (kHalf) {
     half = b & 1;
     rg.whole_slice0 = b >> 1;
     rg.whole = 1;
-  } else {
-    rg.whole_slice0 = b * p.stream_whole;
-    rg.whole = p.stream_whole;
-    if constexpr (kPieces) {
-      stream_pieces(rg, b, left_blocks, grid, nbs, s_left);
-    }
   }
 
   if constexpr (kPieces) {
@@ -181,71 +132,13 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
           slot ^= 1;
         }
       }
-#pragma unroll
-      for (int pc = 0; pc < 2; ++pc) {
-        if (!has[pc]) {
-          continue;
-        }
-        const int slice = pc == 0 ? rg.head_slice : rg.tail_slice;
-        // This workgroup's slot: piece pc of workgroup b.
-        float* mine = p.partials + (static_cast<size_t>(b) * 2 + pc) * kOut;
-#pragma unroll
-        for (int i = 0; i < kOutPerLane; ++i) {
-          const int o = lane + 64 * i;
-          if (o < kOut) {
-            __hip_atomic_store(&mine[o], v[pc][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-        }
-        // Hand-off without cache-wide fences (an agent-scope release writes back the whole L2
-        // and costs microseconds): the partials are agent-scope stores, which gfx950 writes
-        // through the XCD's L2 to the memory-side coherence point; s_waitcnt vmcnt(0) holds the
-        // wave until all of them are acknowledged there, and only then is the counter bumped. The
-        // last part's loads are agent-scope too, so they miss the L2 and read the coherence
-        // point, after its counter bump has returned the final count. Every part does the same,
-        // so whichever arrives last sees all parts' partials.
-        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-        // Parts of the slice: the workgroups owning its first and last block.
-        const int s0 = (slice - s_left) * nbs;
-        const int b_first = range_owner(s0, left_blocks, grid);
-        const int b_last = range_owner(s0 + nbs - 1, left_blocks, grid);
-        uint32_t prev = 0;
-        if (lane == 0) {
-          prev = __hip_atomic_fetch_add(&p.counters[slice], 1u, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
-        }
-        prev = __builtin_amdgcn_readfirstlane(prev);
-        if (prev == static_cast<uint32_t>(b_last - b_first)) {
-          float acc[kOutPerLane];
-#pragma unroll
-          for (int i = 0; i < kOutPerLane; ++i) {
-            acc[i] = 0.0f;
-          }
-          for (int bb = b_first; bb <= b_last; ++bb) {
-            // The slice is the head piece of a workgroup whose range starts inside it.
-            const int pp = range_start(bb, left_blocks, grid) > s0 ? 0 : 1;
-            const float* part = p.partials + (static_cast<size_t>(bb) * 2 + pp) * kOut;
-#pragma unroll
-            for (int i = 0; i < kOutPerLane; ++i) {
-              const int o = lane + 64 * i;
-              if (o < kOut) {
-                acc[i] += __hip_atomic_load(&part[o], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-              }
-            }
-          }
-#pragma unroll
-          for (int i = 0; i < kOutPerLane; ++i) {
-            const int o = lane + 64 * i;
-            const int m = o / kSliceCols;
-            if (o < kOut && m < p.M) {
-              p.out[static_cast<size_t>(m) * p.N + static_cast<size_t>(slice) * kSliceCols +
-                    o % kSliceCols] = float_to_act_bits<A>(acc[i]);
-            }
-          }
-          if (lane == 0) {
-            __hip_atomic_store(&p.counters[slice], 0u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-          }
-        }
+      if (has[0]) {
+        stream_hand_off<A, kOutPerLane>(p, b, 0, rg.head_slice, grid, p.stream_whole, slices, nbs,
+                                        kOut, kOut, v[0], lane);
+      }
+      if (has[1]) {
+        stream_hand_off<A, kOutPerLane>(p, b, 1, rg.tail_slice, grid, p.stream_whole, slices, nbs,
+                                        kOut, kOut, v[1], lane);
       }
       for (int r = 0; r < rg.whole; ++r) {
         lds_barrier();

@@ -298,6 +298,14 @@ bool stream_pieces_enabled() {
 }
 
 
+// FK_W4A16_MFMA_STREAM=0 keeps 3-8-row native launches off the matrix-core stream kernel.
+constexpr int kMfmaStreamMinBatch = 3;
+constexpr int kMfmaStreamMaxBatch = 8;
+bool mfma_stream_enabled() {
+  static const bool enabled = env_enabled("FK_W4A16_MFMA_STREAM");
+  return enabled;
+}
+
 // FK_W4A16_STREAM_HALF=0 keeps shapes with at most half as many slices as CUs off half-slices.
 bool stream_half_enabled() {
   static const bool enabled = [] {
@@ -337,6 +345,63 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
   }
   ArcW4A16Plan plan = plan_arc_impl(batch, n, k, group_size, activation_dtype, split_k_slices,
                                     cu_count, m_tile_for_kernel(batch, kernel));
+  if (format != fk::PacketFormat::kArc && plain && split_k_slices == 0 &&
+      batch >= kMfmaStreamMinBatch && batch <= kMfmaStreamMaxBatch && kernel != kKernelDot2 &&
+      mfma_stream_enabled()) {
+    // The matrix cores on the stream schedule (w4a16_gemm_mfma_stream.hip): the rows staged whole
+    // in LDS, one workgroup per CU, pieces of the slices left over (as the one-row stream plan).
+    // Measured on MI355X (benchmark configuration 3, 14336 x 4096, G = 64, asymmetric, fp16;
+    // alternating runs on one GPU, against the automatic plan without it): 4 rows 12.8 -> 11.0-11.4
+    // us, 8 rows 13.0 -> 12.6 us; 2 rows 9.7 -> 10.8 us and 16 rows 13.0 -> 15.6 us are slower
+    // (two rows are cheaper on the dot2 loop; sixteen rows of K staged per workgroup are as many
+    // bytes as its weights), so it takes 3-8 rows.
+    const std::size_t lds_limit = cu_count_given ? kGfx950LdsBytes : device_lds_per_block();
+    const int depth = fk::stream_depth_for_kb(group_size, fk::kStreamKB);
+    const int num_groups = k / group_size;
+    const int nbs = num_groups / (fk::kStreamWaves * depth);
+    const long long slices = n / fk::kSliceCols;
+    const long long cus = cu_count;
+    if (num_groups % (fk::kStreamWaves * depth) == 0 && fk::mfma_stream_fits(group_size, k, batch) &&
+        fk::mfma_stream_lds(group_size, k, batch) <= lds_limit && slices <= fk::kStreamMaxSlices) {
+      const long long left = slices % cus;
+      long long grid = 0;
+      int whole = 0;
+      bool pieces = false;
+      if (slices >= cus && left == 0) {
+        grid = cus;
+        whole = static_cast<int>(slices / cus);
+      } else if (slices > cus && left * nbs >= cus) {
+        grid = cus;
+        whole = static_cast<int>(slices / cus);
+        pieces = true;
+      } else if (slices < cus) {
+        grid = slices;
+        whole = 1;
+      }
+      if (grid > 0) {
+        plan.m_tile = fk::kMfmaRows;
+        plan.schedule = kScheduleStream;
+        plan.slice_cols = fk::kSliceCols;
+        plan.workgroups = static_cast<int>(grid);
+        plan.stream_depth = depth;
+        plan.stream_whole = whole;
+        plan.stream_pieces = pieces ? 1 : 0;
+        plan.stream_half = 0;
+        const long long left_blocks = (slices - grid * whole) * nbs;
+        const long long piece_blocks = pieces ? (left_blocks + grid - 1) / grid : 0;
+        plan.groups_per_workgroup = static_cast<int>(
+            whole * num_groups + piece_blocks * fk::kStreamWaves * depth);
+        plan.max_tile_contributors =
+            pieces ? static_cast<int>((nbs * grid + left_blocks - 1) / left_blocks + 1) : 1;
+        plan.workspace_bytes =
+            pieces ? kCounterRegionBytes + fk::stream_partial_floats(static_cast<int>(grid),
+                                                                     fk::kMfmaRows) *
+                                               sizeof(float)
+                   : 0;
+        return plan;
+      }
+    }
+  }
   if (format == fk::PacketFormat::kArc || plan.m_tile == fk::kMfmaRows) {
     return plan;  // the matrix-core kernel reads whole tiles in every format
   }
@@ -547,9 +612,10 @@ void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::u
     l.units_per_workgroup = 2 * plan.groups_per_workgroup;
   } else if (plan.schedule == kScheduleStream) {
     const int cols = plan.stream_half ? fk::kSliceCols / 2 : fk::kSliceCols;
-    if (format == fk::PacketFormat::kArc || plan.m_tile != batch || plan.slice_cols != cols ||
+    const bool rows_ok = plan.m_tile == fk::kMfmaRows ? batch <= fk::kMfmaRows : plan.m_tile == batch;
+    if (format == fk::PacketFormat::kArc || !rows_ok || plan.slice_cols != cols ||
         fuse != fk::GemvFuse::kNone) {
-      throw std::logic_error("stream schedule on a plan that is not one unfused native row");
+      throw std::logic_error("stream schedule on a plan that is not an unfused native one");
     }
     l.stream = true;
     l.slice_cols = fk::kSliceCols;

@@ -221,13 +221,15 @@ def test_native_format_validation_without_gpu(lib: ctypes.CDLL) -> None:
         ((1, 12288, 8192, 128), (32, 96, 256, 2)),     # 1 slice + pieces of the 128 left over
         ((1, 22016, 4096, 128), (32, 32, 688, 0)),     # 7B gate_up: 344 pairs would fill 2 rounds unevenly
         ((2, 12288, 4096, 128), (32, 32, 384, 0)),     # pairs and stream for one row only
+        ((4, 12288, 4096, 128), (32, 48, 256, 2)),     # four rows: matrix cores on the stream schedule
         ((1, 57344, 8192, 128), (32, 448, 256, 2)),    # 70B gate_up: 7 whole slices per CU
         ((1, 8192, 28672, 128), (32, 224, 256, 2)),    # 70B down: one slice of 224 groups per CU
         ((1, 8192, 28672 + 128, 128), (32, 113, 510, 0)),  # 225 groups: not a multiple of 16
         ((1, 4096, 4096, 128), (16, 32, 256, 2)),      # 128 slices: a half slice per CU
         ((1, 4096, 14336, 128), (16, 112, 256, 2)),    # 128 slices of 112 groups: halves, whole K
-        ((4, 14336, 4096, 64), (32, 64, 448, 0)),      # four rows share a slice's runs
-        ((16, 14336, 4096, 64), (128, 16, 448, 0)),    # matrix cores: the reference-format plan
+        ((4, 14336, 4096, 64), (32, 128, 256, 2)),     # four rows: 1 slice + pieces on the matrix cores
+        ((8, 14336, 4096, 64), (32, 128, 256, 2)),     # eight rows, the same stream plan
+        ((16, 14336, 4096, 64), (128, 16, 448, 0)),    # sixteen rows: matrix-core tiles
     ],
 )
 def test_native_plan_policy_without_gpu(lib: ctypes.CDLL, shape, want) -> None:
@@ -264,11 +266,12 @@ def test_fused_entry_points_validate_without_gpu(lib: ctypes.CDLL) -> None:
 
 def test_kernel_choice_plans_without_gpu(lib: ctypes.CDLL) -> None:
     """FK_KERNEL_DOT2 keeps every batch on m-tiles of at most 8 rows, FK_KERNEL_MFMA puts every
-    batch on 16-row tiles over whole 128-column tiles, FK_KERNEL_AUTO is the forward's dispatch;
-    another value is an invalid argument."""
+    batch on 16-row tiles (3-8 rows on the stream schedule over 32-column slices, others over
+    whole 128-column tiles), FK_KERNEL_AUTO is the forward's dispatch; another value is an
+    invalid argument."""
     lib.fk_last_error.restype = ctypes.c_char_p
     for batch, kernel, want in [(16, 1, (8, 32)), (2, 2, (16, 128)), (2, 0, (2, 32)),
-                                (16, 0, (16, 128))]:
+                                (16, 0, (16, 128)), (4, 0, (16, 32)), (4, 2, (16, 32))]:
         p = Plan()
         assert lib.fk_w4a16_plan_for_kernel(batch, 14336, 4096, 64, 0, 0, 256, 1, kernel,
                                             ctypes.byref(p)) == 0

@@ -257,3 +257,36 @@ def test_stream_schedule_variants(n: int, k: int, g: int, act: str, asym: bool, 
     np.testing.assert_array_equal(ys[0], ys[2])
     rows = _rows(n)
     _assert_gemv_close(ys[0][:, rows], _oracle_rows(case, rows, act), case, f"stream {plan}")
+
+
+@pytest.mark.parametrize(
+    "m,n,k,g,act,asym",
+    [
+        (3, 12288, 4096, 128, "bf16", False),  # 1 slice + pieces, four-row staging
+        (4, 14336, 4096, 64, "f16", True),     # configuration 3, four rows
+        (8, 8192, 4096, 128, "bf16", True),    # whole slices, eight rows
+        (7, 6144, 4096, 128, "f16", False),    # 192 slices: one per workgroup, an odd batch
+        (5, 8192, 4096, 128, "bf16", False),   # eight-row staging, G = 128
+        (8, 14336, 4096, 64, "bf16", True),    # configuration 3's shape in bf16, eight rows
+    ],
+)
+def test_mfma_stream_variants(m: int, n: int, k: int, g: int, act: str, asym: bool) -> None:
+    """The matrix-core kernel on the stream schedule (rows staged whole in LDS, pieces handed off
+    by the control wave): both group sizes, dtypes and formats, odd batches; every row against the
+    oracle on a spread of columns, and identical bits over three calls."""
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the shapes are chosen for 256 CUs")
+    case = make_case(m, n, k, g, act=act, asymmetric=asym, seed=3 * n + k + g + m)
+    x, q, a, b = _upload(case)
+    fmt = "native_asym" if asym else "native_sym"
+    slabs = convert_arc_to_native_packets(pack_arc_w4a16_packets(q, a, b, group_size=g), n=n, k=k,
+                                          group_size=g, packet_format=fmt)
+    plan = arc_w4a16_plan(batch=m, n=n, k=k, group_size=g,
+                          activation_dtype=x.dtype, packet_format=2 if asym else 1)
+    assert plan["schedule"] == 2 and plan["m_tile"] == 16, plan
+    ys = [_bits(arc_w4a16_forward_native(x, slabs, n=n, k=k, group_size=g, packet_format=fmt))
+          for _ in range(3)]
+    np.testing.assert_array_equal(ys[0], ys[1])
+    np.testing.assert_array_equal(ys[0], ys[2])
+    rows = _rows(n)
+    _assert_gemv_close(ys[0][:, rows], _oracle_rows(case, rows, act), case, f"mfma stream {plan}")

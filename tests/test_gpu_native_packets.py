@@ -186,8 +186,9 @@ def test_forward_native_matches_reference_packets(asym, group_size, batch, act) 
         ((3, 1024, 37 * 64, 64), "f16", True, 32),   # odd group count over two 32-group chunks
         ((2, 2048, 130 * 64, 64), "bf16", False, 32),  # three 64-group chunks, the last of 2 groups
         ((2, 4096, 4096, 64), "f16", True, 32),      # two rows
-        ((8, 4096, 4096, 64), "bf16", True, 128),    # eight rows (half-depth pipeline)
+        ((8, 4096, 4096, 64), "bf16", True, 32),     # eight rows: matrix cores, stream schedule
         ((16, 4096, 4096, 64), "bf16", True, 128),   # matrix-core tile over four slabs per group
+        ((5, 4096, 8192, 64), "f16", False, 32),     # staging past the registers: dot2 runs
     ],
 )
 def test_forward_native_plans_match_oracle(shape, act, asym, cols) -> None:
