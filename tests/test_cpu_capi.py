@@ -281,3 +281,15 @@ def test_kernel_choice_plans_without_gpu(lib: ctypes.CDLL) -> None:
     assert b"kernel" in lib.fk_last_error()
     rc = lib.fk_w4a16_forward_kernel(None, None, None, None, 0, 1, 128, 256, 128, 0, 0, 0, 5, None)
     assert rc == 1 and b"kernel" in lib.fk_last_error()
+
+
+@pytest.mark.parametrize("split", [1, 2, 4])
+def test_forced_split_never_pairs_or_streams(lib: ctypes.CDLL, split: int) -> None:
+    """A forced K split at shapes that would otherwise stream slice pairs (10240 x 4096) or take
+    the stream schedule (8192 x 8192) plans per-slice runs of ceil(K/G/split) groups: the pair and
+    stream kernels only take whole slices over all of K from the automatic policy."""
+    for n, k in ((10240, 4096), (8192, 8192)):
+        p = Plan()
+        assert lib.fk_w4a16_plan_for_format(1, n, k, 128, 0, split, 256, 1, ctypes.byref(p)) == 0
+        assert p.schedule == 0 and p.slice_cols == 32, (n, k, split)
+        assert p.groups_per_workgroup == -(-(k // 128) // split)
