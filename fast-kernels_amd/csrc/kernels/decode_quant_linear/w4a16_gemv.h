@@ -49,13 +49,14 @@ struct GemvLaunch {
   int stream_waves = 0;   // stream schedule: streaming waves per workgroup (kStreamWaves)
   int stream_depth = 0;   // stream schedule: units in flight per wave
   int stream_grid = 0;    // stream schedule: workgroups
-  int stream_whole = 0;   // stream schedule: whole slices per workgroup (1 for half slices)
+  int stream_whole = 0;   // stream schedule: whole slices (or half-slices) per workgroup
   // The slices left over past stream_grid * stream_whole (fewer than the workgroups) are dealt
   // as equal block ranges, a head and a tail piece per workgroup, finished through the
   // workspace: counters, one per slice; partials, 2 * 32 floats per workgroup.
   bool stream_pieces = false;
-  // Half-slices (G = 128, one row): workgroup b streams the 16 columns 16 * (b & 1) .. of slice
-  // b / 2, reading half of every slab (stream_grid = 2 * slices).
+  // Half-slices (G = 128, one row): workgroup b streams the stream_whole half-slices
+  // b * stream_whole .., half-slice hs being the 16 columns 16 * (hs & 1) .. of slice hs / 2
+  // (half of every slab); stream_grid * stream_whole = 2 * slices.
   bool stream_half = false;
 };
 

@@ -37,9 +37,11 @@
 //    on meanwhile; the control wave meets them at every later barrier (s_barrier counts waves).
 //  * With the logical-to-hardware workgroup remap consecutive ranges, and so the parts of a split
 //    slice, run on one XCD, whose L2 then serves the partials the last part reads.
-//  * kHalf (one row, G = 128, at most half as many slices as CUs): workgroup b streams 16 columns,
-//    the first or second KB of every slab of slice b / 2, so that every CU streams and no slice
-//    is split over K.
+//  * kHalf (one row, G = 128): the slices' 16-column halves are the units (the first or second KB
+//    of every slab). Workgroup b streams half-slices b * whole .. (slice hs / 2, half hs & 1):
+//    with at most half as many slices as CUs one each, so every CU streams and no slice is split
+//    over K; with twice the slices a multiple of the CUs (8B gate_up: 1792 halves, 7 per CU) an
+//    even share of halves, where whole slices would not divide.
 //
 // Math per group is native_compute_group's (w4a16_gemv_native.h); results equal the per-slice
 // kernel's up to fp32 summation order across waves.
@@ -99,12 +101,9 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
 
   const int slices = p.N / kSliceCols;
   StreamRange rg = stream_range(b, grid, p.stream_whole, slices, nbs, kPieces);
+  // kHalf: half-slices hs0 .. hs0 + whole - 1, half-slice hs being half hs & 1 of slice hs / 2.
+  const int hs0 = kHalf ? b * p.stream_whole : 0;
   int half = 0;
-  if constexpr (kHalf) {
-    half = b & 1;
-    rg.whole_slice0 = b >> 1;
-    rg.whole = 1;
-  }
 
   if constexpr (kPieces) {
     if (wave == kW) {
@@ -179,11 +178,21 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     }
     return p.packets + static_cast<size_t>(static_cast<uint32_t>(c * kW + off)) * stride;
   };
-  auto load_slab = [&](NativeLoad<G>& ld, const uint8_t* ptr) {
+  // kHalf: the wave's slab i is slab jj of half-slice r (spr slabs a half-slice), uniform 32-bit
+  // arithmetic.
+  const int spr = nbs * D;
+  auto load_slab = [&](NativeLoad<G>& ld, int i) {
     if constexpr (kHalf) {
-      native_load_half<G, F>(ld, ptr, lane, half);
+      const int c = __builtin_amdgcn_readfirstlane(min(i, j_last));
+      const int r = static_cast<int>(static_cast<uint32_t>(c) / static_cast<uint32_t>(spr));
+      const int hs = hs0 + r;
+      const int jj = c - r * spr;
+      native_load_half<G, F>(
+          ld, p.packets + static_cast<size_t>(static_cast<uint32_t>((hs >> 1) * ng + wave + kW * jj)) *
+                              stride,
+          lane, hs & 1);
     } else {
-      native_load<G, F>(ld, ptr, lane);
+      native_load<G, F>(ld, slab(i), lane);
     }
   };
 
@@ -208,7 +217,7 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   NativeLoad<G> buf[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
-    load_slab(buf[d], slab(d));
+    load_slab(buf[d], d);
     __builtin_amdgcn_sched_barrier(0);  // the same issue order as the refills in the loop
   }
   int staged = 0;
@@ -258,7 +267,7 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     for (int d = 0; d < D; ++d) {
       native_compute_group<G, A, MT, F, StreamLds<G>, kHalf ? 1 : 2>(sm, buf[d], gl0 + kW * d, t,
                                                                      mask_lo, mask_hi, y, half);
-      load_slab(buf[d], slab(j + d + D));
+      load_slab(buf[d], j + d + D);
       // Issue the refill here, not after the block's later slabs: the scheduler would otherwise
       // sink every load below the block's arithmetic and drain the pipeline once per block.
       __builtin_amdgcn_sched_barrier(0);
@@ -311,6 +320,9 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     }
   }
   for (int r = 0; r < rg.whole; ++r) {
+    if constexpr (kHalf) {
+      half = (hs0 + r) & 1;
+    }
     // Without pieces: blocks that each stage one more pass, then blocks that do not: two loops,
     // no branch in either.
     int blk = 0;
@@ -332,7 +344,8 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     const int slot = reduce();
     // One wave, rotating with the slice, writes it.
     constexpr int kCols = kHalf ? kSliceCols / 2 : kSliceCols;
-    const size_t slice = static_cast<size_t>(rg.whole_slice0) + r;
+    const size_t slice = kHalf ? static_cast<size_t>((hs0 + r) >> 1)
+                               : static_cast<size_t>(rg.whole_slice0) + r;
     if (wave == (r & (kW - 1))) {
 #pragma unroll
       for (int i = 0; i < (MT * kCols + 63) / 64; ++i) {
@@ -364,6 +377,19 @@ hipError_t launch_stream_t(const GemvLaunch& l, hipStream_t stream) {
   p.stream_whole = l.stream_whole;
   p.xcd_remap = grid % 8 == 0 ? 1 : 0;
   const size_t lds = static_cast<size_t>(MT) * stream_lds_bytes(G, l.K / G + 1);
+  if constexpr (D != stream_depth_for_kb(G, kStreamKB)) {
+    // the deeper pipeline serves half slices only (a half-slab is half the bytes)
+    if constexpr (G == 128 && MT == 1) {
+      if (!l.stream_half || l.stream_pieces) {
+        return hipErrorInvalidValue;
+      }
+      hipLaunchKernelGGL((w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, 1, false, true>),
+                         dim3(grid), dim3(64 * kW), lds, stream, p);
+      return hipGetLastError();
+    } else {
+      return hipErrorInvalidValue;
+    }
+  }
   if (l.stream_pieces) {
     hipLaunchKernelGGL((w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, MT, true, false>),
                        dim3(grid), dim3(64 * (kW + 1)), lds, stream, p);
@@ -396,8 +422,15 @@ hipError_t stream_dispatch_slots(const GemvLaunch& l, hipStream_t stream) {
 template <int G, Act A, PacketFormat F>
 hipError_t stream_dispatch_rows(const GemvLaunch& l, hipStream_t stream) {
   constexpr int D = stream_depth_for_kb(G, kStreamKB);
-  if (l.stream_waves != kStreamWaves || l.stream_depth != D) {
+  if (l.stream_waves != kStreamWaves ||
+      (l.stream_depth != D && !(l.stream_half && l.stream_depth == 2 * D))) {
     return hipErrorInvalidValue;
+  }
+  if constexpr (G == 128) {
+    // half slices with the weights' bytes in flight of whole slices
+    if (l.stream_half && l.stream_depth == 2 * D && l.M == 1) {
+      return stream_dispatch_slots<G, A, F, kStreamWaves, 2 * D, 1>(l, stream);
+    }
   }
   // MT > 1 (several rows per slab) builds, but measured slower than the per-slice runs on MI355X
   // (benchmark configuration 3, 14336 x 4096, G = 64: two rows 9.7 -> 10.5 us, four rows 12.9 ->
@@ -437,7 +470,8 @@ hipError_t launch_w4a16_gemv_stream(const GemvLaunch& l, hipStream_t stream) {
   }
   const long long slices = l.N / kSliceCols;
   if (l.stream_half) {
-    if (l.group_size != 128 || l.M != 1 || l.stream_pieces || l.stream_grid != 2 * slices) {
+    if (l.group_size != 128 || l.M != 1 || l.stream_pieces || l.stream_whole <= 0 ||
+        static_cast<long long>(l.stream_grid) * l.stream_whole != 2 * slices) {
       return hipErrorInvalidValue;
     }
   } else if (l.stream_pieces) {

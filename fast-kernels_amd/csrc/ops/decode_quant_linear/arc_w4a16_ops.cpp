@@ -315,6 +315,14 @@ bool stream_half_enabled() {
   return enabled;
 }
 
+// FK_W4A16_HALF_WHOLE=0 keeps shapes whose half-slices (not slices) divide over the CUs off the
+// stream schedule.
+constexpr long long kMaxHalvesPerCu = 4;
+bool stream_half_whole_enabled() {
+  static const bool enabled = env_enabled("FK_W4A16_HALF_WHOLE");
+  return enabled;
+}
+
 // FK_W4A16_STREAM_SMALL=0 keeps shapes with fewer slices than CUs on the per-slice runs.
 bool stream_small_enabled() {
   static const bool enabled = [] {
@@ -447,6 +455,9 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
   //  * at most half as many slices as CUs (G = 128, one row): a half-slice (16 columns, the first
   //    or second KB of every slab) per workgroup, so every CU streams and no slice is split over
   //    K (8B o 4.0 -> 3.9 us, 8B down 8.8 -> 8.0);
+  //  * twice the slices a multiple of the CUs, up to kMaxHalvesPerCu half-slices per CU: an even
+  //    share of half-slices, 4 KB of half-slabs in flight per wave (7B qkv, 3 per CU, 7.35 ->
+  //    6.97 us against slice pairs; 8B gate_up, 7 per CU, 13.5 -> 13.9 us, stays on pairs);
   //  * otherwise fewer slices than CUs and K too short to split (per == K/G): one whole slice per
   //    workgroup (8B qkv 5.16 -> 4.44 us, 7B o 4.67 -> 4.15). Pieces with no whole slice to hide
   //    their hand-off behind cost more than they save (8B o 4.8 -> 5.7 us), and 8B down as whole
@@ -477,6 +488,11 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
         grid = cus;
         whole = static_cast<int>(slices / cus);
         pieces = true;
+      } else if (batch == 1 && group_size == 128 && 2 * slices > cus && (2 * slices) % cus == 0 &&
+                 2 * slices <= kMaxHalvesPerCu * cus && stream_half_whole_enabled()) {
+        grid = cus;
+        whole = static_cast<int>(2 * slices / cus);
+        half = true;
       } else if (batch == 1 && group_size == 128 && 2 * slices <= cus && stream_half_enabled()) {
         grid = 2 * slices;
         whole = 1;
@@ -489,7 +505,11 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
         plan.schedule = kScheduleStream;
         plan.slice_cols = half ? fk::kSliceCols / 2 : fk::kSliceCols;
         plan.workgroups = static_cast<int>(grid);
-        plan.stream_depth = depth;
+        // Half-slices with several per workgroup keep a whole slice's 4 KB in flight per wave
+        // (four half-slabs); one half-slice per workgroup measured no better with them.
+        plan.stream_depth =
+            half && whole > 1 && num_groups % (fk::kStreamWaves * 2 * depth) == 0 ? 2 * depth
+                                                                                    : depth;
         plan.stream_whole = whole;
         plan.stream_pieces = pieces ? 1 : 0;
         plan.stream_half = half ? 1 : 0;

@@ -216,7 +216,7 @@ def test_native_format_validation_without_gpu(lib: ctypes.CDLL) -> None:
         ((1, 8192, 8192, 128), (32, 64, 256, 2)),      # 256 slices: one per CU, streamed
         ((1, 10240, 8192, 128), (32, 80, 256, 2)),     # 70B qkv: 1 slice + a quarter slice per CU
         ((1, 10240, 4096, 128), (64, 32, 160, 1)),     # 320 slices in 160 pairs
-        ((1, 12288, 4096, 128), (64, 32, 192, 1)),     # 7B qkv: 384 slices in 192 pairs (K short for pieces)
+        ((1, 12288, 4096, 128), (16, 96, 256, 2)),     # 7B qkv: 768 half-slices, 3 per CU
         ((1, 28672, 4096, 128), (64, 32, 448, 1)),     # 8B gate_up: 896 slices in 448 pairs
         ((1, 12288, 8192, 128), (32, 96, 256, 2)),     # 1 slice + pieces of the 128 left over
         ((1, 22016, 4096, 128), (32, 32, 688, 0)),     # 7B gate_up: 344 pairs would fill 2 rounds unevenly

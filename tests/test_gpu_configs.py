@@ -232,6 +232,8 @@ def test_config2_layer_graph_replays_match_eager() -> None:
         (4096, 4096, 128, "bf16", False, 1),   # 8B o
         (4096, 14336, 128, "f16", True, 1),    # 8B down, asymmetric
         (1024, 2048, 128, "bf16", True, 1),    # 64 workgroups
+        (12288, 4096, 128, "bf16", True, 1),   # 768 half-slices, 3 per CU (7B qkv)
+        (16384, 4096, 128, "f16", False, 1),   # 1024 half-slices, 4 per CU
         (6144, 4096, 128, "f16", False, 1),  # one slice per workgroup, 192 workgroups
     ],
 )
