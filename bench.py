@@ -18,7 +18,7 @@ after a graph of the W warm-up steps. value = algorithmic bytes
 per step / time per step (int4 codes + fp16 scales + activations + outputs; the reference
 packets' fp16 beta, when measured, is read but not credited).
 
-Also reported: per-shape us/call and GB/s (each shape's own graph, events over >= 200 launches),
+Also reported: per-shape us/call and GB/s (each shape's own graph of >= 300 launches, replayed once),
 a roofline object for the dominant kernel (gate_up), and the reference's CPU arithmetic (fp32
 accumulation) timed on all of this process's host cores on a bounded sample of the workload.
 """
@@ -285,15 +285,22 @@ def measure(torch, native, args, act, g, shapes, packets):
     ws_bytes = max(max(b.plan["workspace_bytes"] for b in bufs), 1)
     ws = torch.zeros(ws_bytes + 256, device="cuda", dtype=torch.uint8)
     torch.cuda.synchronize()
-    # Per-shape timing: each shape's own graph over its R rotations.
+    # Per-shape timing: each shape's own graph of reps x R launches (its R rotations in turn),
+    # replayed once between events, so that no graph launch boundary falls inside the run.
     per_shape = {}
     for b in bufs:
         R = len(b.packets)
-        run = make_runner(torch, lambda b=b: [b.launch(native, torch, ws, r) for r in range(R)], R, args.eager)
-        reps = max(1, args.per_shape_launches // R)
+        reps = max(1, -(-args.per_shape_launches // R))
+
+        def shape_fn(b=b, R=R, reps=reps):
+            for _ in range(reps):
+                for r in range(R):
+                    b.launch(native, torch, ws, r)
+
+        run = make_runner(torch, shape_fn, reps * R, args.eager)
         # warm as long as the timed run: the first shape otherwise pays for the clocks ramping up
-        time_events(torch, run, reps)
-        ms = time_events(torch, run, reps)
+        time_events(torch, run, 1)
+        ms = time_events(torch, run, 1)
         us = ms * 1e3 / (reps * R)
         per_shape[b.name] = {
             "n": b.n,
