@@ -57,7 +57,9 @@ struct MfmaParams {
   uint16_t* out;
   float* partials;
   uint32_t* counters;
-  int M, N, K, NG, tiles, mtiles, per, max_contrib, xcd_remap;
+  int M, N, K, NG, tiles, mtiles, per, max_contrib;
+  int grid;       // workgroups of the launch (gridDim would be a second, dependent argument load)
+  int xcd_remap;  // grid / 8 when consecutive logical workgroups are kept on one XCD, else 0
 };
 
 template <int G>
@@ -439,11 +441,9 @@ __global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_mfma_kernel(MfmaParams
   const uint32_t mask_lo = vgpr_constant(0x000f000fu);
   const uint32_t mask_hi = vgpr_constant(0x00f000f0u);
   const size_t stride = static_cast<size_t>(format_packet_stride(G, F));
-  const int grid = static_cast<int>(gridDim.x);
+  const int grid = p.grid;
   int b = static_cast<int>(blockIdx.x);
-  if (p.xcd_remap) {
-    b = (b & 7) * (grid >> 3) + (b >> 3);
-  }
+  b = p.xcd_remap != 0 ? (b & 7) * p.xcd_remap + (b >> 3) : b;
   // 32-bit unit arithmetic (the host keeps the unit count below 2^31): 64-bit divisions put
   // about 180 instructions ahead of the first weight load.
   const uint32_t ng = static_cast<uint32_t>(p.NG);
@@ -565,7 +565,8 @@ hipError_t launch_mfma_t(const GemvLaunch& l, hipStream_t stream) {
   p.max_contrib = l.max_contributors;
   const long long total = static_cast<long long>(p.tiles) * p.mtiles * p.NG;
   const int grid = static_cast<int>((total + p.per - 1) / p.per);
-  p.xcd_remap = (grid % 8 == 0) ? 1 : 0;
+  p.grid = grid;
+  p.xcd_remap = grid % 8 == 0 ? grid / 8 : 0;
   hipLaunchKernelGGL((w4a16_gemm_mfma_kernel<G, A, F>), dim3(grid), dim3(kThreads), 0, stream, p);
   return hipGetLastError();
 }

@@ -97,11 +97,9 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   const uint32_t mask_lo = vgpr_constant(0x000f000fu);
   const uint32_t mask_hi = vgpr_constant(0x00f000f0u);
   const size_t stride = static_cast<size_t>(format_packet_stride(G, F));
-  const int grid = static_cast<int>(gridDim.x);
+  const int grid = p.grid;
   int b = static_cast<int>(blockIdx.x);
-  if (p.xcd_remap) {
-    b = (b & 7) * (grid >> 3) + (b >> 3);
-  }
+  b = p.xcd_remap != 0 ? (b & 7) * p.xcd_remap + (b >> 3) : b;
   const int ng = p.NG;
   const int nbs = ng / Q;
   const int slices = p.N / kSliceCols;
@@ -391,7 +389,8 @@ hipError_t launch_mfma_stream_t(const GemvLaunch& l, hipStream_t stream) {
   p.pair = 0;
   p.stream_whole = l.stream_whole;
   grid = l.stream_grid;
-  p.xcd_remap = grid % 8 == 0 ? 1 : 0;
+  p.grid = grid;
+  p.xcd_remap = grid % 8 == 0 ? grid / 8 : 0;
   const size_t lds = mfma_stream_lds_bytes<G, MT>(l.K / G, kStreamWaves);
   if (l.stream_pieces) {
     hipLaunchKernelGGL((w4a16_gemm_mfma_stream_kernel<G, A, F, kStreamWaves, D, MT, true>),

@@ -106,7 +106,10 @@ struct GemvParams {
   int tiles, mtiles, splits, gps;  // kPartials: fixed split of every tile
   int per;                          // stream-K: group units per workgroup
   int max_contrib;                  // stream-K: partial slots per slice in the scratch
-  int xcd_remap;
+  // Workgroups of the launch, read with the other arguments (gridDim is a kernel argument of its
+  // own, and a second, dependent argument load at the start of every workgroup).
+  int grid;
+  int xcd_remap;  // grid / 8 when consecutive logical workgroups are kept on one XCD, else 0
   const uint16_t* norm_weight;      // RMSNorm prologue: gamma [K] (activation dtype), else null
   float eps;                        // RMSNorm prologue: epsilon
   int pair;                         // native slabs: each run streams two adjacent whole slices
@@ -566,11 +569,9 @@ w4a16_gemv_kernel(GemvParams p) {
   const size_t stride = static_cast<size_t>(format_packet_stride(G, F));
 
   // Logical workgroup id: keep consecutive ids (the contributors of one slice) on one XCD.
-  const int grid = static_cast<int>(gridDim.x);
+  const int grid = p.grid;
   int b = static_cast<int>(blockIdx.x);
-  if (p.xcd_remap) {
-    b = (b & 7) * (grid >> 3) + (b >> 3);
-  }
+  b = p.xcd_remap != 0 ? (b & 7) * p.xcd_remap + (b >> 3) : b;
 
   if constexpr (MODE == GemvMode::kPartials) {
     static_assert(CW == kTileCols, "the partials protocol runs on whole tiles");
@@ -647,7 +648,8 @@ hipError_t launch_t(const GemvLaunch& l, hipStream_t stream) {
     const long long total = static_cast<long long>(p.tiles) * (kTileCols / CW) * p.mtiles * p.NG;
     grid = static_cast<int>((total + p.per - 1) / p.per);
   }
-  p.xcd_remap = (grid % 8 == 0) ? 1 : 0;
+  p.grid = grid;
+  p.xcd_remap = grid % 8 == 0 ? grid / 8 : 0;
   hipLaunchKernelGGL((w4a16_gemv_kernel<G, A, MT, MODE, CW, F>), dim3(grid), dim3(kThreads), 0,
                      stream, p);
   return hipGetLastError();

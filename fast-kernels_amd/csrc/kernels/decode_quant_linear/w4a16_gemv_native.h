@@ -561,13 +561,11 @@ w4a16_gemv_native_kernel(GemvParams p) {
   const uint32_t mask_lo = vgpr_constant(0x000f000fu);
   const uint32_t mask_hi = vgpr_constant(0x00f000f0u);
   const size_t stride = static_cast<size_t>(format_packet_stride(G, F));
-  const int grid = static_cast<int>(gridDim.x);
+  const int grid = p.grid;
   if constexpr (kNorm) {
     }
   int b = static_cast<int>(blockIdx.x);
-  if (p.xcd_remap) {
-    b = (b & 7) * (grid >> 3) + (b >> 3);
-  }
+  b = p.xcd_remap != 0 ? (b & 7) * p.xcd_remap + (b >> 3) : b;
   const uint32_t total_units =
       static_cast<uint32_t>(p.tiles) * kSlicesPerTile * p.mtiles * p.NG;
   const uint32_t u_begin = static_cast<uint32_t>(b) * p.per;
@@ -626,7 +624,8 @@ GemvParams native_params(const GemvLaunch& l, int* grid) {
   p.pair = l.slice_pair ? 1 : 0;
   const long long total = static_cast<long long>(p.tiles) * kSlicesPerTile * p.mtiles * p.NG;
   *grid = p.per > 0 ? static_cast<int>((total + p.per - 1) / p.per) : 0;
-  p.xcd_remap = (*grid % 8 == 0) ? 1 : 0;
+  p.grid = *grid;
+  p.xcd_remap = *grid % 8 == 0 ? *grid / 8 : 0;
   return p;
 }
 

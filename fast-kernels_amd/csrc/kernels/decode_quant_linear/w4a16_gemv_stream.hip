@@ -91,12 +91,10 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   const uint32_t mask_lo = vgpr_constant(0x000f000fu);
   const uint32_t mask_hi = vgpr_constant(0x00f000f0u);
   const size_t stride = static_cast<size_t>(format_packet_stride(G, F));
-  const int grid = static_cast<int>(gridDim.x);
+  const int grid = p.grid;
   int b = static_cast<int>(blockIdx.x);
   // Consecutive logical workgroups on one XCD (the hardware deals workgroup b to XCD b % 8).
-  if (p.xcd_remap) {
-    b = (b & 7) * (grid >> 3) + (b >> 3);
-  }
+  b = p.xcd_remap != 0 ? (b & 7) * p.xcd_remap + (b >> 3) : b;
   const int ng = p.NG;
   constexpr int Q = kW * D;  // groups per block
   const int nbs = ng / Q;    // blocks per slice
@@ -387,7 +385,8 @@ hipError_t launch_stream_t(const GemvLaunch& l, hipStream_t stream) {
   p.pair = 0;
   grid = l.stream_grid;
   p.stream_whole = l.stream_whole;
-  p.xcd_remap = grid % 8 == 0 ? 1 : 0;
+  p.grid = grid;
+  p.xcd_remap = grid % 8 == 0 ? grid / 8 : 0;
   const size_t lds = static_cast<size_t>(MT) * stream_lds_bytes(G, l.K / G + 1);
   if constexpr (D != stream_depth_for_kb(G, kStreamKB)) {
     // the deeper pipeline serves half slices only (a half-slab is half the bytes)
