@@ -298,9 +298,33 @@ bool stream_pieces_enabled() {
 }
 
 
-// FK_W4A16_MFMA_STREAM=0 keeps 3-8-row native launches off the matrix-core stream kernel.
-constexpr int kMfmaStreamMinBatch = 3;
-constexpr int kMfmaStreamMaxBatch = 8;
+// FK_W4A16_STREAM_DIVISOR=0 keeps shapes whose slices divide only over fewer workgroups than
+// CUs off the stream schedule's divisor grids.
+bool stream_divisor_enabled() {
+  static const bool enabled = env_enabled("FK_W4A16_STREAM_DIVISOR");
+  return enabled;
+}
+
+// The largest grid of at least 7/8 of the CUs that divides more slices than CUs: every workgroup
+// then streams the same whole slices with no piece to hand off, the idle CUs costing less than
+// the pieces' imbalance (blocks do not divide evenly either) and hand-offs. 0 when there is none.
+long long divisor_grid(long long slices, long long cus) {
+  if (slices <= cus || !stream_divisor_enabled()) {
+    return 0;
+  }
+  for (long long g = cus; 8 * g >= 7 * cus; --g) {
+    if (slices % g == 0) {
+      return g;
+    }
+  }
+  return 0;
+}
+
+// FK_W4A16_MFMA_STREAM=0 keeps 2-16-row native launches off the matrix-core stream kernel.
+constexpr int kMfmaStreamMinBatch = 2;
+constexpr int kMfmaStreamMaxBatch = 16;
+constexpr int kMfmaPiecesMinBatch = 3;
+constexpr int kMfmaPiecesMaxBatch = 8;
 bool mfma_stream_enabled() {
   static const bool enabled = env_enabled("FK_W4A16_MFMA_STREAM");
   return enabled;
@@ -357,12 +381,13 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
       batch >= kMfmaStreamMinBatch && batch <= kMfmaStreamMaxBatch && kernel != kKernelDot2 &&
       mfma_stream_enabled()) {
     // The matrix cores on the stream schedule (w4a16_gemm_mfma_stream.hip): the rows staged whole
-    // in LDS, one workgroup per CU, pieces of the slices left over (as the one-row stream plan).
-    // Measured on MI355X (benchmark configuration 3, 14336 x 4096, G = 64, asymmetric, fp16;
-    // alternating runs on one GPU, against the automatic plan without it): 4 rows 12.8 -> 11.0-11.4
-    // us, 8 rows 13.0 -> 12.6 us; 2 rows 9.7 -> 10.8 us and 16 rows 13.0 -> 15.6 us are slower
-    // (two rows are cheaper on the dot2 loop; sixteen rows of K staged per workgroup are as many
-    // bytes as its weights), so it takes 3-8 rows.
+    // in LDS, one workgroup per CU streaming whole slices. Measured on MI355X (benchmark
+    // configuration 3, 14336 x 4096, G = 64, asymmetric, fp16: 448 slices, two per workgroup on a
+    // divisor grid of 224 CUs; alternating runs on one GPU against the plans without it): 2 rows
+    // 9.8 -> 8.6 us, 4 rows 10.9 -> 8.6, 8 rows 12.5 -> 10.0, 16 rows 13.0 -> 11.4. With pieces of
+    // the slices left over (256 CUs, a block of 32 groups the unit, so ranges of 1 or 2 blocks) the
+    // same shape took 11.0 us at 4 rows and 12.6 at 8, and two and sixteen rows were slower than
+    // without the stream schedule: pieces only for 3-8 rows.
     const std::size_t lds_limit = cu_count_given ? kGfx950LdsBytes : device_lds_per_block();
     const int depth = fk::stream_depth_for_kb(group_size, fk::kStreamKB);
     const int num_groups = k / group_size;
@@ -372,17 +397,22 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
     if (num_groups % (fk::kStreamWaves * depth) == 0 && fk::mfma_stream_fits(group_size, k, batch) &&
         fk::mfma_stream_lds(group_size, k, batch) <= lds_limit && slices <= fk::kStreamMaxSlices) {
       const long long left = slices % cus;
+      const long long dgrid = divisor_grid(slices, cus);
       long long grid = 0;
       int whole = 0;
       bool pieces = false;
       if (slices >= cus && left == 0) {
         grid = cus;
         whole = static_cast<int>(slices / cus);
-      } else if (slices > cus && left * nbs >= cus) {
+      } else if (dgrid > 0) {
+        grid = dgrid;
+        whole = static_cast<int>(slices / dgrid);
+      } else if (slices > cus && left * nbs >= cus && batch >= kMfmaPiecesMinBatch &&
+                 batch <= kMfmaPiecesMaxBatch) {
         grid = cus;
         whole = static_cast<int>(slices / cus);
         pieces = true;
-      } else if (slices < cus) {
+      } else if (slices < cus && batch >= kMfmaPiecesMinBatch && batch <= kMfmaPiecesMaxBatch) {
         grid = slices;
         whole = 1;
       }
@@ -458,6 +488,9 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
   //  * twice the slices a multiple of the CUs, up to kMaxHalvesPerCu half-slices per CU: an even
   //    share of half-slices, 4 KB of half-slabs in flight per wave (7B qkv, 3 per CU, 7.35 ->
   //    6.97 us against slice pairs; 8B gate_up, 7 per CU, 13.5 -> 13.9 us, stays on pairs);
+  //  * more slices than CUs with a divisor of them over at least 7/8 of the CUs: that many
+  //    workgroups of whole slices, no pieces (8B gate_up, 896 slices, 4 per CU on 224 CUs: 12.4 ->
+  //    11.4 us against slice pairs);
   //  * otherwise fewer slices than CUs and K too short to split (per == K/G): one whole slice per
   //    workgroup (8B qkv 5.16 -> 4.44 us, 7B o 4.67 -> 4.15). Pieces with no whole slice to hide
   //    their hand-off behind cost more than they save (8B o 4.8 -> 5.7 us), and 8B down as whole
@@ -488,6 +521,9 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
         grid = cus;
         whole = static_cast<int>(slices / cus);
         pieces = true;
+      } else if (const long long dgrid = divisor_grid(slices, cus); dgrid > 0) {
+        grid = dgrid;
+        whole = static_cast<int>(slices / dgrid);
       } else if (batch == 1 && group_size == 128 && 2 * slices > cus && (2 * slices) % cus == 0 &&
                  2 * slices <= kMaxHalvesPerCu * cus && stream_half_whole_enabled()) {
         grid = cus;

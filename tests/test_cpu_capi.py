@@ -217,7 +217,7 @@ def test_native_format_validation_without_gpu(lib: ctypes.CDLL) -> None:
         ((1, 10240, 8192, 128), (32, 80, 256, 2)),     # 70B qkv: 1 slice + a quarter slice per CU
         ((1, 10240, 4096, 128), (64, 32, 160, 1)),     # 320 slices in 160 pairs
         ((1, 12288, 4096, 128), (16, 96, 256, 2)),     # 7B qkv: 768 half-slices, 3 per CU
-        ((1, 28672, 4096, 128), (64, 32, 448, 1)),     # 8B gate_up: 896 slices in 448 pairs
+        ((1, 28672, 4096, 128), (32, 128, 224, 2)),    # 8B gate_up: 896 slices, 4 per CU on 224 CUs
         ((1, 12288, 8192, 128), (32, 96, 256, 2)),     # 1 slice + pieces of the 128 left over
         ((1, 22016, 4096, 128), (32, 32, 688, 0)),     # 7B gate_up: 344 pairs would fill 2 rounds unevenly
         ((2, 12288, 4096, 128), (32, 32, 384, 0)),     # pairs and stream for one row only
@@ -227,9 +227,12 @@ def test_native_format_validation_without_gpu(lib: ctypes.CDLL) -> None:
         ((1, 8192, 28672 + 128, 128), (32, 113, 510, 0)),  # 225 groups: not a multiple of 16
         ((1, 4096, 4096, 128), (16, 32, 256, 2)),      # 128 slices: a half slice per CU
         ((1, 4096, 14336, 128), (16, 112, 256, 2)),    # 128 slices of 112 groups: halves, whole K
-        ((4, 14336, 4096, 64), (32, 128, 256, 2)),     # four rows: 1 slice + pieces on the matrix cores
-        ((8, 14336, 4096, 64), (32, 128, 256, 2)),     # eight rows, the same stream plan
-        ((16, 14336, 4096, 64), (128, 16, 448, 0)),    # sixteen rows: matrix-core tiles
+        ((2, 14336, 4096, 64), (32, 128, 224, 2)),     # config 3: 448 slices, 2 per CU on 224 CUs
+        ((4, 14336, 4096, 64), (32, 128, 224, 2)),     # on the matrix cores, no pieces
+        ((8, 14336, 4096, 64), (32, 128, 224, 2)),     # eight rows, the same stream plan
+        ((16, 14336, 4096, 64), (32, 128, 224, 2)),    # sixteen rows, the same stream plan
+        ((4, 12288, 4096, 64), (32, 96, 256, 2)),      # 384 slices: 1 slice + pieces, 4 rows
+        ((16, 12288, 4096, 64), (128, 16, 384, 0)),    # the same at 16 rows: matrix-core tiles
     ],
 )
 def test_native_plan_policy_without_gpu(lib: ctypes.CDLL, shape, want) -> None:
@@ -266,14 +269,17 @@ def test_fused_entry_points_validate_without_gpu(lib: ctypes.CDLL) -> None:
 
 def test_kernel_choice_plans_without_gpu(lib: ctypes.CDLL) -> None:
     """FK_KERNEL_DOT2 keeps every batch on m-tiles of at most 8 rows, FK_KERNEL_MFMA puts every
-    batch on 16-row tiles (3-8 rows on the stream schedule over 32-column slices, others over
-    whole 128-column tiles), FK_KERNEL_AUTO is the forward's dispatch; another value is an
+    batch on 16-row tiles (on the stream schedule over 32-column slices where the slices divide
+    over 7/8 of the CUs or more, or 3-8 rows with pieces; others over whole 128-column tiles), FK_KERNEL_AUTO is the forward's dispatch; another value is an
     invalid argument."""
     lib.fk_last_error.restype = ctypes.c_char_p
-    for batch, kernel, want in [(16, 1, (8, 32)), (2, 2, (16, 128)), (2, 0, (2, 32)),
-                                (16, 0, (16, 128)), (4, 0, (16, 32)), (4, 2, (16, 32))]:
+    for batch, n, kernel, want in [(16, 14336, 1, (8, 32)), (2, 14336, 2, (16, 32)),
+                                   (2, 14336, 0, (16, 32)), (16, 14336, 0, (16, 32)),
+                                   (4, 14336, 0, (16, 32)), (4, 14336, 2, (16, 32)),
+                                   (2, 12288, 0, (2, 32)), (2, 12288, 2, (16, 128)),
+                                   (16, 12288, 0, (16, 128))]:
         p = Plan()
-        assert lib.fk_w4a16_plan_for_kernel(batch, 14336, 4096, 64, 0, 0, 256, 1, kernel,
+        assert lib.fk_w4a16_plan_for_kernel(batch, n, 4096, 64, 0, 0, 256, 1, kernel,
                                             ctypes.byref(p)) == 0
         assert (p.m_tile, p.slice_cols) == want, (batch, kernel)
     p = Plan()

@@ -224,7 +224,6 @@ def test_config2_layer_graph_replays_match_eager() -> None:
         # pieces of the slices left over past whole ones per CU, finished through the workspace
         (10240, 8192, 128, "bf16", False, 1),  # 1 slice + a quarter of one per CU
         (12288, 8192, 128, "f16", True, 1),    # 1 slice + a head and a tail piece (1.5 blocks)
-        (28672, 8192, 128, "bf16", False, 1),  # 3 slices + a half
         (12288, 4096, 64, "bf16", False, 1),   # G = 64: halves of 64 groups
         (10240, 16384, 64, "f16", True, 1),    # G = 64: quarters of 256 groups
         (22016, 8192, 128, "f16", True, 1),    # ranges of 1 or 2 blocks over 176 slices
@@ -235,6 +234,9 @@ def test_config2_layer_graph_replays_match_eager() -> None:
         (12288, 4096, 128, "bf16", True, 1),   # 768 half-slices, 3 per CU (7B qkv)
         (16384, 4096, 128, "f16", False, 1),   # 1024 half-slices, 4 per CU
         (6144, 4096, 128, "f16", False, 1),  # one slice per workgroup, 192 workgroups
+        # more slices than CUs, a divisor of them over at least 7/8 of the CUs: whole slices only
+        (28672, 8192, 128, "bf16", False, 1),  # 896 slices: 4 per workgroup on 224 CUs
+        (28672, 4096, 128, "bf16", True, 1),   # 8B gate_up, asymmetric
     ],
 )
 def test_stream_schedule_variants(n: int, k: int, g: int, act: str, asym: bool, m: int) -> None:
@@ -270,6 +272,10 @@ def test_stream_schedule_variants(n: int, k: int, g: int, act: str, asym: bool, 
         (7, 6144, 4096, 128, "f16", False),    # 192 slices: one per workgroup, an odd batch
         (5, 8192, 4096, 128, "bf16", False),   # eight-row staging, G = 128
         (8, 14336, 4096, 64, "bf16", True),    # configuration 3's shape in bf16, eight rows
+        # 448 slices: two per workgroup on 224 of the CUs, no pieces, 2 to 16 rows
+        (2, 14336, 4096, 64, "f16", True),     # configuration 3, two rows
+        (16, 14336, 4096, 64, "f16", True),    # configuration 3, sixteen rows
+        (13, 14336, 4096, 128, "bf16", False),  # sixteen-row staging at G = 128, an odd batch
     ],
 )
 def test_mfma_stream_variants(m: int, n: int, k: int, g: int, act: str, asym: bool) -> None:
