@@ -34,7 +34,8 @@ namespace {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
-// LDS of the MFMA stream kernel: xs [NG][G/8][MT] paired activation words (row fastest),
+// LDS of the MFMA stream kernel: xs [NG][G/8][MT] paired activation words (row fastest, the row
+// slot swizzled by the word row: see xs_slot),
 // sums [NG][MT] {-1024 S_e - 64 S_o, S_e + S_o}, scale [NG][MT] bf16 staging scales, then the
 // reduction slot red [kW][MT][32].
 template <int G, int MT>
@@ -49,6 +50,17 @@ template <int G, int MT>
 __host__ __device__ constexpr size_t mfma_stream_lds_bytes(int ng, int waves) {
   return static_cast<size_t>(ng) * MT * ((G / 8) * 16 + 8 + 4) +
          static_cast<size_t>(waves) * MT * kSliceCols * 4;
+}
+
+// Slot of row m in word row wr of xs. The staging's consecutive lanes store one row's
+// consecutive word rows, MT * 16 bytes apart, which with MT slots per word row put 4-8 of every
+// 8 lanes' 16-byte stores in the same banks; the row xor a function of the word row spreads
+// them over distinct 16-byte slots of each 128 bytes (MT >= 8: wr mod 8; MT = 4: two word rows
+// per 128 bytes, so (wr / 2) mod 4). The compute's reads (16 rows of one word row per 16 lanes)
+// stay conflict-free: xor is a permutation of the word row's slots.
+template <int MT>
+__device__ __forceinline__ int xs_slot(int wr, int m) {
+  return m ^ (MT >= 8 ? (wr & 7) : ((wr >> 1) & (MT - 1)));
 }
 
 // Code word -> 8 fp16 values in the slot order (k0,k4)(k1,k5)(k2,k6)(k3,k7): 1024 + q for even
@@ -218,13 +230,14 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     native_load<G, F>(buf[d], slab(d), lane);
     __builtin_amdgcn_sched_barrier(0);
   }
-  // Convert and store: rows past the batch stage zeros; a pass past the wave's last group stores
-  // that group's values again.
+  // Convert and store: rows past the batch stage zeros (a mask, not a branch); a pass past the
+  // wave's last group stores that group's values again.
 #pragma unroll
   for (int i = 0; i < kStage; ++i) {
     const int g = wave + kW * pass_group(i);
     const int m = pass_row(i);
-    uint4 v = m < rows ? raw[i] : make_uint4(0u, 0u, 0u, 0u);
+    const uint32_t keep = m < rows ? 0xffffffffu : 0u;
+    uint4 v = make_uint4(raw[i].x & keep, raw[i].y & keep, raw[i].z & keep, raw[i].w & keep);
     float undo = 1.0f;
     if constexpr (A == Act::kBF16) {
       const uint32_t e = group_max<WR>(bf16_max_mag(v)) >> 7;
@@ -243,10 +256,12 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     float so = dot2<Act::kF16>(xp.w, kOnes, dot2<Act::kF16>(xp.y, kOnes, 0.0f));
     se = group_sum<WR>(se);
     so = group_sum<WR>(so);
-    sm.xs[(g * WR + wr) * MT + m] = xp;
+    sm.xs[(g * WR + wr) * MT + xs_slot<MT>(wr, m)] = xp;
     // every lane of the (group, row) holds the same values and writes them (no branch)
     sm.sums[g * MT + m] = make_float2(fmaf(-1024.0f, se, -64.0f * so), se + so);
-    sm.scale[g * MT + m] = undo;
+    if constexpr (A == Act::kBF16) {
+      sm.scale[g * MT + m] = undo;
+    }
   }
   // The wave reads back only what it wrote (its LDS accesses complete in order); the fences keep
   // the compiler from hoisting the reads.
@@ -267,7 +282,8 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     half8_t a[U];
 #pragma unroll
     for (int j = 0; j < U; ++j) {
-      const uint4 xv = sm.xs[(static_cast<size_t>(gl) * WR + U * t + j) * MT + min(n, MT - 1)];
+      const uint4 xv = sm.xs[(static_cast<size_t>(gl) * WR + U * t + j) * MT +
+                             xs_slot<MT>(U * t + j, min(n, MT - 1))];
       a[j] = __builtin_bit_cast(half8_t, n < MT ? xv : make_uint4(0u, 0u, 0u, 0u));
     }
     float4_t seed;
@@ -281,7 +297,7 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
       s[r] = live ? v.y : 0.0f;
       const float c = F == PacketFormat::kNativeSym ? fmaf(-8.0f, v.y, v.x) : v.x;
       seed[r] = live ? c : 0.0f;
-      sc[r] = sm.scale[gl * MT + row];
+      sc[r] = A == Act::kBF16 ? sm.scale[gl * MT + row] : 1.0f;
     }
     uint32_t beta_pair = 0;
     if constexpr (F == PacketFormat::kNativeAsym) {
