@@ -97,7 +97,10 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   b = p.xcd_remap != 0 ? (b & 7) * p.xcd_remap + (b >> 3) : b;
   const int ng = p.NG;
   constexpr int Q = kW * D;  // groups per block
-  const int nbs = ng / Q;    // blocks per slice
+  // Blocks per slice. Half slices may have a group count that is not a multiple of Q: the last
+  // block's groups past the slice re-read its last slab and compute against the spare group slot
+  // of the staged row, which holds zeros, so they add nothing.
+  const int nbs = (ng + Q - 1) / Q;
   constexpr int kOut = MT * kSliceCols;  // outputs of a slice
   constexpr int kOutPerLane = (kOut + 63) / 64;
 
@@ -190,7 +193,8 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
       const int hs = hs0 + r;
       const int jj = c - r * spr;
       native_load_half<G, F>(
-          ld, p.packets + static_cast<size_t>(static_cast<uint32_t>((hs >> 1) * ng + wave + kW * jj)) *
+          ld, p.packets + static_cast<size_t>(static_cast<uint32_t>((hs >> 1) * ng +
+                                                                    min(wave + kW * jj, ng - 1))) *
                               stride,
           lane, hs & 1);
     } else {
@@ -202,7 +206,7 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   // (lane l, word row l % WR) of every row.
   constexpr int WR = G / 8;
   constexpr int kGroupsPerPass = 64 / WR;
-  const int n_pass = (ng / kW + kGroupsPerPass - 1) / kGroupsPerPass;
+  const int n_pass = (nbs * D + kGroupsPerPass - 1) / kGroupsPerPass;
   uint4 raw[kStageSlots][MT];
 #pragma unroll
   for (int i = 0; i < kStageSlots; ++i) {
@@ -226,12 +230,16 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   // Stages the next pass from raw[0] and shifts the slots down (register moves; a runtime slot
   // index would put the slots in scratch memory).
   auto stage_one = [&]() {
-    // Groups past the row (the wave's last pass may be partial) are staged into the spare group
+    // Groups past the row (the wave's last pass may be partial) stage zeros into the spare group
     // slot past the row's, so the staging has no branch.
-    const int g = min(wave + kW * (staged * kGroupsPerPass + lane / WR), ng);
+    const int g_raw = wave + kW * (staged * kGroupsPerPass + lane / WR);
+    const int g = min(g_raw, ng);
+    const uint32_t keep = g_raw < ng ? 0xffffffffu : 0u;
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-      native_stage_unit<G, A, F>(sm, raw[0][m], m, g, lane % WR);
+      const uint4 v = raw[0][m];
+      native_stage_unit<G, A, F>(sm, make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep),
+                                 m, g, lane % WR);
     }
 #pragma unroll
     for (int i = 0; i + 1 < kStageSlots; ++i) {
@@ -267,7 +275,8 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   auto block = [&](int gl0) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      native_compute_group<G, A, MT, F, StreamLds<G>, kHalf ? 1 : 2>(sm, buf[d], gl0 + kW * d, t,
+      native_compute_group<G, A, MT, F, StreamLds<G>, kHalf ? 1 : 2>(sm, buf[d],
+                                                                     min(gl0 + kW * d, ng), t,
                                                                      mask_lo, mask_hi, y, half);
       load_slab(buf[d], j + d + D);
       // Issue the refill here, not after the block's later slabs: the scheduler would otherwise
@@ -474,9 +483,11 @@ hipError_t launch_w4a16_gemv_stream(const GemvLaunch& l, hipStream_t stream) {
   // Blocks of waves * depth groups. Half slices: G = 128, one row, two workgroups per slice.
   // Pieces: the workspace to finish the split slices. Else whole slices, the same count per
   // workgroup.
+  // Whole blocks of waves * depth groups per slice, except half slices (whose last block may be
+  // partial).
   const int ng = l.K / l.group_size;
   const int quantum = l.stream_waves * l.stream_depth;
-  if (ng % quantum != 0) {
+  if (ng % quantum != 0 && !l.stream_half) {
     return hipErrorInvalidValue;
   }
   const long long slices = l.N / kSliceCols;

@@ -507,21 +507,24 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
     const int depth = fk::stream_depth_for_kb(group_size, fk::kStreamKB);
     const int nbs = num_groups / (fk::kStreamWaves * depth);  // blocks per slice
     const long long cus = static_cast<long long>(cu_count) * stream_workgroups_per_cu();
-    if (num_groups % (fk::kStreamWaves * depth) == 0 && lds <= lds_limit) {
+    // Whole blocks per slice, except for half slices, whose last block may be partial (7B down,
+    // K/G = 86: 7.4 -> 7.0 us against runs split over K).
+    const bool exact = num_groups % (fk::kStreamWaves * depth) == 0;
+    if (nbs >= 1 && lds <= lds_limit) {
       long long grid = 0;
       int whole = 0;
       bool pieces = false;
       bool half = false;
       const long long left = slices % cus;
-      if (slices >= cus && left == 0) {
+      if (exact && slices >= cus && left == 0) {
         grid = cus;
         whole = static_cast<int>(slices / cus);
-      } else if (slices > cus && left * nbs >= cus && num_groups >= kMinPieceGroups &&
+      } else if (exact && slices > cus && left * nbs >= cus && num_groups >= kMinPieceGroups &&
                  slices <= fk::kStreamMaxSlices && stream_pieces_enabled()) {
         grid = cus;
         whole = static_cast<int>(slices / cus);
         pieces = true;
-      } else if (const long long dgrid = divisor_grid(slices, cus); dgrid > 0) {
+      } else if (const long long dgrid = exact ? divisor_grid(slices, cus) : 0; dgrid > 0) {
         grid = dgrid;
         whole = static_cast<int>(slices / dgrid);
       } else if (batch == 1 && group_size == 128 && 2 * slices > cus && (2 * slices) % cus == 0 &&
@@ -533,7 +536,7 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
         grid = 2 * slices;
         whole = 1;
         half = true;
-      } else if (slices < cus && per == num_groups && stream_small_enabled()) {
+      } else if (exact && slices < cus && per == num_groups && stream_small_enabled()) {
         grid = slices;
         whole = 1;
       }

@@ -224,7 +224,10 @@ def test_native_format_validation_without_gpu(lib: ctypes.CDLL) -> None:
         ((4, 12288, 4096, 128), (32, 48, 256, 2)),     # four rows: matrix cores on the stream schedule
         ((1, 57344, 8192, 128), (32, 448, 256, 2)),    # 70B gate_up: 7 whole slices per CU
         ((1, 8192, 28672, 128), (32, 224, 256, 2)),    # 70B down: one slice of 224 groups per CU
-        ((1, 8192, 28672 + 128, 128), (32, 113, 510, 0)),  # 225 groups: not a multiple of 16
+        ((1, 8192, 28672 + 128, 128), (16, 450, 256, 2)),  # 225 groups: 2 half slices per CU,
+                                                           # the last block of each partial
+        ((1, 4096, 11008, 128), (16, 86, 256, 2)),     # 7B down, 86 groups: a half slice per CU
+        ((1, 4096, 1920, 128), (32, 15, 128, 0)),      # 15 groups: less than one block, runs
         ((1, 4096, 4096, 128), (16, 32, 256, 2)),      # 128 slices: a half slice per CU
         ((1, 4096, 14336, 128), (16, 112, 256, 2)),    # 128 slices of 112 groups: halves, whole K
         ((2, 14336, 4096, 64), (32, 128, 224, 2)),     # config 3: 448 slices, 2 per CU on 224 CUs

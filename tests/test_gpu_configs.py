@@ -234,6 +234,9 @@ def test_config2_layer_graph_replays_match_eager() -> None:
         (12288, 4096, 128, "bf16", True, 1),   # 768 half-slices, 3 per CU (7B qkv)
         (16384, 4096, 128, "f16", False, 1),   # 1024 half-slices, 4 per CU
         (6144, 4096, 128, "f16", False, 1),  # one slice per workgroup, 192 workgroups
+        # half slices whose last block is partial (K/G not a multiple of 16)
+        (4096, 11008, 128, "f16", False, 1),   # 7B down: 86 groups
+        (8192, 28800, 128, "bf16", True, 1),   # 225 groups, two half slices per CU
         # more slices than CUs, a divisor of them over at least 7/8 of the CUs: whole slices only
         (28672, 8192, 128, "bf16", False, 1),  # 896 slices: 4 per workgroup on 224 CUs
         (28672, 4096, 128, "bf16", True, 1),   # 8B gate_up, asymmetric
