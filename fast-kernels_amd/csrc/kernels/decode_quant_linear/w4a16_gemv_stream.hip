@@ -76,10 +76,11 @@ struct StreamLds {
 // (slabs in flight) per wave, MT activation rows; one workgroup per CU. kStageSlots passes of
 // 64 / (G / 8) groups per wave stage K <= kStageSlots * 64 * kW * 8 activations.
 template <int G, Act A, PacketFormat F, int kStageSlots, int kW, int D, int MT, bool kPieces,
-          bool kHalf>
+          bool kHalf, bool kRagged = false>
 __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     w4a16_gemv_stream_kernel(GemvParams p) {
   static_assert(!kHalf || (MT == 1 && !kPieces && G == 128), "half slices: one row, no pieces");
+  static_assert(!kRagged || kHalf, "a partial last block: half slices only");
   extern __shared__ uint4 stream_lds[];
   // Wave totals: slots 0 and 1 for the pieces, then two rounds of kRing whole slices.
   constexpr int kRing = 4;
@@ -97,10 +98,14 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   b = p.xcd_remap != 0 ? (b & 7) * p.xcd_remap + (b >> 3) : b;
   const int ng = p.NG;
   constexpr int Q = kW * D;  // groups per block
-  // Blocks per slice. Half slices may have a group count that is not a multiple of Q: the last
+  // Blocks per slice. kRagged (half slices whose group count is not a multiple of Q): the last
   // block's groups past the slice re-read its last slab and compute against the spare group slot
-  // of the staged row, which holds zeros, so they add nothing.
-  const int nbs = (ng + Q - 1) / Q;
+  // of the staged row, which holds zeros, so they add nothing. The clamps this takes cost the
+  // other shapes 0.1-0.6 us, so they are compiled in only there.
+  const int nbs = kRagged ? (ng + Q - 1) / Q : ng / Q;
+  // slice-local group g clamped into the slice (kRagged), for the weights and the staged row
+  auto clamp_w = [&](int g) { return kRagged ? min(g, ng - 1) : g; };
+  auto clamp_x = [&](int g) { return kRagged ? min(g, ng) : g; };
   constexpr int kOut = MT * kSliceCols;  // outputs of a slice
   constexpr int kOutPerLane = (kOut + 63) / 64;
 
@@ -194,7 +199,7 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
       const int jj = c - r * spr;
       native_load_half<G, F>(
           ld, p.packets + static_cast<size_t>(static_cast<uint32_t>((hs >> 1) * ng +
-                                                                    min(wave + kW * jj, ng - 1))) *
+                                                                    clamp_w(wave + kW * jj))) *
                               stride,
           lane, hs & 1);
     } else {
@@ -230,16 +235,18 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   // Stages the next pass from raw[0] and shifts the slots down (register moves; a runtime slot
   // index would put the slots in scratch memory).
   auto stage_one = [&]() {
-    // Groups past the row (the wave's last pass may be partial) stage zeros into the spare group
-    // slot past the row's, so the staging has no branch.
+    // Groups past the row (the wave's last pass may be partial) go to the spare group
+    // slot past the row's (zeros with kRagged, which reads it), so the staging has no branch.
     const int g_raw = wave + kW * (staged * kGroupsPerPass + lane / WR);
     const int g = min(g_raw, ng);
-    const uint32_t keep = g_raw < ng ? 0xffffffffu : 0u;
+    const uint32_t keep = !kRagged || g_raw < ng ? 0xffffffffu : 0u;
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-      const uint4 v = raw[0][m];
-      native_stage_unit<G, A, F>(sm, make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep),
-                                 m, g, lane % WR);
+      uint4 v = raw[0][m];
+      if constexpr (kRagged) {
+        v = make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep);
+      }
+      native_stage_unit<G, A, F>(sm, v, m, g, lane % WR);
     }
 #pragma unroll
     for (int i = 0; i + 1 < kStageSlots; ++i) {
@@ -276,7 +283,7 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       native_compute_group<G, A, MT, F, StreamLds<G>, kHalf ? 1 : 2>(sm, buf[d],
-                                                                     min(gl0 + kW * d, ng), t,
+                                                                     clamp_x(gl0 + kW * d), t,
                                                                      mask_lo, mask_hi, y, half);
       load_slab(buf[d], j + d + D);
       // Issue the refill here, not after the block's later slabs: the scheduler would otherwise
@@ -403,8 +410,15 @@ hipError_t launch_stream_t(const GemvLaunch& l, hipStream_t stream) {
       if (!l.stream_half || l.stream_pieces) {
         return hipErrorInvalidValue;
       }
-      hipLaunchKernelGGL((w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, 1, false, true>),
-                         dim3(grid), dim3(64 * kW), lds, stream, p);
+      if ((l.K / G) % (kW * D) != 0) {
+        hipLaunchKernelGGL(
+            (w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, 1, false, true, true>),
+            dim3(grid), dim3(64 * kW), lds, stream, p);
+      } else {
+        hipLaunchKernelGGL(
+            (w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, 1, false, true>),
+            dim3(grid), dim3(64 * kW), lds, stream, p);
+      }
       return hipGetLastError();
     } else {
       return hipErrorInvalidValue;
@@ -415,8 +429,15 @@ hipError_t launch_stream_t(const GemvLaunch& l, hipStream_t stream) {
                        dim3(grid), dim3(64 * (kW + 1)), lds, stream, p);
   } else if (l.stream_half) {
     if constexpr (G == 128 && MT == 1) {
-      hipLaunchKernelGGL((w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, 1, false, true>),
-                         dim3(grid), dim3(64 * kW), lds, stream, p);
+      if ((l.K / G) % (kW * D) != 0) {
+        hipLaunchKernelGGL(
+            (w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, 1, false, true, true>),
+            dim3(grid), dim3(64 * kW), lds, stream, p);
+      } else {
+        hipLaunchKernelGGL(
+            (w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, 1, false, true>),
+            dim3(grid), dim3(64 * kW), lds, stream, p);
+      }
     } else {
       return hipErrorInvalidValue;
     }
