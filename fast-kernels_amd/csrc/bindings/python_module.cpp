@@ -340,6 +340,7 @@ PYBIND11_MODULE(_native, m) {
         d["max_tile_contributors"] = plan.max_tile_contributors;
         d["workspace_bytes"] = plan.workspace_bytes;
         d["slice_cols"] = plan.slice_cols;
+        d["schedule"] = plan.schedule;
         return d;
       },
       py::arg("batch"), py::arg("n"), py::arg("k"), py::arg("group_size"),

@@ -76,9 +76,10 @@ constexpr int kStreamKB = 4;
 constexpr int stream_depth_for_kb(int group_size, int kb) { return kb / (group_size == 128 ? 2 : 1); }
 // Most 32-column slices a stream launch with pieces may have (one arrival counter each).
 constexpr int kStreamMaxSlices = 16384;
-// Static LDS of the stream kernel besides the dynamic part: two reduction slots of 8 waves x
-// rows x 32 floats, per activation row.
-constexpr size_t kStreamStaticLdsBytes = 2 * 8 * 32 * sizeof(float);
+// Static LDS of the stream kernel besides the dynamic part, per activation row: ten reduction
+// slots (two for pieces, a ring of eight for whole slices) of 8 waves x 32 floats, and the 8
+// waves' RMS partial sums.
+constexpr size_t kStreamStaticLdsBytes = (10 * 8 * 32 + 8) * sizeof(float);
 // Workspace floats of a stream launch with pieces: two partial slots of rows x 32 per workgroup
 // (the matrix-core stream kernel's slots hold 16 rows whatever the batch).
 inline size_t stream_partial_floats(int grid, int rows) {

@@ -75,16 +75,29 @@ struct StreamLds {
 // kW streaming waves per workgroup (plus the control wave with kPieces), D register buffers
 // (slabs in flight) per wave, MT activation rows; one workgroup per CU. kStageSlots passes of
 // 64 / (G / 8) groups per wave stage K <= kStageSlots * 64 * kW * 8 activations.
+//
+// kFuse (one row, whole slices, no pieces): kRmsNorm stages round(gamma * round(x * inv_rms))
+// with inv_rms = 1 / sqrt(mean(x^2) + eps) of the row, formed per workgroup from the staging
+// loads it issues anyway (each wave's sum over its own groups, one barrier). kSiluMul: the weight
+// is [W_gate; W_up] stacked along N, and workgroup b streams the gate slices b * whole .. and then
+// the same up slices (slice + N / 64), keeps all their totals in the LDS ring, and writes
+// round(round(silu(round(g))) * round(u)) to out[N / 2] (the unfused GEMV, SiLU and product, each
+// rounded to the activation dtype). kRmsNormSiluMul: both.
 template <int G, Act A, PacketFormat F, int kStageSlots, int kW, int D, int MT, bool kPieces,
-          bool kHalf, bool kRagged = false>
+          bool kHalf, bool kRagged = false, GemvFuse kFuse = GemvFuse::kNone>
 __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     w4a16_gemv_stream_kernel(GemvParams p) {
   static_assert(!kHalf || (MT == 1 && !kPieces && G == 128), "half slices: one row, no pieces");
   static_assert(!kRagged || kHalf, "a partial last block: half slices only");
+  constexpr bool kNorm = kFuse == GemvFuse::kRmsNorm || kFuse == GemvFuse::kRmsNormSiluMul;
+  constexpr bool kSilu = kFuse == GemvFuse::kSiluMul || kFuse == GemvFuse::kRmsNormSiluMul;
+  static_assert(kFuse == GemvFuse::kNone || (MT == 1 && !kPieces && !kHalf),
+                "fused: one row over whole slices");
   extern __shared__ uint4 stream_lds[];
   // Wave totals: slots 0 and 1 for the pieces, then two rounds of kRing whole slices.
   constexpr int kRing = 4;
   __shared__ float red[2 + 2 * kRing][kW][MT * kSliceCols];
+  __shared__ float rms_part[kW];
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -111,6 +124,9 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
 
   const int slices = p.N / kSliceCols;
   StreamRange rg = stream_range(b, grid, p.stream_whole, slices, nbs, kPieces);
+  if constexpr (kSilu) {
+    rg.whole_slice0 = b * (p.stream_whole / 2);  // gate slices (whole / 2 of them), then up
+  }
   // kHalf: half-slices hs0 .. hs0 + whole - 1, half-slice hs being half hs & 1 of slice hs / 2.
   const int hs0 = kHalf ? b * p.stream_whole : 0;
   int half = 0;
@@ -172,6 +188,9 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   // Slab index of the wave's i-th slab: i * kW plus a per-part offset (uniform 32-bit arithmetic;
   // selects of 64-bit addresses compile to branches).
   const int off_w = rg.whole_slice0 * ng + wave - (n_h + n_t) * kW;
+  // kSilu: the first half of the range is the gate slices, the second the same up slices
+  const int n_gate = kSilu ? rg.whole / 2 * nbs * D : 0;
+  const int off_up = (rg.whole_slice0 + slices / 2) * ng + wave - n_gate * kW;
   const int off_t = rg.tail_slice * ng + wave - n_h * kW;
   const int off_h = rg.head_slice * ng + rg.head_blk0 * Q + wave;
   auto slab = [&](int i) -> const uint8_t* {
@@ -185,6 +204,10 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
       in_t = __builtin_amdgcn_readfirstlane(in_t);
       in_h = __builtin_amdgcn_readfirstlane(in_h);
       off += in_t * (off_t - off_w) + in_h * (off_h - off_t);
+    }
+    if constexpr (kSilu) {
+      const int in_up = __builtin_amdgcn_readfirstlane(c >= n_gate ? 1 : 0);
+      off += in_up * (off_up - off_w);
     }
     return p.packets + static_cast<size_t>(static_cast<uint32_t>(c * kW + off)) * stride;
   };
@@ -224,12 +247,56 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
                                                   static_cast<size_t>(g) * G + (lane % WR) * 8);
     }
   }
+  // kNorm: gamma of the same units (one row of K for all rows)
+  uint4 gam[kNorm ? kStageSlots : 1];
+  if constexpr (kNorm) {
+#pragma unroll
+    for (int i = 0; i < kStageSlots; ++i) {
+      const int g = min(wave + kW * (i * kGroupsPerPass + lane / WR), ng - 1);
+      gam[i] = *reinterpret_cast<const uint4*>(p.norm_weight + static_cast<size_t>(g) * G +
+                                               (lane % WR) * 8);
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
   NativeLoad<G> buf[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
     load_slab(buf[d], d);
     __builtin_amdgcn_sched_barrier(0);  // the same issue order as the refills in the loop
+  }
+  // kNorm: 1 / sqrt(mean(x^2) + eps) of the row (fp32 sums). Every unit of the row is in exactly
+  // one lane's staging registers (slots of the wave's passes, groups inside the row), so the
+  // waves' sums add up to the row's; the weights' loads are in flight meanwhile.
+  float inv_rms = 1.0f;
+  if constexpr (kNorm) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kStageSlots; ++i) {
+      const bool live = i < n_pass && wave + kW * (i * kGroupsPerPass + lane / WR) < ng;
+      float si = 0.0f;
+      si = sum_sq_word<A>(raw[i][0].x, si);
+      si = sum_sq_word<A>(raw[i][0].y, si);
+      si = sum_sq_word<A>(raw[i][0].z, si);
+      si = sum_sq_word<A>(raw[i][0].w, si);
+      ss += live ? si : 0.0f;
+    }
+    // the wave's total: DPP within each 16-lane row, then the four rows' lanes 0 read out (a
+    // shuffle per step would be an LDS round trip)
+    ss = group_sum<16>(ss);
+    ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ss), 0)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ss), 16)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ss), 32)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ss), 48));
+    if (lane == 0) {
+      rms_part[wave] = ss;
+    }
+    lds_barrier();
+    float total = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kW; ++w) {
+      total += rms_part[w];
+    }
+    inv_rms = 1.0f / sqrtf(total / static_cast<float>(p.K) + p.eps);
   }
   int staged = 0;
   // Stages the next pass from raw[0] and shifts the slots down (register moves; a runtime slot
@@ -246,6 +313,11 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
       if constexpr (kRagged) {
         v = make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep);
       }
+      if constexpr (kNorm) {
+        const uint4 gw = gam[0];
+        v = make_uint4(norm_pair<A>(v.x, gw.x, inv_rms), norm_pair<A>(v.y, gw.y, inv_rms),
+                       norm_pair<A>(v.z, gw.z, inv_rms), norm_pair<A>(v.w, gw.w, inv_rms));
+      }
       native_stage_unit<G, A, F>(sm, v, m, g, lane % WR);
     }
 #pragma unroll
@@ -253,6 +325,9 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
         raw[i][m] = raw[i + 1][m];
+      }
+      if constexpr (kNorm) {
+        gam[i] = gam[i + 1];
       }
     }
     ++staged;
@@ -364,6 +439,32 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     // the last) lets all waves write the round's outputs at once, adding the waves' totals in wave
     // order. Rounds alternate between two sets of slots: a wave writes a set again only after the
     // next round's barrier, which every wave reaches after reading it.
+    if constexpr (kSilu) {
+      // every slice's totals stay in the ring (2 * whole <= 2 * kRing slots); one barrier after
+      // the last, then the gate and up totals of each output
+      fold(2 + r);
+      if (r == rg.whole - 1) {
+        lds_barrier();
+        const int pairs = rg.whole / 2;
+        for (int o = tid; o < pairs * kSliceCols; o += 64 * kW) {
+          const int rr = o / kSliceCols;
+          const int c = o % kSliceCols;
+          float gv = red[2 + rr][0][c];
+          float uv = red[2 + pairs + rr][0][c];
+#pragma unroll
+          for (int w = 1; w < kW; ++w) {
+            gv += red[2 + rr][w][c];
+            uv += red[2 + pairs + rr][w][c];
+          }
+          const float gr = act_bits_to_float<A>(float_to_act_bits<A>(gv));
+          const float ur = act_bits_to_float<A>(float_to_act_bits<A>(uv));
+          const float sg = act_bits_to_float<A>(float_to_act_bits<A>(gr / (1.0f + expf(-gr))));
+          p.out[static_cast<size_t>(rg.whole_slice0 + rr) * kSliceCols + c] =
+              float_to_act_bits<A>(sg * ur);
+        }
+      }
+      continue;
+    }
     const int in_round = r % kRing;
     fold(2 + r % (2 * kRing));
     if (in_round == kRing - 1 || r == rg.whole - 1) {
@@ -404,6 +505,33 @@ hipError_t launch_stream_t(const GemvLaunch& l, hipStream_t stream) {
   p.grid = grid;
   p.xcd_remap = grid % 8 == 0 ? grid / 8 : 0;
   const size_t lds = static_cast<size_t>(MT) * stream_lds_bytes(G, l.K / G + 1);
+  if (l.fuse != GemvFuse::kNone) {
+    if constexpr (MT == 1 && D == stream_depth_for_kb(G, kStreamKB)) {
+      if (l.stream_pieces || l.stream_half) {
+        return hipErrorInvalidValue;
+      }
+      switch (l.fuse) {
+        case GemvFuse::kRmsNorm:
+          hipLaunchKernelGGL((w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, 1, false, false,
+                                                       false, GemvFuse::kRmsNorm>),
+                             dim3(grid), dim3(64 * kW), lds, stream, p);
+          break;
+        case GemvFuse::kSiluMul:
+          hipLaunchKernelGGL((w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, 1, false, false,
+                                                       false, GemvFuse::kSiluMul>),
+                             dim3(grid), dim3(64 * kW), lds, stream, p);
+          break;
+        default:
+          hipLaunchKernelGGL((w4a16_gemv_stream_kernel<G, A, F, kStageSlots, kW, D, 1, false, false,
+                                                       false, GemvFuse::kRmsNormSiluMul>),
+                             dim3(grid), dim3(64 * kW), lds, stream, p);
+          break;
+      }
+      return hipGetLastError();
+    } else {
+      return hipErrorInvalidValue;
+    }
+  }
   if constexpr (D != stream_depth_for_kb(G, kStreamKB)) {
     // the deeper pipeline serves half slices only (a half-slab is half the bytes)
     if constexpr (G == 128 && MT == 1) {
@@ -496,22 +624,29 @@ hipError_t stream_dispatch(const GemvLaunch& l, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_w4a16_gemv_stream(const GemvLaunch& l, hipStream_t stream) {
-  if (l.mode != GemvMode::kStreamK || l.m_tile != l.M || l.fuse != GemvFuse::kNone ||
-      l.slice_cols != kSliceCols || l.slice_pair || l.K > kStreamMaxK || l.stream_depth <= 0 ||
-      l.stream_grid <= 0) {
+  if (l.mode != GemvMode::kStreamK || l.m_tile != l.M || l.slice_cols != kSliceCols ||
+      l.slice_pair || l.K > kStreamMaxK || l.stream_depth <= 0 || l.stream_grid <= 0) {
     return hipErrorInvalidValue;
   }
-  // Blocks of waves * depth groups. Half slices: G = 128, one row, two workgroups per slice.
-  // Pieces: the workspace to finish the split slices. Else whole slices, the same count per
-  // workgroup.
   // Whole blocks of waves * depth groups per slice, except half slices (whose last block may be
-  // partial).
+  // partial). Half slices: G = 128, one row, two workgroups per slice. Pieces: the workspace to
+  // finish the split slices. Else whole slices, the same count per workgroup; with the SiLU
+  // epilogue, gate and up slices in pairs (whole / 2 of each, up to the ring's 8 slots).
   const int ng = l.K / l.group_size;
   const int quantum = l.stream_waves * l.stream_depth;
   if (ng % quantum != 0 && !l.stream_half) {
     return hipErrorInvalidValue;
   }
   const long long slices = l.N / kSliceCols;
+  if (l.fuse != GemvFuse::kNone) {
+    const bool norm = l.fuse == GemvFuse::kRmsNorm || l.fuse == GemvFuse::kRmsNormSiluMul;
+    const bool silu = l.fuse == GemvFuse::kSiluMul || l.fuse == GemvFuse::kRmsNormSiluMul;
+    if (l.M != 1 || l.stream_half || l.stream_pieces || (norm && l.norm_weight == nullptr) ||
+        l.stream_whole <= 0 || (silu && (slices % 2 != 0 || l.stream_whole % 2 != 0 ||
+                                          l.stream_whole > 8))) {
+      return hipErrorInvalidValue;
+    }
+  }
   if (l.stream_half) {
     if (l.group_size != 128 || l.M != 1 || l.stream_pieces || l.stream_whole <= 0 ||
         static_cast<long long>(l.stream_grid) * l.stream_whole != 2 * slices) {

@@ -264,6 +264,15 @@ def test_fused_entry_points_validate_without_gpu(lib: ctypes.CDLL) -> None:
     assert rc == 1 and b"must not be null" in lib.fk_last_error()
     rc = lib.fk_w4a16_forward_silu_mul(None, None, None, 1, 384, 256, 128, 1, 0, None, f(0.0), None)
     assert rc == 1 and b"256" in lib.fk_last_error()
+    # one row: the stream kernel with the prologue fused (a slice per workgroup at 192 slices;
+    # whole slices on a divisor grid), none at several rows or with a forced split
+    p = Plan()
+    assert lib.fk_w4a16_plan_rmsnorm(1, 6144, 4096, 128, 1, 0, 256, 1, ctypes.byref(p)) == 0
+    assert (p.schedule, p.workgroups, p.groups_per_workgroup, p.workspace_bytes) == (2, 192, 32, 0)
+    assert lib.fk_w4a16_plan_rmsnorm(1, 28672, 4096, 128, 1, 0, 256, 1, ctypes.byref(p)) == 0
+    assert (p.schedule, p.workgroups, p.groups_per_workgroup) == (2, 224, 128)
+    assert lib.fk_w4a16_plan_rmsnorm(1, 6144, 4096, 128, 1, 2, 256, 1, ctypes.byref(p)) == 0
+    assert p.schedule != 2
     p = Plan()
     assert lib.fk_w4a16_plan_rmsnorm(16, 4096, 4096, 128, 0, 0, 256, 1, ctypes.byref(p)) == 0
     assert (p.m_tile, p.slice_cols) == (8, 32)

@@ -204,3 +204,84 @@ def test_rmsnorm_silu_mul_matches_unfused_pipeline(act, batch) -> None:
     err = np.abs(got - want)
     assert np.all(err <= atol + 2e-2 * np.abs(want)), f"max err {err.max():.4g}"
     assert np.mean(got == want) > 0.9  # the normalised activations rarely differ in a last bit
+
+
+@pytest.mark.parametrize(
+    "n,k,g,fuse",
+    [
+        (6144, 4096, 128, "rmsnorm"),         # Llama-8B qkv: 192 slices, one per workgroup
+        (28672, 4096, 128, "rmsnorm_silu"),   # Llama-8B gate_up: 448 pairs, 2 per CU on 224 CUs
+        (28672, 4096, 128, "silu"),
+        (57344, 8192, 128, "silu"),           # Llama-70B gate_up: 896 pairs, 4 per CU on 224 CUs
+        (16384, 4096, 64, "rmsnorm_silu"),    # G = 64: 256 pairs, one per CU
+    ],
+)
+def test_stream_fused_one_row(n, k, g, fuse) -> None:
+    """The fused neighbours on the stream kernel (one row, whole slices or gate/up slice pairs per
+    workgroup): the RMSNorm prologue against torch's RMSNorm then the plain forward, and the SiLU
+    epilogue against the plain forward then torch's SiLU and product (the same kernel's sums, so
+    equal up to one ulp), and both against the oracle on a spread of columns."""
+    from fast_kernels.native import native_module
+
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the shapes are chosen for 256 CUs")
+    act = "bf16"
+    case = make_case(1, n, k, g, act=act, seed=2100 + n // 1024 + k)
+    x, slabs, fmt = _slabs(case, False)
+    norm = fuse.startswith("rmsnorm")
+    w = None
+    xin = x
+    eps = 1e-5
+    if norm:
+        gen = torch.Generator(device="cpu").manual_seed(5)
+        w = (0.5 + torch.rand(k, generator=gen)).to(x.dtype).to(DEV)
+        xin = _hf_rmsnorm(x, w, eps)
+    native = native_module()
+    if fuse == "rmsnorm":
+        plan = native.w4a16_plan_rmsnorm(1, n, k, g, 1, 0, 0, 1)
+        assert plan["schedule"] == 2, plan
+        got = arc_w4a16_forward_rmsnorm(x, w, slabs, n=n, k=k, group_size=g, eps=eps,
+                                        packet_format=fmt)
+        want = arc_w4a16_forward_native(xin, slabs, n=n, k=k, group_size=g, packet_format=fmt)
+        torch.cuda.synchronize()
+        _assert_gemv_close(_bits(got), _bits(want), case, f"stream rmsnorm {n}x{k}")
+        assert float((got == want).float().mean()) > 0.9
+        xn_bits = xin.view(torch.int16).cpu().numpy().view(np.uint16)
+        cols = np.unique(np.linspace(0, n - 1, 96).astype(int))
+        ref, _ = oracle.gemv(xn_bits, np.ascontiguousarray(case.q_u8[cols]),
+                             np.ascontiguousarray(case.alpha[cols]),
+                             np.ascontiguousarray(case.beta[cols]), g, act)
+        _assert_gemv_close(_bits(got)[:, cols], ref, case, f"stream rmsnorm vs oracle {n}x{k}")
+        return
+    got = arc_w4a16_forward_silu_mul(x, slabs, n=n, k=k, group_size=g, norm_weight=w, eps=eps)
+    y = arc_w4a16_forward_native(xin, slabs, n=n, k=k, group_size=g, packet_format=fmt)
+    gate, up = y[:, : n // 2].float(), y[:, n // 2 :].float()
+    want = (torch.nn.functional.silu(gate).to(x.dtype).float() * up).to(x.dtype)
+    torch.cuda.synchronize()
+    gotf, wantf = got.float(), want.float()
+    ulp = 2.0 ** -7
+    if norm:
+        # the row's 1 / rms may differ from torch's in a last bit: within the GEMV bar
+        max_alpha = float(f16_bits_to_f32(case.alpha).max())
+        atol = 1e-2 * np.sqrt(k) * max_alpha * (float(wantf.abs().max()) + 1.0)
+        err = (gotf - wantf).abs()
+        assert bool((err <= atol + 2e-2 * wantf.abs()).all()), f"max err {float(err.max()):.4g}"
+        assert float((gotf == wantf).float().mean()) > 0.9
+    else:
+        assert bool(((gotf - wantf).abs() <= ulp * wantf.abs() + 1e-6).all())
+        assert float((gotf == wantf).float().mean()) > 0.99
+    # the oracle's gate and up GEMVs (a spread of output columns), combined in float64
+    cols = np.unique(np.linspace(0, n // 2 - 1, 64).astype(int))
+    both = np.concatenate([cols, cols + n // 2])
+    xb = xin.view(torch.int16).cpu().numpy().view(np.uint16)
+    ref_bits, _ = oracle.gemv(xb, np.ascontiguousarray(case.q_u8[both]),
+                              np.ascontiguousarray(case.alpha[both]),
+                              np.ascontiguousarray(case.beta[both]), g, act)
+    yo = _to_f32(ref_bits, act).astype(np.float64)
+    go, uo = yo[:, : cols.size], yo[:, cols.size :]
+    so = _round_act(go / (1.0 + np.exp(-go)), act).astype(np.float64)
+    want_o = so * uo
+    max_alpha = float(f16_bits_to_f32(case.alpha).max())
+    atol = 1e-2 * np.sqrt(k) * max_alpha * (np.abs(uo).max() + np.abs(so).max() + 1.0)
+    err = np.abs(got[:, cols].float().cpu().numpy().astype(np.float64) - want_o)
+    assert np.all(err <= atol + 2e-2 * np.abs(want_o)), f"max err {err.max():.4g}"
