@@ -52,8 +52,12 @@ def _find(directory: str | Path, suffix: str) -> Path:
     return hits[0]
 
 
-def kernel_trace_by_grid(directory: str | Path, name_filter: str = "") -> list[dict]:
-    """Per (kernel, grid) dispatch-duration statistics from a --kernel-trace CSV."""
+def kernel_trace_by_grid(directory: str | Path, name_filter: str = "",
+                         split_us: float | None = None) -> list[dict]:
+    """Per (kernel, grid) dispatch-duration statistics from a --kernel-trace CSV. split_us: a group
+    whose dispatches fall on both sides of that duration, at least a tenth of them on each (two
+    shapes with one kernel and grid, e.g. bench.py's 70B o and gate_up), is reported as two rows,
+    the kernel name suffixed with the side."""
     path = _find(directory, "_kernel_trace.csv")
     groups: dict[tuple[str, int, int], list[int]] = defaultdict(list)
     with path.open(newline="") as fh:
@@ -64,12 +68,27 @@ def kernel_trace_by_grid(directory: str | Path, name_filter: str = "") -> list[d
             grid = int(row["Grid_Size_X"]) * int(row.get("Grid_Size_Y", 1) or 1)
             wg = int(row["Workgroup_Size_X"])
             groups[(name, grid, wg)].append(int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
+    if split_us is not None:
+        cut = int(split_us * 1e3)
+        split: dict[tuple[str, int, int], list[int]] = {}
+        for (name, grid, wg), durs in groups.items():
+            lo = [d for d in durs if d < cut]
+            hi = [d for d in durs if d >= cut]
+            if min(len(lo), len(hi)) >= 0.1 * len(durs):  # two populations, not outliers
+                split[(f"{name} [< {split_us:g} us]", grid, wg)] = lo
+                split[(f"{name} [>= {split_us:g} us]", grid, wg)] = hi
+            else:
+                split[(name, grid, wg)] = durs
+        groups = split
     out = []
     for (name, grid, wg), durs in groups.items():
         durs.sort()
+        label = short_kernel_name(name)
+        if name.endswith(" us]"):
+            label += " " + name[name.rindex("["):]
         out.append(
             {
-                "kernel": short_kernel_name(name),
+                "kernel": label,
                 "grid_threads": grid,
                 "workgroups": grid // max(wg, 1),
                 "calls": len(durs),
@@ -188,6 +207,9 @@ def main(argv: list[str] | None = None) -> int:
     t = sub.add_parser("trace")
     t.add_argument("directory")
     t.add_argument("--filter", default="")
+    t.add_argument("--split-us", type=float, default=None,
+                   help="split (kernel, grid) rows whose dispatches fall on both sides of this "
+                   "duration")
     c = sub.add_parser("traffic")
     c.add_argument("--fetch", required=True)
     c.add_argument("--write", required=True)
@@ -198,7 +220,7 @@ def main(argv: list[str] | None = None) -> int:
     c.add_argument("--bench-json", help="bench.py line of the profiled run: key rows by shape")
     args = p.parse_args(argv)
     if args.cmd == "trace":
-        print(_markdown_trace(kernel_trace_by_grid(args.directory, args.filter)))
+        print(_markdown_trace(kernel_trace_by_grid(args.directory, args.filter, args.split_us)))
     else:
         result = traffic(args.fetch, args.write, args.copy_fetch, args.copy_write, args.copy_bytes,
                          args.filter)
