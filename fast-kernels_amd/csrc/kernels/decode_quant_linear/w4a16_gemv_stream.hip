@@ -50,6 +50,8 @@
 #include "w4a16_gemv_native.h"
 #include "w4a16_stream_common.h"
 
+#include <type_traits>
+
 namespace fk {
 namespace {
 
@@ -354,19 +356,24 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   // host plans K/G as a multiple of kW * D), so the block loops have no branch: the compiler's
   // wait for a buffer is then the in-order count of the loads issued after it, not a drain of the
   // pipeline.
-  auto block = [&](int gl0) {
+  // refill = false: the wave's last block, whose refills would only re-read its last slab and
+  // hold the wave (the end waits for every load) one memory latency after its last arithmetic.
+  auto block_r = [&](int gl0, auto refill) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       native_compute_group<G, A, MT, F, StreamLds<G>, kHalf ? 1 : 2>(sm, buf[d],
                                                                      clamp_x(gl0 + kW * d), t,
                                                                      mask_lo, mask_hi, y, half);
-      load_slab(buf[d], j + d + D);
+      if constexpr (decltype(refill)::value) {
+        load_slab(buf[d], j + d + D);
+      }
       // Issue the refill here, not after the block's later slabs: the scheduler would otherwise
       // sink every load below the block's arithmetic and drain the pipeline once per block.
       __builtin_amdgcn_sched_barrier(0);
     }
     j += D;
   };
+  auto block = [&](int gl0) { block_r(gl0, std::true_type{}); };
   int n_red = 0;  // piece reductions so far: LDS slot 0 (head) or 1 (tail)
   // Folds the lane partials over the column's four quarters (lanes n, n+16, n+32, n+48) into LDS
   // slot `slot` and clears them.
@@ -420,15 +427,25 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     // Without pieces: blocks that each stage one more pass, then blocks that do not: two loops,
     // no branch in either.
     int blk = 0;
+    // the last slice's last block is the wave's last: no refills
+    const int n_loop = r == rg.whole - 1 ? nbs - 1 : nbs;
     if constexpr (!kPieces) {
-      const int n_staging = min(nbs, n_pass - staged);
+      const int n_staging = min(n_loop, n_pass - staged);
       for (; blk < n_staging; ++blk) {
         block(blk * Q + wave);
         stage_one();
       }
     }
-    for (; blk < nbs; ++blk) {
+    for (; blk < n_loop; ++blk) {
       block(blk * Q + wave);
+    }
+    if (r == rg.whole - 1) {
+      if constexpr (!kPieces) {
+        while (staged < n_pass) {  // the passes the last block reads, if still due
+          stage_one();
+        }
+      }
+      block_r((nbs - 1) * Q + wave, std::false_type{});
     }
     if constexpr (!kPieces) {
       while (staged < n_pass) {
