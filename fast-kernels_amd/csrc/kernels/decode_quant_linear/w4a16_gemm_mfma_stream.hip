@@ -28,6 +28,8 @@
 #include "w4a16_gemv_native.h"
 #include "w4a16_stream_common.h"
 
+#include <type_traits>
+
 namespace fk {
 namespace {
 
@@ -336,15 +338,20 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     }
   };
   int j = 0;
-  auto block = [&](int gl0) {
+  // refill = false: the wave's last block (refills past it would only re-read its last slab and
+  // hold the wave one memory latency past its last arithmetic).
+  auto block_r = [&](int gl0, auto refill) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       compute(buf[d], gl0 + kW * d);
-      native_load<G, F>(buf[d], slab(j + d + D), lane);
+      if constexpr (decltype(refill)::value) {
+        native_load<G, F>(buf[d], slab(j + d + D), lane);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
     j += D;
   };
+  auto block = [&](int gl0) { block_r(gl0, std::true_type{}); };
   // The wave's partial tile (rows < M) into the slot, then the first barrier.
   auto reduce = [&]() {
 #pragma unroll
@@ -377,8 +384,12 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     }
   }
   for (int r = 0; r < rg.whole; ++r) {
-    for (int blk = 0; blk < nbs; ++blk) {
+    const int n_loop = r == rg.whole - 1 ? nbs - 1 : nbs;
+    for (int blk = 0; blk < n_loop; ++blk) {
       block(blk * Q + wave);
+    }
+    if (r == rg.whole - 1) {
+      block_r((nbs - 1) * Q + wave, std::false_type{});
     }
     reduce();
     if (wave == (r & (kW - 1))) {
