@@ -128,7 +128,7 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   sm.red = sm.scale + static_cast<size_t>(ng) * MT;
 
   // Adds the waves' partial tiles of output o in wave order.
-  auto total = [&](int o) {
+  auto total = [&](int o) __attribute__((always_inline)) {
     float s = 0.0f;
 #pragma unroll
     for (int w = 0; w < kW; ++w) {
@@ -180,7 +180,7 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   const int off_w = rg.whole_slice0 * ng + wave - (n_h + n_t) * kW;
   const int off_t = rg.tail_slice * ng + wave - n_h * kW;
   const int off_h = rg.head_slice * ng + rg.head_blk0 * Q + wave;
-  auto slab = [&](int i) -> const uint8_t* {
+  auto slab = [&](int i) __attribute__((always_inline)) -> const uint8_t* {
     const int c = min(i, j_last);
     int off = off_w;
     if constexpr (kPieces) {
@@ -211,10 +211,10 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   const int g_last = ng / kW - 1;  // the wave's last group index
   // Group index and row of this lane's unit in pass i (i a compile-time constant). Passes past
   // the wave's last group stage that group again (the same values; the host bounds the passes).
-  auto pass_group = [&](int i) {
+  auto pass_group = [&](int i) __attribute__((always_inline)) {
     return P >= 64 ? min((i * 64) / P, g_last) : min(i * kGroupsPerPass + gsub, g_last);
   };
-  auto pass_row = [&](int i) { return (P >= 64 ? ((i * 64) % P) / WR : 0) + m_l; };
+  auto pass_row = [&](int i) __attribute__((always_inline)) { return (P >= 64 ? ((i * 64) % P) / WR : 0) + m_l; };
   constexpr int kStage = max_stage_per_lane(MT);
   uint4 raw[kStage];
 #pragma unroll
@@ -279,28 +279,39 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     }
   }
   const int r0 = 4 * t;  // D rows of this lane
-  // Slab of slice-local group gl: 2 U MFMAs and the epilogue.
-  auto compute = [&](const NativeLoad<G>& ld, int gl) {
+  // The staged operands of slice-local group gl: the A windows, the chain seeds and the offset
+  // sums of the lane's rows, and (bf16) their staging scales. A block reads the next slab's
+  // while the current one's chains run, so the LDS latency is not on the slab's path.
+  struct Op {
     half8_t a[U];
+    float4_t seed;
+    float s[4];
+    float sc[4];
+  };
+  auto load_op = [&](int gl, Op& o) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < U; ++j) {
       const uint4 xv = sm.xs[(static_cast<size_t>(gl) * WR + U * t + j) * MT +
                              xs_slot<MT>(U * t + j, min(n, MT - 1))];
-      a[j] = __builtin_bit_cast(half8_t, n < MT ? xv : make_uint4(0u, 0u, 0u, 0u));
+      o.a[j] = __builtin_bit_cast(half8_t, n < MT ? xv : make_uint4(0u, 0u, 0u, 0u));
     }
-    float4_t seed;
-    float s[4];
-    float sc[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = min(r0 + r, MT - 1);
       const float2 v = sm.sums[gl * MT + row];
       const bool live = r0 + r < MT;
-      s[r] = live ? v.y : 0.0f;
+      o.s[r] = live ? v.y : 0.0f;
       const float c = F == PacketFormat::kNativeSym ? fmaf(-8.0f, v.y, v.x) : v.x;
-      seed[r] = live ? c : 0.0f;
-      sc[r] = A == Act::kBF16 ? sm.scale[gl * MT + row] : 1.0f;
+      o.seed[r] = live ? c : 0.0f;
+      o.sc[r] = A == Act::kBF16 ? sm.scale[gl * MT + row] : 1.0f;
     }
+  };
+  // Slab of one group: 2 U MFMAs and the epilogue.
+  auto compute = [&](const NativeLoad<G>& ld, const Op& o) __attribute__((always_inline)) {
+    const auto& a = o.a;
+    const float4_t seed = o.seed;
+    const auto& s = o.s;
+    const auto& sc = o.sc;
     uint32_t beta_pair = 0;
     if constexpr (F == PacketFormat::kNativeAsym) {
       beta_pair = __builtin_bit_cast(
@@ -340,20 +351,48 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   int j = 0;
   // refill = false: the wave's last block (refills past it would only re-read its last slab and
   // hold the wave one memory latency past its last arithmetic).
-  auto block_r = [&](int gl0, auto refill) {
+  // One slab of a block: compute with `cur` (its operands), then read the next slab's into `nxt`
+  // ahead of the refill.
+  auto step = [&](int d, int gl0, const Op& cur, Op& nxt, auto refill)
+      __attribute__((always_inline)) {
+    if (d + 1 < D) {
+      load_op(gl0 + kW * (d + 1), nxt);
+    }
+    compute(buf[d], cur);
+    if constexpr (decltype(refill)::value) {
+      native_load<G, F>(buf[d], slab(j + d + D), lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  static_assert(D % 2 == 0, "slabs in pairs: the operand registers alternate");
+  auto block_r = [&](int gl0, auto refill) __attribute__((always_inline)) {
+    if constexpr (kPieces) {
+      // (with pieces the prefetch registers push the kernel into scratch memory)
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-      compute(buf[d], gl0 + kW * d);
-      if constexpr (decltype(refill)::value) {
-        native_load<G, F>(buf[d], slab(j + d + D), lane);
+      for (int d = 0; d < D; ++d) {
+        Op op;
+        load_op(gl0 + kW * d, op);
+        compute(buf[d], op);
+        if constexpr (decltype(refill)::value) {
+          native_load<G, F>(buf[d], slab(j + d + D), lane);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      __builtin_amdgcn_sched_barrier(0);
+    } else {
+      Op op0;
+      Op op1;
+      load_op(gl0, op0);
+#pragma unroll
+      for (int d = 0; d < D; d += 2) {
+        step(d, gl0, op0, op1, refill);
+        step(d + 1, gl0, op1, op0, refill);
+      }
     }
     j += D;
   };
-  auto block = [&](int gl0) { block_r(gl0, std::true_type{}); };
+  auto block = [&](int gl0) __attribute__((always_inline)) { block_r(gl0, std::true_type{}); };
   // The wave's partial tile (rows < M) into the slot, then the first barrier.
-  auto reduce = [&]() {
+  auto reduce = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
