@@ -406,6 +406,83 @@ __device__ __forceinline__ void native_compute_group(const S& sm,
   }
 }
 
+// One row's staged operands of one group for a lane (quarter t): its U activation words, the
+// {offset, sum} pair and (bf16) the staging scale, read from LDS ahead of the slab they serve.
+template <int G>
+struct RowOps {
+  uint4 x[native_unit_words(G)];
+  float2 sums;
+  float scale;
+};
+
+template <int G, Act A, class S>
+__device__ __forceinline__ void native_load_ops(const S& sm, int gl, int t, RowOps<G>& o) {
+  constexpr int U = native_unit_words(G);
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    o.x[j] = sm.x_at(0, gl, U * t + j);
+  }
+  o.sums = sm.sums_at(0, gl, t);
+  o.scale = A == Act::kBF16 ? sm.scale_at(0, gl) : 1.0f;
+}
+
+// native_compute_group for one row from operands already in registers (RowOps): the same
+// arithmetic in the same order.
+template <int G, Act A, PacketFormat F, int kCols = 2>
+__device__ __forceinline__ void native_compute_ops(const RowOps<G>& o, const NativeLoad<G>& ld,
+                                                   uint32_t mask_lo, uint32_t mask_hi,
+                                                   float (&y)[1][2], int half = 0) {
+  static_assert(kCols == 2 || G == 128, "half slabs need G = 128");
+  constexpr int U = native_unit_words(G);
+  float acc[2][2];
+#pragma unroll
+  for (int i = 0; i < kCols; ++i) {
+    acc[i][0] = o.sums.x;
+    acc[i][1] = 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const uint4 xp = o.x[j];
+#pragma unroll
+    for (int i = 0; i < kCols; ++i) {
+      const uint32_t wv = unit_word<G>(ld, i, j);
+      const uint32_t w8 = wv >> 8;
+      const uint32_t e0 = (wv & mask_lo) | kBiasLow;
+      const uint32_t o0 = (wv & mask_hi) | kBiasHigh;
+      const uint32_t e1 = (w8 & mask_lo) | kBiasLow;
+      const uint32_t o1 = (w8 & mask_hi) | kBiasHigh;
+      acc[i][0] = dot2<Act::kF16>(e0, xp.x, acc[i][0]);
+      acc[i][1] = dot2<Act::kF16>(o0, xp.y, acc[i][1]);
+      acc[i][0] = dot2<Act::kF16>(e1, xp.z, acc[i][0]);
+      acc[i][1] = dot2<Act::kF16>(o1, xp.w, acc[i][1]);
+    }
+  }
+  uint32_t beta_pair = 0;
+  if constexpr (F == PacketFormat::kNativeAsym) {
+    beta_pair = __builtin_bit_cast(
+        uint32_t, __builtin_bit_cast(half2_t, ld.alpha) * __builtin_bit_cast(half2_t, ld.zp));
+  }
+#pragma unroll
+  for (int i = 0; i < kCols; ++i) {
+    const int sh = 16 * (kCols == 2 ? i : half);
+    const float a = half_bits_to_float(static_cast<uint16_t>(ld.alpha >> sh));
+    const float b = half_bits_to_float(static_cast<uint16_t>(beta_pair >> sh));
+    const float sum = acc[i][0] + acc[i][1];
+    if constexpr (A == Act::kBF16) {
+      float t_sum = a * sum;
+      if constexpr (F == PacketFormat::kNativeAsym) {
+        t_sum = fmaf(b, o.sums.y, t_sum);
+      }
+      y[0][i] = fmaf(t_sum, o.scale, y[0][i]);
+    } else {
+      y[0][i] = fmaf(a, sum, y[0][i]);
+      if constexpr (F == PacketFormat::kNativeAsym) {
+        y[0][i] = fmaf(b, o.sums.y, y[0][i]);
+      }
+    }
+  }
+}
+
 // Groups [g_lo, g_hi) of one slice: stage the activations of up to kChunk groups in LDS, then
 // each wave streams groups g_lo + wave, g_lo + wave + 4, ... through D register buffers (as the
 // reference-packet kernel's stream_groups).
