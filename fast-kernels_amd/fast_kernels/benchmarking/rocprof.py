@@ -55,9 +55,10 @@ def _find(directory: str | Path, suffix: str) -> Path:
 def kernel_trace_by_grid(directory: str | Path, name_filter: str = "",
                          split_us: float | None = None) -> list[dict]:
     """Per (kernel, grid) dispatch-duration statistics from a --kernel-trace CSV. split_us: a group
-    whose dispatches fall on both sides of that duration, at least a tenth of them on each (two
-    shapes with one kernel and grid, e.g. bench.py's 70B o and gate_up), is reported as two rows,
-    the kernel name suffixed with the side."""
+    whose dispatches fall on both sides of that duration, at least a tenth of them on each and the
+    two sides' medians at least twice apart (two shapes with one kernel and grid, e.g. bench.py's
+    70B o and gate_up, not one shape whose spread straddles the cut), is reported as two rows, the
+    kernel name suffixed with the side."""
     path = _find(directory, "_kernel_trace.csv")
     groups: dict[tuple[str, int, int], list[int]] = defaultdict(list)
     with path.open(newline="") as fh:
@@ -74,7 +75,8 @@ def kernel_trace_by_grid(directory: str | Path, name_filter: str = "",
         for (name, grid, wg), durs in groups.items():
             lo = [d for d in durs if d < cut]
             hi = [d for d in durs if d >= cut]
-            if min(len(lo), len(hi)) >= 0.1 * len(durs):  # two populations, not outliers
+            two = min(len(lo), len(hi)) >= 0.1 * len(durs)  # two populations, not outliers
+            if two and sorted(hi)[len(hi) // 2] >= 2 * sorted(lo)[len(lo) // 2]:
                 split[(f"{name} [< {split_us:g} us]", grid, wg)] = lo
                 split[(f"{name} [>= {split_us:g} us]", grid, wg)] = hi
             else:

@@ -51,3 +51,10 @@ def test_split_keeps_outliers_in_their_row(tmp_path: Path) -> None:
     d = _write(tmp_path / "b", [(KERNEL, 131072, 7000)] * 50 + [(KERNEL, 131072, 25000)] * 2)
     rows = kernel_trace_by_grid(d, "w4a16", split_us=20)
     assert len(rows) == 1 and rows[0]["calls"] == 52
+
+
+def test_split_keeps_one_shape_across_the_cut(tmp_path: Path) -> None:
+    # one shape whose durations straddle the cut (medians 19.9 and 20.4 us) stays one row
+    d = _write(tmp_path / "c", [(KERNEL, 131072, 19900)] * 25 + [(KERNEL, 131072, 20400)] * 75)
+    rows = kernel_trace_by_grid(d, "w4a16", split_us=20)
+    assert len(rows) == 1 and rows[0]["calls"] == 100
