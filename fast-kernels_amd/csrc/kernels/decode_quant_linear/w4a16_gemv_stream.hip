@@ -124,38 +124,10 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   constexpr int kOut = MT * kSliceCols;  // outputs of a slice
   constexpr int kOutPerLane = (kOut + 63) / 64;
 
-  // Activations: every pass's loads first, ahead of the range arithmetic (with pieces some hundred
-  // scalar instructions of divisions); the control wave issues them too and ignores them. Pass i
-  // stages groups wave + kW (i * 64 / WR + l / WR) (lane l, word row l % WR) of every row.
-  constexpr int WR = G / 8;
-  constexpr int kGroupsPerPass = 64 / WR;
-  const int n_pass = (nbs * D + kGroupsPerPass - 1) / kGroupsPerPass;
-  uint4 raw[kStageSlots][MT];
-#pragma unroll
-  for (int i = 0; i < kStageSlots; ++i) {
-    // clamped and unconditional (a load under a branch waits for the one before it); slots past
-    // the wave's passes and groups past the row are never staged
-    const int g = min(wave + kW * (i * kGroupsPerPass + lane / WR), ng - 1);
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      raw[i][m] = *reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * p.K +
-                                                  static_cast<size_t>(g) * G + (lane % WR) * 8);
-    }
-  }
-  // (keeps the loads above the control wave's branch)
-  asm volatile("" ::"v"(raw[0][0].x));
-  __builtin_amdgcn_sched_barrier(0);
   const int slices = p.N / kSliceCols;
-  StreamRange rg = stream_range(b, grid, p.stream_whole, slices, nbs, kPieces);
-  if constexpr (kSilu) {
-    rg.whole_slice0 = b * (p.stream_whole / 2);  // gate slices (whole / 2 of them), then up
-  }
-  // kHalf: half-slices hs0 .. hs0 + whole - 1, half-slice hs being half hs & 1 of slice hs / 2.
-  const int hs0 = kHalf ? b * p.stream_whole : 0;
-  int half = 0;
-
   if constexpr (kPieces) {
     if (wave == kW) {
+      const StreamRange rg = stream_range(b, grid, p.stream_whole, slices, nbs, true);
       // Control wave. Totals of the pieces first (a barrier each), then their hand-offs, then the
       // whole slices' barriers.
       float v[2][kOutPerLane];
@@ -194,6 +166,35 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
       return;
     }
   }
+
+  // Activations: every pass's loads first, ahead of the range arithmetic (with pieces some hundred
+  // scalar instructions of divisions). Pass i stages groups wave + kW (i * 64 / WR + l / WR) (lane
+  // l, word row l % WR) of every row.
+  constexpr int WR = G / 8;
+  constexpr int kGroupsPerPass = 64 / WR;
+  const int n_pass = (nbs * D + kGroupsPerPass - 1) / kGroupsPerPass;
+  uint4 raw[kStageSlots][MT];
+#pragma unroll
+  for (int i = 0; i < kStageSlots; ++i) {
+    // clamped and unconditional (a load under a branch waits for the one before it); slots past
+    // the wave's passes and groups past the row are never staged
+    const int g = min(wave + kW * (i * kGroupsPerPass + lane / WR), ng - 1);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      raw[i][m] = *reinterpret_cast<const uint4*>(p.x + static_cast<size_t>(m) * p.K +
+                                                  static_cast<size_t>(g) * G + (lane % WR) * 8);
+    }
+  }
+  // (no use of the loaded registers here: that would wait for the first load before the weights'
+  // loads go out)
+  __builtin_amdgcn_sched_barrier(0);
+  StreamRange rg = stream_range(b, grid, p.stream_whole, slices, nbs, kPieces);
+  if constexpr (kSilu) {
+    rg.whole_slice0 = b * (p.stream_whole / 2);  // gate slices (whole / 2 of them), then up
+  }
+  // kHalf: half-slices hs0 .. hs0 + whole - 1, half-slice hs being half hs & 1 of slice hs / 2.
+  const int hs0 = kHalf ? b * p.stream_whole : 0;
+  int half = 0;
 
   StreamLds<G> sm;
   sm.slots = ng + 1;
