@@ -12,9 +12,12 @@ as the drop-in entry points take them) is measured too and reported under "other
 whose total exceeds twice the 256 MiB Infinity Cache, and consecutive steps use different copies,
 so every launch streams its weights from HBM.
 
-Timing: the launches of exactly K steps are captured into one HIP graph (torch.cuda.CUDAGraph;
-step s uses weight copy s mod R) and replayed once between HIP events on the capture stream,
-after a graph of the W warm-up steps. value = algorithmic bytes
+Timing: exactly K steps, launched from HIP graphs (torch.cuda.CUDAGraph; step s of a graph uses
+weight copy s mod R) between HIP events on the capture stream: K // W replays of a graph of W
+steps, whose first replay is the W warm-up steps, and a graph of the K mod W left-over steps
+(W = K when no warm-up is asked for, or W >= K). The graphs are captured before the per-shape
+runs below, which keep the GPU busy up to the warm-up (after an idle capture a replay runs slower
+for its first tens of milliseconds while the clocks ramp up). value = algorithmic bytes
 per step / time per step (int4 codes + fp16 scales + activations + outputs; the reference
 packets' fp16 beta, when measured, is read but not credited).
 
@@ -86,7 +89,7 @@ def parse_args() -> argparse.Namespace:
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=1000)  # 1000 steps of the 70B layer: 80 ms
-    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=200)
     p.add_argument("--workload", choices=sorted(WORKLOADS), default="llama70b_layer_m1_bf16")
     p.add_argument("--batch", type=int, default=1)
     p.add_argument("--split-k", type=int, default=0, help="0 = built-in plan")
@@ -285,6 +288,41 @@ def measure(torch, native, args, act, g, shapes, packets):
     ws_bytes = max(max(b.plan["workspace_bytes"] for b in bufs), 1)
     ws = torch.zeros(ws_bytes + 256, device="cuda", dtype=torch.uint8)
     torch.cuda.synchronize()
+    # Whole step: step s of a graph launches every shape with rotation s mod R, so consecutive
+    # steps read different weight copies.
+    R_step = max(len(b.packets) for b in bufs)
+
+    def steps_fn(count):
+        def fn():
+            for s_i in range(count):
+                for b in bufs:
+                    b.launch(native, torch, ws, s_i % R_step)
+        return fn
+
+    # Steady state: the K timed steps are replays of one graph of W steps (the warm-up is one
+    # replay of that same graph), plus a graph of the K mod W left-over steps. The first replay of
+    # a freshly instantiated graph runs about 1 % slower (0.8 us per 70B step, measured on
+    # MI355X), a one-time cost that a single K-step graph would put inside the timed run.
+    # A graph's steps start over at copy 0, so a copy comes back after at most W steps: W must
+    # span more than twice the Infinity Cache of step traffic, else the single K-step graph.
+    min_chunk = rotations_for(sum(b.bytes for b in bufs))
+    use_chunks = min_chunk <= args.warmup < args.steps
+    chunk = args.warmup if use_chunks else args.steps
+    run_chunk = make_runner(torch, steps_fn(chunk), chunk * len(bufs), args.eager)
+    left = args.steps % chunk
+    run_left = make_runner(torch, steps_fn(left), left * len(bufs), args.eager) if left else None
+    if use_chunks:
+        warm = run_chunk
+    else:  # no warm-up, or one too short to chunk the run or of at least K steps: its own graph
+        warm = (make_runner(torch, steps_fn(args.warmup), args.warmup * len(bufs), args.eager)
+                if args.warmup > 0 else None)
+
+    def run_steps(times):
+        for _ in range(times):
+            run_chunk(args.steps // chunk)
+            if run_left is not None:
+                run_left(1)
+
     # Per-shape timing: each shape's own graph of reps x R launches (its R rotations in turn),
     # replayed once between events, so that no graph launch boundary falls inside the run.
     per_shape = {}
@@ -317,23 +355,13 @@ def measure(torch, native, args, act, g, shapes, packets):
             "threads_per_workgroup": _threads_per_workgroup(b.plan, b.k // b.g),
         }
 
-    # Whole step: exactly `steps` steps captured in one graph (step s launches every shape with
-    # rotation s mod R, so consecutive steps read different weight copies), replayed once between
-    # events; the `warmup` steps are a graph of their own, replayed before.
-    R_step = max(len(b.packets) for b in bufs)
-
-    def steps_fn(count):
-        def fn():
-            for s_i in range(count):
-                for b in bufs:
-                    b.launch(native, torch, ws, s_i % R_step)
-        return fn
-
-    if args.warmup > 0:
-        make_runner(torch, steps_fn(args.warmup), args.warmup * len(bufs), args.eager)(1)
-    run = make_runner(torch, steps_fn(args.steps), args.steps * len(bufs), args.eager)
+    # The step's graphs were captured before the per-shape runs, so the GPU has been streaming
+    # right up to the warm-up: the capture of thousands of launches leaves it idle long enough
+    # for its clocks to drop, and a replay right after idle runs slower for its first tens of ms.
     torch.cuda.synchronize()
-    ms = time_events(torch, run, 1)
+    if warm is not None:
+        warm(1)
+    ms = time_events(torch, run_steps, 1)
     torch.cuda.synchronize()
     steps = args.steps
     ms_per_step = ms / steps
