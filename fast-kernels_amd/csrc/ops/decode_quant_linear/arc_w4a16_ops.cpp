@@ -605,11 +605,12 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
         plan.schedule = kScheduleStream;
         plan.slice_cols = half ? fk::kSliceCols / 2 : fk::kSliceCols;
         plan.workgroups = static_cast<int>(grid);
-        // Half-slices with several per workgroup keep a whole slice's 4 KB in flight per wave
-        // (four half-slabs); one half-slice per workgroup measured no better with them.
-        plan.stream_depth =
-            half && whole > 1 && num_groups % (fk::kStreamWaves * 2 * depth) == 0 ? 2 * depth
-                                                                                    : depth;
+        // Half-slices keep a whole slice's 4 KB in flight per wave (four half-slabs) when there are
+        // several per workgroup, or one of short K (8B and 7B o, K/G = 32: 3.72 -> 3.53 and 3.64
+        // -> 3.52 us); one half-slice of long K measured no better with them.
+        const bool deep = half && (whole > 1 || num_groups <= 32) &&
+                          num_groups % (fk::kStreamWaves * 2 * depth) == 0;
+        plan.stream_depth = deep ? 2 * depth : depth;
         plan.stream_whole = whole;
         plan.stream_pieces = pieces ? 1 : 0;
         plan.stream_half = half ? 1 : 0;
