@@ -194,6 +194,15 @@ def rotations_for(total_packet_bytes: int) -> int:
     return max(2, math.ceil(2 * INFINITY_CACHE_BYTES / max(1, total_packet_bytes)) + 1)
 
 
+def step_chunk(steps: int, warmup: int, min_chunk: int) -> tuple[int, bool]:
+    """Steps per graph of the timed run and whether the warm-up is that graph's first replay:
+    W steps per graph when W spans at least min_chunk steps (a graph restarts at weight copy 0)
+    and is shorter than the run, else one graph of all K steps with a warm-up graph of its own.
+    The timed run is steps // chunk replays plus a graph of steps % chunk: exactly K steps."""
+    use = min_chunk <= warmup < steps
+    return (warmup if use else steps), use
+
+
 def make_runner(torch, fn, launches_per_call: int, eager: bool):
     """Returns run(times) that issues `times` x launches_per_call launches on the current stream."""
     if eager:
@@ -305,9 +314,8 @@ def measure(torch, native, args, act, g, shapes, packets):
     # MI355X), a one-time cost that a single K-step graph would put inside the timed run.
     # A graph's steps start over at copy 0, so a copy comes back after at most W steps: W must
     # span more than twice the Infinity Cache of step traffic, else the single K-step graph.
-    min_chunk = rotations_for(sum(b.bytes for b in bufs))
-    use_chunks = min_chunk <= args.warmup < args.steps
-    chunk = args.warmup if use_chunks else args.steps
+    chunk, use_chunks = step_chunk(args.steps, args.warmup,
+                                   rotations_for(sum(b.bytes for b in bufs)))
     run_chunk = make_runner(torch, steps_fn(chunk), chunk * len(bufs), args.eager)
     left = args.steps % chunk
     run_left = make_runner(torch, steps_fn(left), left * len(bufs), args.eager) if left else None
