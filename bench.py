@@ -8,16 +8,22 @@ device), packed into the reference packet layout and, for the headline (--packet
 default), converted on the GPU to the native symmetric slabs: the same code words (8 codes along K
 per uint32, the reference's packing) and alphas, laid out slice-major for contiguous streaming,
 without the fp16 offsets that zp = 8 fixes. The other format (--packets arc: the reference packets
-as the drop-in entry points take them) is measured too and reported under "other_packets". Each shape has R rotated weight copies
-whose total exceeds twice the 256 MiB Infinity Cache, and consecutive steps use different copies,
-so every launch streams its weights from HBM.
+as the drop-in entry points take them) is measured too and reported under "other_packets". Shape b
+has R_b rotated weight copies (together more than twice the 256 MiB Infinity Cache), step s uses
+copy s mod R_b of it, and R_b is chosen so that a graph's restart at copy 0 does not bring a copy
+back early, so every launch streams its weights from HBM.
 
-Timing: exactly K steps, launched from HIP graphs (torch.cuda.CUDAGraph; step s of a graph uses
-weight copy s mod R) between HIP events on the capture stream: K // W replays of a graph of W
-steps, whose first replay is the W warm-up steps, and a graph of the K mod W left-over steps
-(W = K when no warm-up is asked for, or W >= K). The graphs are captured before the per-shape
-runs below, which keep the GPU busy up to the warm-up (after an idle capture a replay runs slower
-for its first tens of milliseconds while the clocks ramp up). value = algorithmic bytes
+Timing: exactly K steps, launched as one replay of a HIP graph of K steps (torch.cuda.CUDAGraph;
+step s uses weight copy s mod R_b of shape b) between HIP events on the capture stream. The
+warm-up replays that same graph (ceil(W / K) times, so at least W untimed steps), since the first
+replay of a freshly instantiated graph runs about 1 % slower. The warm-up is enqueued after a
+synchronisation and the start event right behind it, so the host enqueues the timed replay while
+the GPU runs the warm-up and the timed interval holds no host launch latency. (--graph chunked
+instead replays a W-step graph K // W times plus a graph of the K mod W left-over steps; a
+replay boundary every W steps measured up to 1 us per step slower at W = 5.) The graphs are
+captured before the per-shape runs below, which keep the GPU busy up to the warm-up (after an
+idle capture a replay runs slower for its first tens of milliseconds while the clocks ramp up).
+value = algorithmic bytes
 per step / time per step (int4 codes + fp16 scales + activations + outputs; the reference
 packets' fp16 beta, when measured, is read but not credited).
 
@@ -90,6 +96,13 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=1000)  # 1000 steps of the 70B layer: 80 ms
     p.add_argument("--warmup", type=int, default=200)
+    p.add_argument(
+        "--graph",
+        choices=["single", "chunked"],
+        default="single",
+        help="single: the K timed steps are one replay of a K-step graph, warmed by replaying it; "
+        "chunked: replays of a W-step graph (a replay boundary every W steps)",
+    )
     p.add_argument("--workload", choices=sorted(WORKLOADS), default="llama70b_layer_m1_bf16")
     p.add_argument("--batch", type=int, default=1)
     p.add_argument("--split-k", type=int, default=0, help="0 = built-in plan")
@@ -194,6 +207,19 @@ def rotations_for(total_packet_bytes: int) -> int:
     return max(2, math.ceil(2 * INFINITY_CACHE_BYTES / max(1, total_packet_bytes)) + 1)
 
 
+def step_rotations(chunk: int, r_min: int, min_chunk: int) -> int:
+    """Weight copies of every shape in the step graphs: at least r_min (each shape's own count,
+    so that R copies of any one shape exceed twice the Infinity Cache), and chosen so that the
+    copy sequence also stays cold where a graph of `chunk` steps starts over at copy 0: step s of
+    a graph uses copy s mod R of every shape, so copy 0 comes back after chunk mod R steps at a
+    replay boundary. That is 0 (a seamless cycle), or at least min_chunk steps (more than twice
+    the Infinity Cache of step traffic), or the graph is shorter than R."""
+    r = max(1, r_min)
+    while not (chunk <= r or chunk % r == 0 or chunk % r >= min_chunk):
+        r += 1
+    return r
+
+
 def step_chunk(steps: int, warmup: int, min_chunk: int) -> tuple[int, bool]:
     """Steps per graph of the timed run and whether the warm-up is that graph's first replay:
     W steps per graph when W spans at least min_chunk steps (a graph restarts at weight copy 0)
@@ -223,11 +249,18 @@ def make_runner(torch, fn, launches_per_call: int, eager: bool):
     return run
 
 
-def time_events(torch, run, reps: int) -> float:
-    """Milliseconds for run(reps), by HIP events on the current stream."""
+def time_events(torch, run, reps: int, lead=None) -> float:
+    """Milliseconds for run(reps), by HIP events on the current stream.
+
+    lead: untimed work enqueued after the synchronisation and before the start event (the
+    warm-up). While the GPU runs it, the host enqueues the timed launches, so the timed interval
+    starts with the GPU busy instead of waiting for the host's first graph launch (tens of
+    microseconds, which a short timed run of 20 steps would otherwise count as 1-2 %)."""
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    if lead is not None:
+        lead()
     start.record()
     run(reps)
     end.record()
@@ -287,39 +320,50 @@ def cpu_baseline(workload: str, batch: int, seconds: float) -> dict:
 def measure(torch, native, args, act, g, shapes, packets):
     """Per-shape and whole-step timing over packets of one format. The buffers are freed before
     returning except for what the report needs (plans, byte counts)."""
+    # Shape b has R_b weight copies and step s uses copy s mod R_b of it. R_b is the fewest
+    # copies whose total exceeds twice the Infinity Cache, raised where needed so that a graph's
+    # restart at copy 0 does not bring a copy back early (step_rotations). The weights of all
+    # copies stay few (a larger footprint adds TLB misses that a minimal rotation does not have).
+    step_bytes = sum(algorithmic_bytes(args.batch, n, k, g) for _, n, k in shapes)
+    min_chunk = rotations_for(step_bytes)
+    if args.graph == "single":
+        chunk, use_chunks = args.steps, False
+    else:
+        chunk, use_chunks = step_chunk(args.steps, args.warmup, min_chunk)
     bufs = []
     for name, n, k in shapes:
         pk_bytes = (n // 128) * (k // g) * (128 * g // 2 + 512)
+        r_b = step_rotations(chunk, rotations_for(pk_bytes), min_chunk)
         bufs.append(
-            ShapeBuffers(torch, native, name, n, k, g, args.batch, act, rotations_for(pk_bytes),
-                         args.split_k, packets)
+            ShapeBuffers(torch, native, name, n, k, g, args.batch, act, r_b, args.split_k,
+                         packets)
         )
     ws_bytes = max(max(b.plan["workspace_bytes"] for b in bufs), 1)
     ws = torch.zeros(ws_bytes + 256, device="cuda", dtype=torch.uint8)
     torch.cuda.synchronize()
     # Whole step: step s of a graph launches every shape with rotation s mod R, so consecutive
     # steps read different weight copies.
-    R_step = max(len(b.packets) for b in bufs)
 
     def steps_fn(count):
         def fn():
             for s_i in range(count):
                 for b in bufs:
-                    b.launch(native, torch, ws, s_i % R_step)
+                    b.launch(native, torch, ws, s_i)
         return fn
 
-    # Steady state: the K timed steps are replays of one graph of W steps (the warm-up is one
-    # replay of that same graph), plus a graph of the K mod W left-over steps. The first replay of
-    # a freshly instantiated graph runs about 1 % slower (0.8 us per 70B step, measured on
-    # MI355X), a one-time cost that a single K-step graph would put inside the timed run.
-    # A graph's steps start over at copy 0, so a copy comes back after at most W steps: W must
-    # span more than twice the Infinity Cache of step traffic, else the single K-step graph.
-    chunk, use_chunks = step_chunk(args.steps, args.warmup,
-                                   rotations_for(sum(b.bytes for b in bufs)))
+    # Steady state: the K timed steps are one replay of a K-step graph (--graph single), or
+    # replays of a W-step graph plus a graph of the K mod W left-over steps (--graph chunked).
+    # Either way the timed replays are not a graph's first (about 1 % slower, 0.8 us per 70B step
+    # on MI355X). A graph's steps start over at copy 0; the copy counts above keep that cold.
     run_chunk = make_runner(torch, steps_fn(chunk), chunk * len(bufs), args.eager)
     left = args.steps % chunk
     run_left = make_runner(torch, steps_fn(left), left * len(bufs), args.eager) if left else None
-    if use_chunks:
+    if args.graph == "single":
+        # The warm-up replays the timed graph itself (ceil(W / K) times, so at least W steps):
+        # the timed replay is then not the graph's first, which runs about 1 % slower.
+        reps_warm = -(-args.warmup // args.steps) if args.warmup > 0 else 0
+        warm = (lambda times, r=reps_warm: run_chunk(times * r)) if reps_warm else None
+    elif use_chunks:
         warm = run_chunk
     else:  # no warm-up, or one too short to chunk the run or of at least K steps: its own graph
         warm = (make_runner(torch, steps_fn(args.warmup), args.warmup * len(bufs), args.eager)
@@ -366,10 +410,9 @@ def measure(torch, native, args, act, g, shapes, packets):
     # The step's graphs were captured before the per-shape runs, so the GPU has been streaming
     # right up to the warm-up: the capture of thousands of launches leaves it idle long enough
     # for its clocks to drop, and a replay right after idle runs slower for its first tens of ms.
-    torch.cuda.synchronize()
-    if warm is not None:
-        warm(1)
-    ms = time_events(torch, run_steps, 1)
+    # The warm-up replay leads the timed replays with no synchronisation in between, so the
+    # host enqueues the timed graphs while the GPU runs the warm-up.
+    ms = time_events(torch, run_steps, 1, lead=(lambda: warm(1)) if warm is not None else None)
     torch.cuda.synchronize()
     steps = args.steps
     ms_per_step = ms / steps
@@ -381,7 +424,7 @@ def measure(torch, native, args, act, g, shapes, packets):
     del ws
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
-    return bufs, per_shape, value, ms_per_step, steps, R_step
+    return bufs, per_shape, value, ms_per_step, steps
 
 
 def main() -> int:
@@ -413,7 +456,7 @@ def main() -> int:
     if not args.no_other_packets:
         other_format = "native_sym" if args.packets == "arc" else "arc"
         other = measure(torch, native, args, act, g, shapes, other_format)
-    bufs, per_shape, value, ms_per_step, steps, R_step = first
+    bufs, per_shape, value, ms_per_step, steps = first
 
     dominant = max(bufs, key=lambda b: b.bytes)
     dom = per_shape[dominant.name]
@@ -454,7 +497,7 @@ def main() -> int:
         },
     }
     if other is not None:
-        o_bufs, o_per_shape, o_value, o_ms, _, _ = other
+        o_bufs, o_per_shape, o_value, o_ms, _ = other
         result["other_packets"] = {
             "packets": "native_sym" if args.packets == "arc" else "arc",
             "value": round(o_value, 1),

@@ -90,6 +90,9 @@ __device__ __forceinline__ void stream_hand_off(const GemvParams& p, int b, int 
     }
   }
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  // The waitcnt builtin is no compiler barrier: a signal fence (no instruction) keeps the
+  // compiler from moving the partial stores past the counter bump below.
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   // Parts of the slice: the workgroups owning its first and last left-over block.
   const int s_left = grid * whole;
   const int left_blocks = (slices - s_left) * nbs;
@@ -105,6 +108,8 @@ __device__ __forceinline__ void stream_hand_off(const GemvParams& p, int b, int 
   if (prev != static_cast<uint32_t>(b_last - b_first)) {
     return;
   }
+  // and the partial loads of the last part ahead of its counter bump
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   float acc[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {

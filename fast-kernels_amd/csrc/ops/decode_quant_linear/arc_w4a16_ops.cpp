@@ -1191,6 +1191,9 @@ void w4a16_forward_noalloc(std::uintptr_t activations_ptr, std::uintptr_t packet
         << "no-allocation entry point holds " << kNoAllocScratchBytes << " per device";
     throw_invalid(oss.str());
   }
+  if (plan.workspace_bytes > 0) {
+    noalloc_claim_stream(stream);
+  }
   void* scratch = noalloc_scratch(kCounterRegionBytes, stream);
   run_gemv(activations_ptr, packets_ptr, output_ptr, scratch, plan, batch, n, k, group_size,
            activation_dtype, stream, format);

@@ -16,4 +16,9 @@ constexpr std::size_t kNoAllocScratchBytes = (8u << 20) + (64u << 10);
 // first lookup the first clear_bytes of it are zeroed by a kernel on `stream`.
 void* noalloc_scratch(std::size_t clear_bytes, hipStream_t stream);
 
+// Records `stream` as the one using the current device's scratch. Throws std::runtime_error when
+// another stream recorded earlier still has work queued (or is being captured), since the two
+// would race on the scratch. Not checked while `stream` itself is being captured.
+void noalloc_claim_stream(hipStream_t stream);
+
 }  // namespace fast_kernels::decode_quant_linear

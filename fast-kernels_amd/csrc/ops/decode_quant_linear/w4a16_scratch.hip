@@ -10,7 +10,9 @@
 // Every call on one GPU shares that GPU's array. The GEMV returns the counter region to zero at
 // the end of every call, and the region is cleared once, by a fill kernel on the first calling
 // stream, when the device's address is first looked up; calls that overlap on one GPU (other
-// streams, concurrent graphs) race on it.
+// streams, concurrent graphs) race on it. As a guard against the common misuse, the last stream
+// that called on a device is recorded, and a call from another stream while that one still has
+// work queued is refused (noalloc_claim_stream).
 #include "ops/decode_quant_linear/w4a16_scratch.h"
 
 #include "fk_w4a16.h"
@@ -72,6 +74,50 @@ void* noalloc_scratch(std::size_t clear_bytes, hipStream_t stream) {
     addresses[device] = ptr;
   }
   return addresses[device];
+}
+
+void noalloc_claim_stream(hipStream_t stream) {
+  static std::array<hipStream_t, kMaxScratchDevices> owners{};
+  static std::array<bool, kMaxScratchDevices> owned{};
+  static std::mutex mutex;
+  int device = 0;
+  check(hipGetDevice(&device), "hipGetDevice");
+  if (device < 0 || device >= kMaxScratchDevices) {
+    throw std::runtime_error("device index out of range");
+  }
+  std::lock_guard<std::mutex> lock(mutex);
+  if (!owned[device] || owners[device] == stream) {
+    owners[device] = stream;
+    owned[device] = true;
+    return;
+  }
+  // A call being captured records kernels that run only when the graph is replayed, so there is
+  // nothing to compare against now (and stream queries are not allowed during a capture).
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &status) == hipSuccess &&
+      status != hipStreamCaptureStatusNone) {
+    return;
+  }
+  bool busy = false;
+  if (hipStreamIsCapturing(owners[device], &status) == hipSuccess &&
+      status != hipStreamCaptureStatusNone) {
+    busy = true;
+  } else {
+    busy = hipStreamQuery(owners[device]) == hipErrorNotReady;
+  }
+  // a query that is not hipSuccess leaves its code as the thread's last error; the launch checks
+  // that follow must not see it
+  (void)hipGetLastError();
+  if (busy) {
+    std::ostringstream oss;
+    oss << "fk_w4a16_forward_noalloc: stream " << static_cast<const void*>(stream)
+        << " would share device " << device << "'s scratch with stream "
+        << static_cast<const void*>(owners[device])
+        << ", which still has work queued; synchronise it first (calls that overlap on one GPU "
+           "race on the scratch)";
+    throw std::runtime_error(oss.str());
+  }
+  owners[device] = stream;
 }
 
 }  // namespace fast_kernels::decode_quant_linear

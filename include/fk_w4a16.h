@@ -202,7 +202,10 @@ int fk_arc_w4a16_forward_native(const void* activations, const void* packets, vo
  * clearing kernel on that call's stream). Launches whose plan needs more scratch than that fail
  * with FK_ERR_INVALID_ARGUMENT before any device work. Every call on one GPU shares its array:
  * calls that overlap on one GPU (different streams, graphs replayed concurrently) race; calls
- * ordered on one stream do not. Results are those of fk_arc_w4a16_forward_native. */
+ * ordered on one stream do not. As a guard, a call whose plan uses the scratch fails with
+ * FK_ERR_RUNTIME when the previous such call on that GPU came from another stream that still has
+ * work queued (not checked while the calling stream is being captured). Results are those of
+ * fk_arc_w4a16_forward_native. */
 #define FK_NOALLOC_SCRATCH_BYTES (8388608 + 65536)
 int fk_w4a16_forward_noalloc(const void* activations, const void* packets, void* output, int batch,
                              int n, int k, int group_size, int packet_format,

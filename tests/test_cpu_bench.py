@@ -36,3 +36,23 @@ def test_min_chunk_spans_twice_the_infinity_cache() -> None:
     step_bytes = 441_460_000  # the 70B layer's four GEMVs
     m = rotations_for(step_bytes)
     assert m * step_bytes >= 2 * 256 * 2**20 and m == 3
+
+
+@pytest.mark.parametrize(
+    "chunk,r_min,min_chunk",
+    [(5, 17, 3), (200, 17, 3), (200, 4, 3), (18, 17, 3), (35, 17, 3), (200, 64, 2), (1000, 9, 3),
+     (7, 7, 3), (64, 21, 2)],
+)
+def test_step_rotations_keep_copies_cold_at_graph_restarts(chunk, r_min, min_chunk) -> None:
+    from bench import step_rotations
+
+    r = step_rotations(chunk, r_min, min_chunk)
+    assert r >= r_min
+    # Replay the copy sequence of three back-to-back replays of one graph: every copy must come
+    # back no sooner than min_chunk steps (R steps inside a graph, chunk mod R at a restart).
+    seq = [s % r for _ in range(3) for s in range(chunk)]
+    last = {}
+    for i, c in enumerate(seq):
+        if c in last:
+            assert i - last[c] >= min_chunk, (chunk, r, i, c)
+        last[c] = i

@@ -311,3 +311,33 @@ def test_forced_split_never_pairs_or_streams(lib: ctypes.CDLL, split: int) -> No
         assert lib.fk_w4a16_plan_for_format(1, n, k, 128, 0, split, 256, 1, ctypes.byref(p)) == 0
         assert p.schedule == 0 and p.slice_cols == 32, (n, k, split)
         assert p.groups_per_workgroup == -(-(k // 128) // split)
+
+
+NOALLOC_SCRATCH_BYTES = 8388608 + 65536  # FK_NOALLOC_SCRATCH_BYTES
+
+
+def test_automatic_plans_fit_the_noalloc_scratch(lib: ctypes.CDLL) -> None:
+    """fk_w4a16_forward_noalloc runs the automatic plan with a fixed per-device scratch array: every
+    automatic plan of up to 16 activation rows and N up to 131072 must fit it, over every packet
+    format, both group sizes and the CU counts of the gfx950 parts (and neighbours)."""
+    assert f"#define FK_NOALLOC_SCRATCH_BYTES (8388608 + 65536)" in HEADER.read_text()
+    lib.fk_w4a16_plan_for_format.argtypes = [ctypes.c_int] * 8 + [ctypes.POINTER(Plan)]
+    worst = (0, None)
+    ns = [128, 1024, 4096, 6144, 8192, 10240, 12288, 14336, 22016, 28672, 32768, 57344, 65536,
+          131072]
+    ks = [512, 1024, 4096, 8192, 11008, 14336, 28672, 32768]
+    for batch in range(1, 17):
+        for n in ns:
+            for k in ks:
+                for g in (64, 128):
+                    if k % g:
+                        continue
+                    for fmt in (0, 1, 2):
+                        for cu in (224, 256, 304):
+                            p = Plan()
+                            rc = lib.fk_w4a16_plan_for_format(batch, n, k, g, 0, 0, cu, fmt,
+                                                              ctypes.byref(p))
+                            assert rc == 0, (batch, n, k, g, fmt, cu)
+                            if p.workspace_bytes > worst[0]:
+                                worst = (p.workspace_bytes, (batch, n, k, g, fmt, cu))
+    assert worst[0] <= NOALLOC_SCRATCH_BYTES, worst

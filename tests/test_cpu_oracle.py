@@ -54,6 +54,39 @@ def test_bf16_round_trip_and_rounding() -> None:
         assert lib.fko_f32_to_bf16_bits(float(v)) == b
 
 
+def test_f32_to_bf16_matches_torch_on_edge_random_and_tie_values() -> None:
+    """fko_f32_to_bf16_bits (the oracle's bf16 output rounding) against torch's IEEE round-to-
+    nearest-even cast to bfloat16, over the fp16 test's value set plus exact bf16 ties (low 16
+    bits 0x8000, both parities of the kept bit), bf16 subnormals, the overflow boundary and
+    signed zeros."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(1)
+    specials = np.array(
+        [0.0, -0.0, 1.0, -1.0, 3.3895314e38, 3.3961776e38, 3.4028235e38, 1e-38, 9.18e-41,
+         -9.18e-41, 1.0e-45, np.inf, -np.inf, 1.00390625, 1.01171875, 65504.0, 1e9, -1e9],
+        dtype=np.float32,
+    )
+    rand = np.concatenate(
+        [
+            rng.standard_normal(20000).astype(np.float32) * 10.0 ** rng.integers(-30, 30, 20000),
+            rng.uniform(-70000, 70000, 5000).astype(np.float32),
+        ]
+    ).astype(np.float32)
+    ties_bits = (rng.integers(0, 2**16, 4000, dtype=np.uint32) << 16) | np.uint32(0x8000)
+    ties = ties_bits.view(np.float32)
+    ties = ties[np.isfinite(ties)]
+    sub_bits = rng.integers(1, 2**23, 1000, dtype=np.uint32) | (
+        rng.integers(0, 2, 1000, dtype=np.uint32) << 31)
+    vals = np.concatenate([specials, rand, ties, sub_bits.view(np.float32)]).astype(np.float32)
+    want = torch.from_numpy(vals).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    lib = oracle.lib()
+    got = np.array([lib.fko_f32_to_bf16_bits(float(v)) for v in vals], dtype=np.uint16)
+    np.testing.assert_array_equal(got, want)
+    np.testing.assert_array_equal(f32_to_bf16_bits(vals), want)  # the host-side input recipe
+    nan = lib.fko_f32_to_bf16_bits(float("nan"))
+    assert nan & 0x7F80 == 0x7F80 and nan & 0x7F
+
+
 def _numpy_dequant(case, group_size):
     q = np.empty((case.n, case.k), dtype=np.float32)
     q[:, 0::2] = case.q_u8 & 0xF

@@ -1,5 +1,7 @@
 """GPU parity at the benchmark configurations' exact shapes, against the CPU oracle.
 
+  * configuration 1 (Llama-7B projections, M = 1, fp16): the four shapes over native symmetric
+    slabs with the automatic plan, every row;
   * configuration 2 (Llama-70B layer, M = 1, bf16): the four projections over native symmetric
     slabs with the automatic plan, i.e. exactly the launches bench.py times (the stream schedule
     for o, gate_up and down, per-slice runs for qkv), and over the reference packets;
@@ -85,6 +87,33 @@ def test_config2_llama70b_bf16_as_benchmarked(name: str, n: int, k: int, packets
     rows = _rows(n)
     _assert_gemv_close(_bits(y)[:, rows], _oracle_rows(case, rows, "bf16"), case,
                        f"70B {name} {packets} plan={plan}")
+
+
+LLAMA7B = [("qkv", 12288, 4096), ("o", 4096, 4096), ("gate_up", 22016, 4096),
+           ("down", 4096, 11008)]
+
+
+@pytest.mark.parametrize("name,n,k", LLAMA7B)
+def test_config1_llama7b_fp16_as_suite_times(name: str, n: int, k: int) -> None:
+    """Configuration 1 (Llama-7B projections, M = 1, G = 128, fp16) over native symmetric slabs
+    with the automatic plan, the launches `fk bench` times for the 7B suite (half slices for o and
+    down, per-slice runs or the stream schedule for qkv and gate_up): every output row against
+    the oracle, and identical bits over three calls."""
+    case = make_case(1, n, k, 128, act="f16")
+    x, q, a, b = _upload(case)
+    slabs = convert_arc_to_native_packets(pack_arc_w4a16_packets(q, a, b, group_size=128), n=n,
+                                          k=k, group_size=128)
+    plan = arc_w4a16_plan(batch=1, n=n, k=k, group_size=128, activation_dtype=torch.float16,
+                          packet_format=1)
+    outs = []
+    for _ in range(3):
+        y = arc_w4a16_forward_native(x, slabs, n=n, k=k, group_size=128, packet_format="native_sym")
+        torch.cuda.synchronize()
+        outs.append(_bits(y))
+    ref, _ = oracle.gemv(case.x, case.q_u8, case.alpha, case.beta, 128, "f16")
+    _assert_gemv_close(outs[0], ref, case, f"7B {name} native_sym plan={plan}")
+    np.testing.assert_array_equal(outs[1], outs[0])
+    np.testing.assert_array_equal(outs[2], outs[0])
 
 
 _CONFIG3_REF: dict[int, tuple] = {}

@@ -94,3 +94,123 @@ def test_noalloc_rejects_invalid_arguments_before_device_work() -> None:
     assert rc == 1 and b"group_size" in lib.fk_last_error()
     rc = lib.fk_w4a16_forward_noalloc(None, None, None, 1, 128, 256, 128, 7, 0, None)
     assert rc == 1 and b"packet_format" in lib.fk_last_error()
+
+
+def _noalloc(lib, x, packets, y, shape, stream):
+    batch, n, k, g, act, fmt = shape
+    return lib.fk_w4a16_forward_noalloc(x.data_ptr(), packets.data_ptr(), y.data_ptr(), batch, n,
+                                        k, g, fmt, 0 if act == "f16" else 1, stream)
+
+
+def test_noalloc_graph_capture_replays_match_eager() -> None:
+    """A noalloc call captured in a HIP graph (torch.cuda.CUDAGraph), replayed three times with
+    eager work in between: every replay equals forward_native bit for bit."""
+    lib = _lib()
+    y_eager, y_ref = _both(lib, TAIL)  # eager noalloc against forward_native, same inputs below
+    np.testing.assert_array_equal(y_eager, y_ref)
+    batch, n, k, g, act, fmt = TAIL
+    x, packets = _inputs(batch, n, k, g, act, fmt, seed=n + k + batch)
+    y = torch.full((batch, n), float("nan"), device=DEV, dtype=x.dtype)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            rc = _noalloc(lib, x, packets, y, TAIL, side.cuda_stream)
+            assert rc == 0, lib.fk_last_error()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(_bits(y), y_ref, err_msg=f"replay {rep}")
+        # eager work on the same scratch between replays
+        y2 = torch.empty_like(y)
+        assert _noalloc(lib, x, packets, y2, TAIL, torch.cuda.current_stream().cuda_stream) == 0
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(_bits(y2), y_ref)
+
+
+def test_noalloc_refuses_a_second_stream_while_the_first_is_busy() -> None:
+    lib = _lib()
+    batch, n, k, g, act, fmt = TAIL
+    x, packets = _inputs(batch, n, k, g, act, fmt, seed=7)
+    y = torch.empty((batch, n), device=DEV, dtype=x.dtype)
+    a, b = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    assert _noalloc(lib, x, packets, y, TAIL, a.cuda_stream) == 0, lib.fk_last_error()
+    with torch.cuda.stream(a):
+        torch.cuda._sleep(200_000_000)  # a bounded spin: stream a has work queued for a while
+    rc = _noalloc(lib, x, packets, y, TAIL, b.cuda_stream)
+    busy = a.query() is False
+    torch.cuda.synchronize()
+    if busy:  # the spin was still running when b called (it takes tens of milliseconds)
+        assert rc == 2 and b"still has work queued" in lib.fk_last_error(), rc
+    # once stream a is idle, stream b takes the scratch over, and the results are unchanged
+    y_b = torch.full_like(y, float("nan"))
+    assert _noalloc(lib, x, packets, y_b, TAIL, b.cuda_stream) == 0, lib.fk_last_error()
+    torch.cuda.synchronize()
+    y_a = torch.full_like(y, float("nan"))
+    assert _noalloc(lib, x, packets, y_a, TAIL, a.cuda_stream) == 0, lib.fk_last_error()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_bits(y_a), _bits(y_b))
+
+
+_FIRST_CALL_UNDER_CAPTURE = r"""
+import sys
+sys.path[:0] = [sys.argv[1], sys.argv[2]]
+import numpy as np
+import torch
+import test_zz_no_alloc as t
+
+lib = t._lib()
+batch, n, k, g, act, fmt = t.TAIL
+x, packets = t._inputs(batch, n, k, g, act, fmt, seed=11)
+torch.cuda.synchronize()
+y = torch.full((batch, n), float("nan"), device="cuda", dtype=x.dtype)
+side = torch.cuda.Stream()
+with torch.cuda.stream(side):
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        rc = t._noalloc(lib, x, packets, y, t.TAIL, side.cuda_stream)  # the process's first call
+assert rc == 0, lib.fk_last_error()
+torch.cuda.synchronize()
+outs = []
+for _ in range(2):
+    y.fill_(float("nan"))
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    outs.append(t._bits(y).copy())
+plan = t.arc_w4a16_plan(batch=batch, n=n, k=k, group_size=g, activation_dtype=x.dtype,
+                        packet_format=fmt)
+ws = torch.zeros(plan["workspace_bytes"] + 256, device="cuda", dtype=torch.uint8)
+y_ref = torch.empty_like(y)
+rc = lib.fk_arc_w4a16_forward_native(x.data_ptr(), packets.data_ptr(), y_ref.data_ptr(),
+                                     ws.data_ptr(), ws.numel(), batch, n, k, g, fmt,
+                                     0 if act == "f16" else 1, 0,
+                                     torch.cuda.current_stream().cuda_stream)
+assert rc == 0, lib.fk_last_error()
+torch.cuda.synchronize()
+for o in outs:
+    np.testing.assert_array_equal(o, t._bits(y_ref))
+print("ok")
+"""
+
+
+def test_noalloc_first_call_of_the_process_under_graph_capture() -> None:
+    """The device set-up (address lookup, clearing kernel) happening inside a capture: a fresh
+    process whose first noalloc call is captured, replayed twice, equal to forward_native."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    tests_dir = Path(__file__).resolve().parent
+    pkg = tests_dir.parent / "fast-kernels_amd"
+    proc = subprocess.run(
+        [sys.executable, "-c", _FIRST_CALL_UNDER_CAPTURE, str(tests_dir), str(pkg)],
+        capture_output=True, text=True, timeout=110, env=dict(os.environ),
+        cwd=str(tests_dir.parent),
+    )
+    assert proc.returncode == 0 and "ok" in proc.stdout, proc.stdout[-2000:] + proc.stderr[-2000:]
