@@ -134,3 +134,22 @@ def test_result_bundle_round_trip(tmp_path: Path) -> None:
     assert loaded.schema_version == 2 and loaded.metadata.schema_version == 2
     assert (tmp_path / "plots" / "hbm_bandwidth.svg").exists()
     assert "1000.0" in (tmp_path / "summary.md").read_text()
+
+
+def test_plan_sweep_report_groups_same_plans_and_ratios() -> None:
+    """The plan sweep's report (fast_kernels.benchmarking.plan_sweep): candidates with the same
+    plan are listed together, and auto/best compares the automatic plan with the fastest one."""
+    from fast_kernels.benchmarking.plan_sweep import _markdown
+
+    plan_a = {"m_tile": 1, "workgroups": 256, "groups_per_workgroup": 64, "slice_cols": 32,
+              "schedule": 2}
+    plan_b = dict(plan_a, schedule=0)
+    rows = [
+        {"config": "2", "shape": "70B o", "cand": "auto", "names": ["auto", "split_k=1"],
+         "us": 7.5, "plan": plan_a, "bytes": 34635776},
+        {"config": "2", "shape": "70B o", "cand": "no_stream", "names": ["no_stream"],
+         "us": 7.0, "plan": plan_b, "bytes": 34635776},
+    ]
+    md = _markdown(rows, "cmd")
+    assert "| 2 | 70B o | stream wg=256 gpw=64 cols=32 mt=1 | 7.50 | no_stream | 7.00 | 1.071 |" in md
+    assert "| auto, split_k=1 | stream" in md
