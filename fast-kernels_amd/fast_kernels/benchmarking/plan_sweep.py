@@ -57,6 +57,15 @@ SHAPES: list[tuple[str, str, int, int, int, int, str, str]] = [
     ("4", "8B o", 1, 4096, 4096, 128, "bf16", "native_sym"),
     ("4", "8B gate_up", 1, 28672, 4096, 128, "bf16", "native_sym"),
     ("4", "8B down", 1, 4096, 14336, 128, "bf16", "native_sym"),
+    # the drop-in path: the same shapes over the reference packets
+    ("1", "7B qkv arc", 1, 12288, 4096, 128, "f16", "arc"),
+    ("0/1", "7B o arc", 1, 4096, 4096, 128, "f16", "arc"),
+    ("1", "7B gate_up arc", 1, 22016, 4096, 128, "f16", "arc"),
+    ("1", "7B down arc", 1, 4096, 11008, 128, "f16", "arc"),
+    ("2", "70B qkv arc", 1, 10240, 8192, 128, "bf16", "arc"),
+    ("2", "70B o arc", 1, 8192, 8192, 128, "bf16", "arc"),
+    ("2", "70B gate_up arc", 1, 57344, 8192, 128, "bf16", "arc"),
+    ("2", "70B down arc", 1, 8192, 28672, 128, "bf16", "arc"),
 ]
 
 # Environments (one child process each): name -> variables.
@@ -71,7 +80,7 @@ ENVS: dict[str, dict[str, str]] = {
     "wpc2": {"FK_W4A16_STREAM_WPC": "2"},
     "no_mfma_stream": {"FK_W4A16_MFMA_STREAM": "0"},
 }
-SPLITS = (1, 2, 4, 8)
+SPLITS = (1, 2, 3, 4, 6, 8, 16)
 KERNELS = {"auto": 0, "dot2": 1, "mfma": 2}
 FORMATS = {"arc": 0, "native_sym": 1, "native_asym": 2}
 PLAN_KEYS = ("m_tile", "workgroups", "groups_per_workgroup", "slice_cols", "schedule")
