@@ -313,10 +313,14 @@ __device__ __forceinline__ float row_strided_sum(float v) {
 
 template <int N>
 __device__ __forceinline__ uint32_t group_max(uint32_t v) {
-  static_assert(N == 8 || N == 16, "group of 8 or 16 lanes");
+  static_assert(N == 2 || N == 4 || N == 8 || N == 16, "group of 2, 4, 8 or 16 lanes");
   v = max(v, dpp::move<dpp::kQuadXor1>(v));
-  v = max(v, dpp::move<dpp::kQuadXor2>(v));
-  v = max(v, dpp::move<dpp::kRowHalfMirror>(v));
+  if constexpr (N >= 4) {
+    v = max(v, dpp::move<dpp::kQuadXor2>(v));
+  }
+  if constexpr (N >= 8) {
+    v = max(v, dpp::move<dpp::kRowHalfMirror>(v));
+  }
   if constexpr (N == 16) {
     v = max(v, dpp::move<dpp::kRowMirror>(v));
   }

@@ -111,6 +111,11 @@ hipError_t launch_w4a16_gemv(const GemvLaunch& launch, hipStream_t stream);
 hipError_t launch_w4a16_gemm_mfma(const GemvLaunch& launch, hipStream_t stream);
 hipError_t launch_w4a16_gemv_native(const GemvLaunch& launch, hipStream_t stream);
 hipError_t launch_w4a16_gemv_stream(const GemvLaunch& launch, hipStream_t stream);
+// One row over the reference packets on the stream schedule (w4a16_gemv_arc_stream.hip): whole
+// 128-column tiles per workgroup plus pieces of the tiles left over; arc_stream_lds: its dynamic
+// LDS bytes.
+hipError_t launch_w4a16_gemv_arc_stream(const GemvLaunch& launch, hipStream_t stream);
+size_t arc_stream_lds(int group_size, int k);
 // Matrix-core kernel on the stream schedule (w4a16_gemm_mfma_stream.hip): native slabs, 1-16 rows
 // (m_tile == kMfmaRows), the rows staged whole in LDS. mfma_stream_fits: K/G a multiple of the
 // waves and a wave's staging within its registers; mfma_stream_lds: its dynamic LDS bytes.

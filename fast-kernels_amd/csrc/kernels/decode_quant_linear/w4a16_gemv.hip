@@ -3,7 +3,8 @@
 // launch: 16-row m-tiles to the matrix-core kernels (w4a16_gemm_mfma.hip, or on the stream schedule
 // w4a16_gemm_mfma_stream.hip), native packet formats to w4a16_gemv_native.hip or, on the stream
 // schedule, w4a16_gemv_stream.hip; the fused decode-step neighbours to w4a16_gemv_fused.hip or, on
-// the stream schedule (one row), w4a16_gemv_stream.hip.
+// the stream schedule (one row), w4a16_gemv_stream.hip; one row over reference packets on the
+// stream schedule to w4a16_gemv_arc_stream.hip.
 #include "w4a16_gemv_kernels.h"
 
 namespace fk {
@@ -21,6 +22,9 @@ int gemv_partials_m_tile_for_batch(int batch) {
 }
 
 hipError_t launch_w4a16_gemv(const GemvLaunch& l, hipStream_t stream) {
+  if (l.stream && l.format == PacketFormat::kArc) {
+    return launch_w4a16_gemv_arc_stream(l, stream);
+  }
   if (l.fuse != GemvFuse::kNone) {
     return l.stream ? launch_w4a16_gemv_stream(l, stream) : launch_w4a16_gemv_fused(l, stream);
   }

@@ -66,9 +66,10 @@ __device__ __forceinline__ StreamRange stream_range(int b, int grid, int whole, 
   return r;
 }
 
-// Hands off piece pc (0 head, 1 tail) of workgroup b, slice `slice`: kPer values per lane, value i
-// being output o = lane + 64 i of the slice's rows x 32 outputs (o < n_out; output o is row
-// o / 32, column o % 32). Called by one wave. Slot size: slot_floats per (workgroup, piece).
+// Hands off piece pc (0 head, 1 tail) of workgroup b, slice `slice` (kCols columns: a 32-column
+// slice of native slabs, or a 128-column tile of reference packets): kPer values per lane, value
+// i being output o = lane + 64 i of the slice's rows x kCols outputs (o < n_out; output o is row
+// o / kCols, column o % kCols). Called by one wave. Slot size: slot_floats per (workgroup, piece).
 //
 // Hand-off without cache-wide fences (an agent-scope release writes back the whole L2 and costs
 // microseconds): the partials are agent-scope stores, which gfx950 writes through the XCD's L2 to
@@ -76,7 +77,7 @@ __device__ __forceinline__ StreamRange stream_range(int b, int grid, int whole, 
 // acknowledged there, and only then is the counter bumped. The last part's loads are agent-scope
 // too, so they miss the L2 and read the coherence point, after its counter bump has returned the
 // final count. Every part does the same, so whichever arrives last sees all parts' partials.
-template <Act A, int kPer>
+template <Act A, int kPer, int kCols = kSliceCols>
 __device__ __forceinline__ void stream_hand_off(const GemvParams& p, int b, int pc, int slice,
                                                 int grid, int whole, int slices, int nbs,
                                                 int n_out, int slot_floats, const float (&v)[kPer],
@@ -130,8 +131,8 @@ __device__ __forceinline__ void stream_hand_off(const GemvParams& p, int b, int 
   for (int i = 0; i < kPer; ++i) {
     const int o = lane + 64 * i;
     if (o < n_out) {
-      p.out[static_cast<size_t>(o / kSliceCols) * p.N + static_cast<size_t>(slice) * kSliceCols +
-            o % kSliceCols] = float_to_act_bits<A>(acc[i]);
+      p.out[static_cast<size_t>(o / kCols) * p.N + static_cast<size_t>(slice) * kCols +
+            o % kCols] = float_to_act_bits<A>(acc[i]);
     }
   }
   if (lane == 0) {

@@ -214,14 +214,18 @@ int m_tile_for_kernel(int batch, int kernel) {
 
 ArcW4A16Plan plan_arc_impl(int batch, int n, int k, int group_size, int activation_dtype,
                            int split_k_slices, int cu_count, int m_tile);
+bool arc_stream_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_size,
+                     int split_k_slices, int cu_count, bool cu_count_given);
 
 }  // namespace
 
 ArcW4A16Plan plan_arc_w4a16_for_cu_count(int batch, int n, int k, int group_size,
                                          int activation_dtype, int split_k_slices, int cu_count) {
   validate_dimensions(batch, n, k, group_size);
-  return plan_arc_impl(batch, n, k, group_size, activation_dtype, split_k_slices, cu_count,
-                       fk::gemv_m_tile_for_batch(batch));
+  ArcW4A16Plan plan = plan_arc_impl(batch, n, k, group_size, activation_dtype, split_k_slices,
+                                    cu_count, fk::gemv_m_tile_for_batch(batch));
+  arc_stream_plan(plan, batch, n, k, group_size, split_k_slices, cu_count, true);
+  return plan;
 }
 
 namespace {
@@ -371,6 +375,60 @@ bool stream_fused_enabled() {
   return enabled;
 }
 
+// FK_W4A16_ARC_STREAM=0 keeps one-row launches over the reference packets off the stream
+// schedule (w4a16_gemv_arc_stream.hip).
+bool arc_stream_enabled() {
+  static const bool enabled = env_enabled("FK_W4A16_ARC_STREAM");
+  return enabled;
+}
+
+// One row over the reference packets on the stream schedule: whole 128-column tiles per CU plus
+// pieces of the tiles left over (the native stream kernel's split, tiles for slices). Blocks are
+// 2 D groups (D = 2 at G = 128, 4 at G = 64). Only with at least one whole tile per CU: measured
+// on MI355X (bench.py --packets arc, alternating runs), 70B gate_up (448 tiles, one whole tile and
+// a piece per CU) 39.6 -> 39.1 us against the per-tile runs, while the shapes with fewer tiles than
+// CUs, all pieces, got slower (70B qkv 11.3 -> 13.2 us, o 8.4 -> 10.4, down 22.4 -> 23.4). False
+// (plan unchanged) when it does not apply.
+bool arc_stream_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_size,
+                     int split_k_slices, int cu_count, bool cu_count_given) {
+  if (batch != 1 || plan.m_tile != 1 || split_k_slices != 0 || k > fk::kStreamMaxK ||
+      !arc_stream_enabled()) {
+    return false;
+  }
+  const int num_groups = k / group_size;
+  const int per_block = group_size == 128 ? 4 : 8;
+  const std::size_t lds = fk::arc_stream_lds(group_size, k) + 16 * 1024;
+  const std::size_t lds_limit = cu_count_given ? kGfx950LdsBytes : device_lds_per_block();
+  if (num_groups % per_block != 0 || lds > lds_limit) {
+    return false;
+  }
+  const long long nbt = num_groups / per_block;
+  const long long tiles = n / fk::kTileCols;
+  const long long cus = cu_count;
+  const long long whole = tiles / cus;
+  const long long left = tiles - whole * cus;
+  const bool pieces = left > 0;
+  if (whole < 1 || tiles > fk::kStreamMaxSlices || (pieces && (left * nbt < cus ||
+                                                  left * nbt * cus >= (1LL << 31)))) {
+    return false;
+  }
+  plan.schedule = kScheduleStream;
+  plan.slice_cols = fk::kTileCols;
+  plan.workgroups = static_cast<int>(cus);
+  plan.stream_depth = group_size == 128 ? 2 : 4;
+  plan.stream_whole = static_cast<int>(whole);
+  plan.stream_pieces = pieces ? 1 : 0;
+  plan.stream_half = 0;
+  const long long piece_blocks = pieces ? (left * nbt + cus - 1) / cus : 0;
+  plan.groups_per_workgroup = static_cast<int>(whole * num_groups + piece_blocks * per_block);
+  plan.max_tile_contributors =
+      pieces ? static_cast<int>((nbt * cus + left * nbt - 1) / (left * nbt) + 1) : 1;
+  plan.workspace_bytes =
+      pieces ? kCounterRegionBytes + static_cast<std::size_t>(cus) * 2 * fk::kTileCols * sizeof(float)
+             : 0;
+  return true;
+}
+
 // The stream kernel with a fused neighbour (one row, w4a16_gemv_stream.hip's kFuse): whole units
 // per workgroup, a unit being a 32-column slice (RMSNorm prologue) or a gate slice with its up
 // slice (SiLU epilogue, up to 4 pairs per workgroup): over every CU when they divide, else over a
@@ -500,6 +558,9 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
         return plan;
       }
     }
+  }
+  if (format == fk::PacketFormat::kArc && plain && kernel != kKernelMfma) {
+    arc_stream_plan(plan, batch, n, k, group_size, split_k_slices, cu_count, cu_count_given);
   }
   if (format == fk::PacketFormat::kArc || plan.m_tile == fk::kMfmaRows) {
     return plan;  // the matrix-core kernel reads whole tiles in every format
@@ -731,6 +792,17 @@ void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::u
     l.slice_cols = fk::kSliceCols;
     l.slice_pair = true;
     l.units_per_workgroup = 2 * plan.groups_per_workgroup;
+  } else if (plan.schedule == kScheduleStream && format == fk::PacketFormat::kArc) {
+    if (batch != 1 || plan.m_tile != 1 || plan.slice_cols != fk::kTileCols ||
+        fuse != fk::GemvFuse::kNone) {
+      throw std::logic_error("stream schedule on a reference-packet plan it does not take");
+    }
+    l.stream = true;
+    l.slice_cols = fk::kTileCols;
+    l.stream_depth = plan.stream_depth;
+    l.stream_grid = plan.workgroups;
+    l.stream_whole = plan.stream_whole;
+    l.stream_pieces = plan.stream_pieces != 0;
   } else if (plan.schedule == kScheduleStream) {
     const int cols = plan.stream_half ? fk::kSliceCols / 2 : fk::kSliceCols;
     const bool rows_ok = plan.m_tile == fk::kMfmaRows ? batch <= fk::kMfmaRows : plan.m_tile == batch;

@@ -67,7 +67,7 @@ def _plan(lib, batch, n, k, g, act=0, split=0, cu=256):
 @pytest.mark.parametrize(
     "shape,want_runs_per_tile,want_slice_cols",
     [
-        ((1, 57344, 8192, 128), 1, 128),  # 448 tiles >= 128: whole tiles over all of K, no fix-up
+        ((1, 28672, 8192, 128), 1, 128),  # 224 tiles >= 128: whole tiles over all of K, no fix-up
         ((1, 10240, 8192, 128), 1, 64),   # 80 tiles -> 160 64-column slices
         ((1, 8192, 8192, 128), 1, 32),    # 64 tiles -> 256 32-column slices
         ((1, 8192, 28672, 128), 4, 128),  # 224 groups: runs of 56 groups, 256 workgroups
@@ -247,7 +247,9 @@ def test_native_plan_policy_without_gpu(lib: ctypes.CDLL, shape, want) -> None:
     assert lib.fk_w4a16_plan_for_format(batch, n, k, g, 0, 0, 256, 0, ctypes.byref(arc)) == 0
     rc, ref = _plan(lib, batch, n, k, g)
     assert rc == 0 and (arc.slice_cols, arc.workgroups) == (ref.slice_cols, ref.workgroups)
-    assert arc.schedule == 0
+    # reference packets: per-tile runs, or the stream schedule with a whole tile per CU, from
+    # either planning entry point
+    assert arc.schedule == ref.schedule == (2 if n // 128 >= 256 and batch == 1 else 0)
     # a fix-up needs a workspace exactly when slices are shared (runs that do not cover whole
     # slices, or stream pieces)
     assert (p.workspace_bytes > 0) == (p.max_tile_contributors > 1)
@@ -341,3 +343,28 @@ def test_automatic_plans_fit_the_noalloc_scratch(lib: ctypes.CDLL) -> None:
                             if p.workspace_bytes > worst[0]:
                                 worst = (p.workspace_bytes, (batch, n, k, g, fmt, cu))
     assert worst[0] <= NOALLOC_SCRATCH_BYTES, worst
+
+
+@pytest.mark.parametrize(
+    "n,k,g,whole_groups,piece_groups",
+    [
+        (57344, 8192, 128, 64, 48),   # 448 tiles: one whole tile + 192 tiles x 16 blocks / 256 CUs
+        (32768, 4096, 128, 32, 0),    # 256 tiles: one whole tile each, no pieces
+        (65536, 8192, 128, 128, 0),   # two whole tiles each
+        (40960, 2048, 64, 32, 8),     # G = 64: blocks of 8 groups; 64 tiles x 4 blocks / 256
+    ],
+)
+def test_reference_packet_stream_plan_without_gpu(lib: ctypes.CDLL, n, k, g, whole_groups,
+                                                  piece_groups) -> None:
+    """One row over reference packets with at least one whole 128-column tile per CU takes the
+    stream schedule (whole tiles + pieces of the tiles left over); fewer tiles keep the runs."""
+    rc, p = _plan(lib, 1, n, k, g)
+    assert rc == 0
+    assert (p.schedule, p.slice_cols, p.workgroups) == (2, 128, 256)
+    assert p.groups_per_workgroup == whole_groups + piece_groups
+    if piece_groups:
+        assert p.workspace_bytes == 65536 + 256 * 2 * 128 * 4
+    else:
+        assert p.workspace_bytes == 0 and p.max_tile_contributors == 1
+    rc, p = _plan(lib, 1, 10240, 8192, 128)  # 80 tiles: per-tile runs
+    assert rc == 0 and p.schedule == 0

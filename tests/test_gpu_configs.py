@@ -330,3 +330,39 @@ def test_mfma_stream_variants(m: int, n: int, k: int, g: int, act: str, asym: bo
     np.testing.assert_array_equal(ys[0], ys[2])
     rows = _rows(n)
     _assert_gemv_close(ys[0][:, rows], _oracle_rows(case, rows, act), case, f"mfma stream {plan}")
+
+
+@pytest.mark.parametrize(
+    "n,k,g,act",
+    [
+        (32768, 4096, 128, "f16"),   # 256 tiles: one whole tile per CU, no pieces
+        (65536, 8192, 128, "bf16"),  # two whole tiles per CU
+        (57344, 8192, 128, "bf16"),  # 70B gate_up: a whole tile and a piece of one per CU
+        (40960, 2048, 64, "bf16"),   # G = 64 (blocks of 8 groups), pieces of a quarter tile
+        (36864, 16384, 64, "f16"),   # G = 64, longer K (more staging passes), pieces
+    ],
+)
+def test_reference_packets_stream_schedule(n: int, k: int, g: int, act: str) -> None:
+    """The reference signature (arc_w4a16_forward, arc_w4a16.cu:687-707) over the reference
+    packets on the stream schedule (w4a16_gemv_arc_stream.hip: whole 128-column tiles per CU plus
+    pieces): sampled rows against the oracle, and identical bits over three calls."""
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the shapes are chosen for 256 CUs")
+    from fast_kernels.ops import arc_w4a16_forward
+
+    case = make_case(1, n, k, g, act=act, asymmetric=True, seed=n + k + g)
+    x, q, a, b = _upload(case)
+    packets = pack_arc_w4a16_packets(q, a, b, group_size=g)
+    plan = arc_w4a16_plan(batch=1, n=n, k=k, group_size=g, activation_dtype=x.dtype,
+                          packet_format=0)
+    assert plan["schedule"] == 2 and plan["slice_cols"] == 128, plan
+    outs = []
+    for _ in range(3):
+        y = arc_w4a16_forward(x, packets, n=n, k=k, group_size=g)
+        torch.cuda.synchronize()
+        outs.append(_bits(y))
+    rows = _rows(n)
+    _assert_gemv_close(outs[0][:, rows], _oracle_rows(case, rows, act), case,
+                       f"reference packets, stream schedule, {n}x{k} G{g} {act} plan={plan}")
+    np.testing.assert_array_equal(outs[1], outs[0])
+    np.testing.assert_array_equal(outs[2], outs[0])
