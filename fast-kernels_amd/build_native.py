@@ -30,6 +30,7 @@ LIB_SOURCES = [
     CSRC / "kernels" / "decode_quant_linear" / "w4a16_gemv_native.hip",
     CSRC / "kernels" / "decode_quant_linear" / "w4a16_gemv_stream.hip",
     CSRC / "kernels" / "decode_quant_linear" / "w4a16_gemv_arc_stream.hip",
+    CSRC / "kernels" / "decode_quant_linear" / "w4a16_gemv_arc_quarter.hip",
     CSRC / "kernels" / "decode_quant_linear" / "w4a16_gemv_fused.hip",
     CSRC / "kernels" / "decode_quant_linear" / "w4a16_gemm_mfma.hip",
     CSRC / "kernels" / "decode_quant_linear" / "w4a16_gemm_mfma_stream.hip",

@@ -114,6 +114,7 @@ struct GemvParams {
   float eps;                        // RMSNorm prologue: epsilon
   int pair;                         // native slabs: each run streams two adjacent whole slices
   int stream_whole;                 // stream schedule: whole slices per workgroup
+  uint32_t ng_magic;                // quarter schedule over reference packets: floor(2^32/NG) + 1
 };
 
 template <int G, int MT, int CW>

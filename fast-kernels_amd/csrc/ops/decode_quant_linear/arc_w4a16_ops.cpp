@@ -216,6 +216,8 @@ ArcW4A16Plan plan_arc_impl(int batch, int n, int k, int group_size, int activati
                            int split_k_slices, int cu_count, int m_tile);
 bool arc_stream_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_size,
                      int split_k_slices, int cu_count, bool cu_count_given);
+bool arc_quarter_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_size,
+                      int split_k_slices, int cu_count, bool cu_count_given);
 
 }  // namespace
 
@@ -224,7 +226,9 @@ ArcW4A16Plan plan_arc_w4a16_for_cu_count(int batch, int n, int k, int group_size
   validate_dimensions(batch, n, k, group_size);
   ArcW4A16Plan plan = plan_arc_impl(batch, n, k, group_size, activation_dtype, split_k_slices,
                                     cu_count, fk::gemv_m_tile_for_batch(batch));
-  arc_stream_plan(plan, batch, n, k, group_size, split_k_slices, cu_count, true);
+  if (!arc_stream_plan(plan, batch, n, k, group_size, split_k_slices, cu_count, true)) {
+    arc_quarter_plan(plan, batch, n, k, group_size, split_k_slices, cu_count, true);
+  }
   return plan;
 }
 
@@ -429,6 +433,82 @@ bool arc_stream_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_size
   return true;
 }
 
+// FK_W4A16_ARC_QUARTER=0 keeps one-row launches over the reference packets off the quarter
+// schedule (w4a16_gemv_arc_quarter.hip).
+bool arc_quarter_enabled() {
+  static const bool enabled = env_enabled("FK_W4A16_ARC_QUARTER");
+  return enabled;
+}
+
+// One row over the reference packets by 32-column quarters of the packets, for the shapes with
+// fewer 128-column tiles than CUs (the whole-tile stream schedule, arc_stream_plan, takes the
+// others: 70B gate_up 39.7 us on it against 41.0 by quarters). The slices are dealt like the
+// native stream kernel's: whole slices per CU when they divide, pieces of the slices left over
+// when there are more slices than CUs and K is long (K/G >= 64), a divisor grid of at least 7/8
+// of the CUs, or one slice per workgroup when there are fewer slices than CUs and the per-tile
+// runs would not split K either. Blocks are 8 waves x D groups (D = 2 at G = 128, 4 at G = 64).
+// Measured on MI355X (bench.py --packets arc, alternating runs against the per-tile runs): 70B
+// qkv 11.4 -> 10.0 us, o 8.4 -> 7.7, down 22.4 -> 21.8; 7B o 5.06 -> 4.24. False (plan
+// unchanged) when it does not apply.
+bool arc_quarter_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_size,
+                      int split_k_slices, int cu_count, bool cu_count_given) {
+  if (batch != 1 || plan.m_tile != 1 || split_k_slices != 0 || k > fk::kStreamMaxK ||
+      !arc_quarter_enabled()) {
+    return false;
+  }
+  const int num_groups = k / group_size;
+  const int depth = group_size == 128 ? 2 : 4;
+  const int per_block = fk::kStreamWaves * depth;
+  const std::size_t lds = fk::arc_quarter_lds(group_size, k) + fk::kStreamStaticLdsBytes;
+  const std::size_t lds_limit = cu_count_given ? kGfx950LdsBytes : device_lds_per_block();
+  const long long slices = n / fk::kSliceCols;
+  if (num_groups % per_block != 0 || lds > lds_limit || slices > fk::kStreamMaxSlices ||
+      !fk::arc_quarter_magic_exact(num_groups, slices)) {
+    return false;
+  }
+  constexpr int kMinPieceGroups = 64;
+  const long long nbs = num_groups / per_block;
+  const long long cus = cu_count;
+  const long long left = slices % cus;
+  long long grid = 0;
+  int whole = 0;
+  bool pieces = false;
+  if (slices >= cus && left == 0) {
+    grid = cus;
+    whole = static_cast<int>(slices / cus);
+  } else if (slices > cus && left * nbs >= cus && num_groups >= kMinPieceGroups &&
+             left * nbs * cus < (1LL << 31)) {
+    grid = cus;
+    whole = static_cast<int>(slices / cus);
+    pieces = true;
+  } else if (const long long dgrid = divisor_grid(slices, cus); dgrid > 0) {
+    grid = dgrid;
+    whole = static_cast<int>(slices / dgrid);
+  } else if (slices < cus && plan.groups_per_workgroup == num_groups) {
+    grid = slices;
+    whole = 1;
+  } else {
+    return false;
+  }
+  plan.schedule = kScheduleStream;
+  plan.slice_cols = fk::kSliceCols;
+  plan.workgroups = static_cast<int>(grid);
+  plan.stream_depth = depth;
+  plan.stream_whole = whole;
+  plan.stream_pieces = pieces ? 1 : 0;
+  plan.stream_half = 0;
+  const long long left_blocks = (slices - grid * whole) * nbs;
+  const long long piece_blocks = pieces ? (left_blocks + grid - 1) / grid : 0;
+  plan.groups_per_workgroup = static_cast<int>(whole * num_groups + piece_blocks * per_block);
+  plan.max_tile_contributors =
+      pieces ? static_cast<int>((nbs * grid + left_blocks - 1) / left_blocks + 1) : 1;
+  plan.workspace_bytes =
+      pieces ? kCounterRegionBytes +
+                   fk::stream_partial_floats(static_cast<int>(grid), 1) * sizeof(float)
+             : 0;
+  return true;
+}
+
 // The stream kernel with a fused neighbour (one row, w4a16_gemv_stream.hip's kFuse): whole units
 // per workgroup, a unit being a 32-column slice (RMSNorm prologue) or a gate slice with its up
 // slice (SiLU epilogue, up to 4 pairs per workgroup): over every CU when they divide, else over a
@@ -559,8 +639,9 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
       }
     }
   }
-  if (format == fk::PacketFormat::kArc && plain && kernel != kKernelMfma) {
-    arc_stream_plan(plan, batch, n, k, group_size, split_k_slices, cu_count, cu_count_given);
+  if (format == fk::PacketFormat::kArc && plain && kernel != kKernelMfma &&
+      !arc_stream_plan(plan, batch, n, k, group_size, split_k_slices, cu_count, cu_count_given)) {
+    arc_quarter_plan(plan, batch, n, k, group_size, split_k_slices, cu_count, cu_count_given);
   }
   if (format == fk::PacketFormat::kArc || plan.m_tile == fk::kMfmaRows) {
     return plan;  // the matrix-core kernel reads whole tiles in every format
@@ -793,12 +874,14 @@ void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::u
     l.slice_pair = true;
     l.units_per_workgroup = 2 * plan.groups_per_workgroup;
   } else if (plan.schedule == kScheduleStream && format == fk::PacketFormat::kArc) {
-    if (batch != 1 || plan.m_tile != 1 || plan.slice_cols != fk::kTileCols ||
+    if (batch != 1 || plan.m_tile != 1 ||
+        (plan.slice_cols != fk::kTileCols && plan.slice_cols != fk::kSliceCols) ||
         fuse != fk::GemvFuse::kNone) {
       throw std::logic_error("stream schedule on a reference-packet plan it does not take");
     }
     l.stream = true;
-    l.slice_cols = fk::kTileCols;
+    l.slice_cols = plan.slice_cols;
+    l.ng_magic = fk::arc_quarter_magic(k / group_size);
     l.stream_depth = plan.stream_depth;
     l.stream_grid = plan.workgroups;
     l.stream_whole = plan.stream_whole;

@@ -67,15 +67,16 @@ def _plan(lib, batch, n, k, g, act=0, split=0, cu=256):
 @pytest.mark.parametrize(
     "shape,want_runs_per_tile,want_slice_cols",
     [
-        ((1, 28672, 8192, 128), 1, 128),  # 224 tiles >= 128: whole tiles over all of K, no fix-up
-        ((1, 10240, 8192, 128), 1, 64),   # 80 tiles -> 160 64-column slices
-        ((1, 8192, 8192, 128), 1, 32),    # 64 tiles -> 256 32-column slices
-        ((1, 8192, 28672, 128), 4, 128),  # 224 groups: runs of 56 groups, 256 workgroups
-        ((1, 4096, 4096, 128), 1, 32),    # 32 tiles -> 128 slices, no K split
+        ((1, 10240, 4096, 128), 1, 64),   # 80 tiles -> 160 64-column slices
+        ((1, 12288, 4096, 128), 1, 64),   # 96 tiles -> 192 64-column slices
+        ((1, 22016, 4096, 128), 1, 128),  # 172 tiles: whole tiles over all of K, no fix-up
         ((1, 4096, 14336, 128), 2, 32),   # 112 groups: runs of 56, 4 slices -> 256 workgroups
+        ((1, 1024, 16384, 128), 2, 32),   # 32 slices, runs of 64 groups -> 64 workgroups
     ],
 )
 def test_plan_policy_without_gpu(lib: ctypes.CDLL, shape, want_runs_per_tile, want_slice_cols) -> None:
+    """One row over the reference packets where neither stream schedule applies (K/G below 64
+    with slices that do not divide over the CUs, or per-tile runs that split K): per-tile runs."""
     batch, n, k, g = shape
     rc, p = _plan(lib, batch, n, k, g)
     assert rc == 0
@@ -247,9 +248,15 @@ def test_native_plan_policy_without_gpu(lib: ctypes.CDLL, shape, want) -> None:
     assert lib.fk_w4a16_plan_for_format(batch, n, k, g, 0, 0, 256, 0, ctypes.byref(arc)) == 0
     rc, ref = _plan(lib, batch, n, k, g)
     assert rc == 0 and (arc.slice_cols, arc.workgroups) == (ref.slice_cols, ref.workgroups)
-    # reference packets: per-tile runs, or the stream schedule with a whole tile per CU, from
-    # either planning entry point
-    assert arc.schedule == ref.schedule == (2 if n // 128 >= 256 and batch == 1 else 0)
+    # reference packets, from either planning entry point: per-tile runs, the whole-tile stream
+    # schedule with a whole tile per CU, or (one row, fewer tiles) the quarter schedule
+    assert arc.schedule == ref.schedule
+    if batch != 1:
+        assert arc.schedule == 0
+    elif n // 128 >= 256:
+        assert (arc.schedule, arc.slice_cols) == (2, 128)
+    elif arc.schedule == 2:
+        assert arc.slice_cols == 32
     # a fix-up needs a workspace exactly when slices are shared (runs that do not cover whole
     # slices, or stream pieces)
     assert (p.workspace_bytes > 0) == (p.max_tile_contributors > 1)
@@ -357,7 +364,8 @@ def test_automatic_plans_fit_the_noalloc_scratch(lib: ctypes.CDLL) -> None:
 def test_reference_packet_stream_plan_without_gpu(lib: ctypes.CDLL, n, k, g, whole_groups,
                                                   piece_groups) -> None:
     """One row over reference packets with at least one whole 128-column tile per CU takes the
-    stream schedule (whole tiles + pieces of the tiles left over); fewer tiles keep the runs."""
+    stream schedule (whole tiles + pieces of the tiles left over); fewer tiles take the quarter
+    schedule where it applies, else the runs."""
     rc, p = _plan(lib, 1, n, k, g)
     assert rc == 0
     assert (p.schedule, p.slice_cols, p.workgroups) == (2, 128, 256)
@@ -366,5 +374,32 @@ def test_reference_packet_stream_plan_without_gpu(lib: ctypes.CDLL, n, k, g, who
         assert p.workspace_bytes == 65536 + 256 * 2 * 128 * 4
     else:
         assert p.workspace_bytes == 0 and p.max_tile_contributors == 1
-    rc, p = _plan(lib, 1, 10240, 8192, 128)  # 80 tiles: per-tile runs
+    rc, p = _plan(lib, 1, 10240, 4096, 128)  # 80 tiles, 32 groups: per-tile runs
     assert rc == 0 and p.schedule == 0
+
+
+@pytest.mark.parametrize(
+    "n,k,g,want",
+    [
+        # (workgroups, groups per workgroup, fix-up workspace) on 256 CUs
+        ((28672), 8192, 128, (256, 3 * 64 + 32, True)),  # 896 slices: 3 whole + pieces of 128
+        (10240, 8192, 128, (256, 64 + 16, True)),          # 70B qkv: a slice and a block
+        (8192, 8192, 128, (256, 64, False)),               # 70B o
+        (8192, 28672, 128, (256, 224, False)),             # 70B down
+        (4096, 4096, 128, (128, 32, False)),               # 7B o: one slice each, K not split
+        (14336, 4096, 128, (224, 64, False)),              # divisor grid (7/8 of the CUs)
+        (10240, 8192, 64, (256, 128 + 32, True)),          # G = 64: blocks of 32 groups
+    ],
+)
+def test_reference_packet_quarter_plan_without_gpu(lib: ctypes.CDLL, n, k, g, want) -> None:
+    """One row over reference packets with fewer whole 128-column tiles than CUs takes the
+    quarter schedule (32-column quarters of the packets on the native stream split); shapes with
+    a whole tile per CU keep the whole-tile stream schedule."""
+    rc, p = _plan(lib, 1, n, k, g)
+    assert rc == 0
+    assert (p.schedule, p.slice_cols, p.m_tile) == (2, 32, 1)
+    assert (p.workgroups, p.groups_per_workgroup, p.workspace_bytes > 0) == want
+    if want[2]:
+        assert p.workspace_bytes == 65536 + p.workgroups * 2 * 32 * 4
+    rc, p = _plan(lib, 1, 57344, 8192, 128)
+    assert rc == 0 and (p.schedule, p.slice_cols) == (2, 128)

@@ -366,3 +366,45 @@ def test_reference_packets_stream_schedule(n: int, k: int, g: int, act: str) -> 
                        f"reference packets, stream schedule, {n}x{k} G{g} {act} plan={plan}")
     np.testing.assert_array_equal(outs[1], outs[0])
     np.testing.assert_array_equal(outs[2], outs[0])
+
+
+@pytest.mark.parametrize(
+    "n,k,g,act,want",
+    [
+        # n, k, G, activation, (workgroups, groups per workgroup, fix-up workspace) on 256 CUs
+        (8192, 8192, 128, "bf16", (256, 64, False)),    # 70B o: one 32-column slice per CU
+        (10240, 8192, 128, "bf16", (256, 80, True)),    # 70B qkv: a slice and a piece per CU
+        (8192, 28672, 128, "bf16", (256, 224, False)),  # 70B down: seven staging passes
+        (4096, 4096, 128, "f16", (128, 32, False)),     # 7B o: fewer slices than CUs, one each
+        (14336, 4096, 128, "f16", (224, 64, False)),    # divisor grid: 448 slices on 224 CUs
+        (16384, 4096, 64, "f16", (256, 128, False)),    # G = 64: blocks of 32 groups
+        (10240, 8192, 64, "bf16", (256, 160, True)),    # G = 64 with pieces
+    ],
+)
+def test_reference_packets_quarter_schedule(n: int, k: int, g: int, act: str, want) -> None:
+    """The reference signature (arc_w4a16_forward, arc_w4a16.cu:687-707) over the reference
+    packets by 32-column quarters of the packets (w4a16_gemv_arc_quarter.hip), asymmetric packets
+    (any fp16 beta): sampled rows against the oracle (every row for 7B o), identical bits over
+    three calls."""
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the shapes are chosen for 256 CUs")
+    from fast_kernels.ops import arc_w4a16_forward
+
+    case = make_case(1, n, k, g, act=act, asymmetric=True, seed=3 * n + k + g)
+    x, q, a, b = _upload(case)
+    packets = pack_arc_w4a16_packets(q, a, b, group_size=g)
+    plan = arc_w4a16_plan(batch=1, n=n, k=k, group_size=g, activation_dtype=x.dtype,
+                          packet_format=0)
+    assert plan["schedule"] == 2 and plan["slice_cols"] == 32, plan
+    got = (plan["workgroups"], plan["groups_per_workgroup"], plan["workspace_bytes"] > 0)
+    assert got == want, plan
+    outs = []
+    for _ in range(3):
+        y = arc_w4a16_forward(x, packets, n=n, k=k, group_size=g)
+        torch.cuda.synchronize()
+        outs.append(_bits(y))
+    rows = np.arange(n) if n * k <= 4096 * 4096 else _rows(n)
+    _assert_gemv_close(outs[0][:, rows], _oracle_rows(case, rows, act), case,
+                       f"reference packets, quarter schedule, {n}x{k} G{g} {act} plan={plan}")
+    np.testing.assert_array_equal(outs[1], outs[0])
+    np.testing.assert_array_equal(outs[2], outs[0])
