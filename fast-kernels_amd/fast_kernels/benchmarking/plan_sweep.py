@@ -11,7 +11,9 @@ backs the table. Candidates per shape:
   * the plans the table's switches select when one rule is turned off (FK_W4A16_STREAM=0: no
     stream schedule at all; _PIECES, _DIVISOR, _HALF, _HALF_WHOLE, _SMALL = 0: one of its
     fallbacks off; FK_W4A16_STREAM_WPC=2: two workgroups per CU; FK_W4A16_MFMA_STREAM=0: the
-    small-batch matrix cores off the stream schedule);
+    small-batch matrix cores off the stream schedule; FK_W4A16_ARC_QUARTER=0 and
+    FK_W4A16_ARC_STREAM=0: the reference packets off the quarter or the whole-tile stream
+    schedule);
   * forced K splits (``split_k_slices`` 1, 2, 4, 8: per-slice runs over that many K ranges);
   * for several rows, each kernel choice (dot2 loop, matrix cores).
 
@@ -79,6 +81,8 @@ ENVS: dict[str, dict[str, str]] = {
     "no_small": {"FK_W4A16_STREAM_SMALL": "0"},
     "wpc2": {"FK_W4A16_STREAM_WPC": "2"},
     "no_mfma_stream": {"FK_W4A16_MFMA_STREAM": "0"},
+    "no_arc_quarter": {"FK_W4A16_ARC_QUARTER": "0"},
+    "no_arc_stream": {"FK_W4A16_ARC_STREAM": "0"},
 }
 SPLITS = (1, 2, 3, 4, 6, 8, 16)
 KERNELS = {"auto": 0, "dot2": 1, "mfma": 2}
