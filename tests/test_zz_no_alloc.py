@@ -78,9 +78,11 @@ LARGE = (1, 4096, 14336, 64, "bf16", 1)    # 128 slices, two runs of 112 groups 
 SMALL = (1, 1024, 8192, 64, "f16", 2)      # 32 slices, K split in four, asymmetric slabs
 BATCHED = (8, 8192, 4096, 64, "f16", 0)    # matrix cores over reference packets, 4.5 MB scratch
 TAIL = (1, 10240, 8192, 128, "bf16", 1)    # stream schedule: a quarter of a left-over slice per CU
+ARC_TAIL = (1, 10240, 8192, 128, "bf16", 0)  # reference packets by 32-column quarters, pieces
 
 
-@pytest.mark.parametrize("order", [(LARGE, SMALL), (BATCHED, LARGE), (SMALL, BATCHED), (TAIL, LARGE)])
+@pytest.mark.parametrize("order", [(LARGE, SMALL), (BATCHED, LARGE), (SMALL, BATCHED), (TAIL, LARGE),
+                                   (ARC_TAIL, SMALL)])
 def test_noalloc_matches_forward_native_two_calls(order) -> None:
     lib = _lib()
     for shape in order:
