@@ -56,3 +56,22 @@ def test_step_rotations_keep_copies_cold_at_graph_restarts(chunk, r_min, min_chu
         if c in last:
             assert i - last[c] >= min_chunk, (chunk, r, i, c)
         last[c] = i
+
+
+def test_hbm_read_floor_probe_builds_for_gfx950(tmp_path) -> None:
+    """The streaming-read probe behind the read floor (fast-kernels_amd/benchmarks/hbm_read_floor.hip,
+    the source of the floor figures in the profiles) compiles for gfx950 with the library's flags,
+    so the figures can be reproduced from the committed source."""
+    import shutil
+    import subprocess
+
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(hipcc).exists():
+        pytest.skip("hipcc is not installed")
+    src = Path(__file__).resolve().parents[1] / "fast-kernels_amd" / "benchmarks" / "hbm_read_floor.hip"
+    out = tmp_path / "hbm_read_floor.o"
+    proc = subprocess.run([hipcc, "--offload-arch=gfx950", "-O3", "-Xclang", "-target-feature",
+                           "-Xclang", "-packed-fp32-ops", "-c", str(src), "-o", str(out)],
+                          capture_output=True, text=True, timeout=600)
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    assert out.stat().st_size > 0
