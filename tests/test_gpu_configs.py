@@ -198,29 +198,44 @@ def test_config4_llama8b_decode_step_graph() -> None:
             np.testing.assert_array_equal(got, eager[(layer, name)])
 
 
-def test_config2_layer_graph_replays_match_eager() -> None:
-    """The 70B layer (its qkv takes pieces with a counter hand-off, the other three whole slices)
-    captured in one HIP graph: four replays, with eager work and synchronisations between them,
-    each bit-identical to the eager call (the counters the pieces leave behind are zero)."""
+@pytest.mark.parametrize("packets", ["native_sym", "arc"])
+def test_config2_layer_graph_replays_match_eager(packets: str) -> None:
+    """The 70B layer captured in one HIP graph (native slabs: qkv takes pieces with a counter
+    hand-off, the other three whole slices; reference packets: qkv pieces of packet quarters,
+    gate_up whole tiles with pieces): four replays, with eager work and synchronisations between
+    them, each bit-identical to the eager call (the counters the pieces leave behind are zero)."""
     if torch.cuda.get_device_properties(0).multi_processor_count != 256:
         pytest.skip("the plans are chosen for 256 CUs")
+    from fast_kernels.ops import arc_w4a16_forward
+
     dev = torch.device(DEV)
-    slabs, xs, outs = {}, {}, {}
+    weights, xs, outs = {}, {}, {}
     for name, n, k in LLAMA70B:
         q, alpha, beta = layer_weights(torch, dev, n, k, 128, 7)
         arc = pack_arc_w4a16_packets(q, alpha, beta, group_size=128)
-        slabs[name] = convert_arc_to_native_packets(arc, n=n, k=k, group_size=128)
+        weights[name] = (arc if packets == "arc"
+                         else convert_arc_to_native_packets(arc, n=n, k=k, group_size=128))
         del arc, q, alpha, beta
         xs[name] = torch.randn((1, k), device=dev).to(torch.bfloat16)
         outs[name] = torch.empty((1, n), device=dev, dtype=torch.bfloat16)
+    for n in (10240, 57344):
+        plan = arc_w4a16_plan(batch=1, n=n, k=8192, group_size=128,
+                              activation_dtype=torch.bfloat16,
+                              packet_format=0 if packets == "arc" else 1)
+        assert plan["schedule"] == 2, plan
     plan = arc_w4a16_plan(batch=1, n=10240, k=8192, group_size=128,
-                          activation_dtype=torch.bfloat16, packet_format=1)
-    assert plan["schedule"] == 2 and plan["workspace_bytes"] > 0, plan
+                          activation_dtype=torch.bfloat16,
+                          packet_format=0 if packets == "arc" else 1)
+    assert plan["workspace_bytes"] > 0, plan
 
     def layer() -> None:
         for name, n, k in LLAMA70B:
-            arc_w4a16_forward_native(xs[name], slabs[name], n=n, k=k, group_size=128,
-                                     packet_format="native_sym", output=outs[name])
+            if packets == "arc":
+                arc_w4a16_forward(xs[name], weights[name], n=n, k=k, group_size=128,
+                                  output=outs[name])
+            else:
+                arc_w4a16_forward_native(xs[name], weights[name], n=n, k=k, group_size=128,
+                                         packet_format="native_sym", output=outs[name])
 
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
