@@ -702,6 +702,7 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
   // (K/G = 64) 11.9 -> 10.6 us, but 8B gate_up (K/G = 32) 12.6 -> 13.2 us against slice pairs and
   // 7B gate_up 10.5 -> 11.9 us against per-slice runs.
   constexpr int kMinPieceGroups = 64;
+  constexpr long long kLargeSlicesPerCu = 4;
   if (plain && split_k_slices == 0 && batch == 1 && plan.m_tile == 1 &&
       k <= fk::kStreamMaxK && stream_schedule_enabled()) {
     const std::size_t lds =
@@ -719,7 +720,16 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
       bool pieces = false;
       bool half = false;
       const long long left = slices % cus;
-      if (exact && slices >= cus && left == 0) {
+      // Many slices per CU: a divisor grid of 7/8 of the CUs or more when one exists, ahead of
+      // every CU (70B gate_up, 1792 slices: 8 per workgroup on 224 CUs 37.0 us against 7 on 256
+      // 37.6-38.1, the 70B step 74.3 -> 73.25 us; alternating runs on one GPU). Shapes with one
+      // slice per CU measured slower on fewer CUs (70B o, down and qkv on 192-224 workgroups).
+      const long long dgrid_large =
+          exact && slices >= kLargeSlicesPerCu * cus ? divisor_grid(slices, cus - 1) : 0;
+      if (dgrid_large > 0) {
+        grid = dgrid_large;
+        whole = static_cast<int>(slices / dgrid_large);
+      } else if (exact && slices >= cus && left == 0) {
         grid = cus;
         whole = static_cast<int>(slices / cus);
       } else if (exact && slices > cus && left * nbs >= cus && num_groups >= kMinPieceGroups &&

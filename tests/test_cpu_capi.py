@@ -223,7 +223,7 @@ def test_native_format_validation_without_gpu(lib: ctypes.CDLL) -> None:
         ((1, 22016, 4096, 128), (32, 32, 688, 0)),     # 7B gate_up: 344 pairs would fill 2 rounds unevenly
         ((2, 12288, 4096, 128), (32, 32, 384, 0)),     # pairs and stream for one row only
         ((4, 12288, 4096, 128), (32, 48, 256, 2)),     # four rows: matrix cores on the stream schedule
-        ((1, 57344, 8192, 128), (32, 448, 256, 2)),    # 70B gate_up: 7 whole slices per CU
+        ((1, 57344, 8192, 128), (32, 512, 224, 2)),    # 70B gate_up: 8 whole slices on 224 CUs
         ((1, 8192, 28672, 128), (32, 224, 256, 2)),    # 70B down: one slice of 224 groups per CU
         ((1, 8192, 28672 + 128, 128), (16, 450, 256, 2)),  # 225 groups: 2 half slices per CU,
                                                            # the last block of each partial

@@ -176,7 +176,7 @@ def test_forward_native_matches_reference_packets(asym, group_size, batch, act) 
         ((1, 1024, 2048, 128), "f16", False, 16),    # 32 slices, a half slice per workgroup
         ((1, 10240, 4096, 128), "f16", True, 64),    # 320 slices in 160 slice pairs
         ((1, 4096, 14336, 128), "bf16", False, 16),  # 128 slices, a half slice per workgroup
-        ((1, 57344, 8192, 128), "bf16", False, 32),  # Llama-70B gate_up, four slices per workgroup
+        ((1, 57344, 8192, 128), "bf16", False, 32),  # Llama-70B gate_up, eight slices on 224 CUs
         ((1, 8192, 28672, 128), "bf16", False, 32),  # Llama-70B down: long K, runs of 112 (fix-up)
         ((1, 12288, 1024, 64), "f16", False, 64),    # slice pairs over 16 groups
         ((1, 28672, 4096, 128), "bf16", True, 32),   # Llama-8B gate_up: 4 slices per CU on 224 CUs
