@@ -387,7 +387,8 @@ bool arc_stream_enabled() {
 }
 
 // One row over the reference packets on the stream schedule: whole 128-column tiles per CU plus
-// pieces of the tiles left over (the native stream kernel's split, tiles for slices). Blocks are
+// pieces of the tiles left over (the native stream kernel's split, tiles for slices), or whole
+// tiles only over a divisor grid of at least 7/8 of the CUs when one exists. Blocks are
 // 2 D groups (D = 2 at G = 128, 4 at G = 64). Only with at least one whole tile per CU: measured
 // on MI355X (bench.py --packets arc, alternating runs), 70B gate_up (448 tiles, one whole tile and
 // a piece per CU) 39.6 -> 39.1 us against the per-tile runs, while the shapes with fewer tiles than
@@ -408,7 +409,14 @@ bool arc_stream_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_size
   }
   const long long nbt = num_groups / per_block;
   const long long tiles = n / fk::kTileCols;
-  const long long cus = cu_count;
+  // Tiles that do not divide over the CUs but over a divisor grid of at least 7/8 of them: that
+  // grid, whole tiles only (70B gate_up, 448 tiles: 2 per workgroup on 224 CUs 37.8-38.1 us
+  // against 1 tile and pieces on 256 CUs 39.3-39.4, and 40.9-41.4 by packet quarters, 8 per
+  // workgroup on 224 CUs; alternating runs on one GPU).
+  long long cus = cu_count;
+  if (const long long dgrid = divisor_grid(tiles, cus); dgrid > 0 && tiles % cus != 0) {
+    cus = dgrid;
+  }
   const long long whole = tiles / cus;
   const long long left = tiles - whole * cus;
   const bool pieces = left > 0;

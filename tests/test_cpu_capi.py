@@ -353,22 +353,24 @@ def test_automatic_plans_fit_the_noalloc_scratch(lib: ctypes.CDLL) -> None:
 
 
 @pytest.mark.parametrize(
-    "n,k,g,whole_groups,piece_groups",
+    "n,k,g,grid,whole_groups,piece_groups",
     [
-        (57344, 8192, 128, 64, 48),   # 448 tiles: one whole tile + 192 tiles x 16 blocks / 256 CUs
-        (32768, 4096, 128, 32, 0),    # 256 tiles: one whole tile each, no pieces
-        (65536, 8192, 128, 128, 0),   # two whole tiles each
-        (40960, 2048, 64, 32, 8),     # G = 64: blocks of 8 groups; 64 tiles x 4 blocks / 256
+        (57344, 8192, 128, 224, 128, 0),  # 448 tiles: two whole tiles each on 224 CUs
+        (49152, 8192, 128, 256, 64, 32),  # 384 tiles: one whole tile + 128 tiles x 16 blocks / 256
+        (32768, 4096, 128, 256, 32, 0),   # 256 tiles: one whole tile each, no pieces
+        (65536, 8192, 128, 256, 128, 0),  # two whole tiles each
+        (40960, 2048, 64, 256, 32, 8),    # G = 64: blocks of 8 groups; 64 tiles x 4 blocks / 256
     ],
 )
-def test_reference_packet_stream_plan_without_gpu(lib: ctypes.CDLL, n, k, g, whole_groups,
+def test_reference_packet_stream_plan_without_gpu(lib: ctypes.CDLL, n, k, g, grid, whole_groups,
                                                   piece_groups) -> None:
     """One row over reference packets with at least one whole 128-column tile per CU takes the
-    stream schedule (whole tiles + pieces of the tiles left over); fewer tiles take the quarter
-    schedule where it applies, else the runs."""
+    stream schedule (whole tiles over a divisor grid of at least 7/8 of the CUs, else whole tiles
+    + pieces of the tiles left over); fewer tiles take the quarter schedule where it applies, else
+    the runs."""
     rc, p = _plan(lib, 1, n, k, g)
     assert rc == 0
-    assert (p.schedule, p.slice_cols, p.workgroups) == (2, 128, 256)
+    assert (p.schedule, p.slice_cols, p.workgroups) == (2, 128, grid)
     assert p.groups_per_workgroup == whole_groups + piece_groups
     if piece_groups:
         assert p.workspace_bytes == 65536 + 256 * 2 * 128 * 4

@@ -352,15 +352,17 @@ def test_mfma_stream_variants(m: int, n: int, k: int, g: int, act: str, asym: bo
     [
         (32768, 4096, 128, "f16"),   # 256 tiles: one whole tile per CU, no pieces
         (65536, 8192, 128, "bf16"),  # two whole tiles per CU
-        (57344, 8192, 128, "bf16"),  # 70B gate_up: a whole tile and a piece of one per CU
+        (57344, 8192, 128, "bf16"),  # 70B gate_up: two whole tiles per workgroup on 224 CUs
+        (49152, 8192, 128, "f16"),   # 384 tiles: a whole tile and a piece of one per CU
         (40960, 2048, 64, "bf16"),   # G = 64 (blocks of 8 groups), pieces of a quarter tile
         (36864, 16384, 64, "f16"),   # G = 64, longer K (more staging passes), pieces
     ],
 )
 def test_reference_packets_stream_schedule(n: int, k: int, g: int, act: str) -> None:
     """The reference signature (arc_w4a16_forward, arc_w4a16.cu:687-707) over the reference
-    packets on the stream schedule (w4a16_gemv_arc_stream.hip: whole 128-column tiles per CU plus
-    pieces): sampled rows against the oracle, and identical bits over three calls."""
+    packets on the stream schedule (w4a16_gemv_arc_stream.hip: whole 128-column tiles per
+    workgroup, over a divisor grid or over every CU plus pieces): sampled rows against the oracle,
+    and identical bits over three calls."""
     if torch.cuda.get_device_properties(0).multi_processor_count != 256:
         pytest.skip("the shapes are chosen for 256 CUs")
     from fast_kernels.ops import arc_w4a16_forward
