@@ -58,9 +58,10 @@ struct GemvLaunch {
   // b * stream_whole .., half-slice hs being the 16 columns 16 * (hs & 1) .. of slice hs / 2
   // (half of every slab); stream_grid * stream_whole = 2 * slices.
   bool stream_half = false;
-  // One row over the reference packets by 32-column quarters (w4a16_gemv_arc_quarter.hip, with
-  // slice_cols == kSliceCols): floor(2^32 / (K/G)) + 1, the reciprocal that turns a unit's linear
-  // (slice, group) index into its slice.
+  // One row over the reference packets by 32-column quarters or 16-column eighths
+  // (w4a16_gemv_arc_quarter.hip, with slice_cols == kSliceCols or kSliceCols / 2):
+  // floor(2^32 / (K/G)) + 1, the reciprocal that turns a unit's linear (unit, group) index into
+  // its unit.
   uint32_t ng_magic = 0;
 };
 
@@ -120,12 +121,13 @@ hipError_t launch_w4a16_gemv_stream(const GemvLaunch& launch, hipStream_t stream
 // LDS bytes.
 hipError_t launch_w4a16_gemv_arc_stream(const GemvLaunch& launch, hipStream_t stream);
 size_t arc_stream_lds(int group_size, int k);
-// One row over the reference packets by 32-column quarters of the packets, on the native stream
-// schedule (w4a16_gemv_arc_quarter.hip): whole slices per workgroup plus pieces of the slices left
-// over. arc_quarter_lds: its dynamic LDS bytes; arc_quarter_magic: GemvLaunch::ng_magic for K/G;
+// One row over the reference packets by 32-column quarters of the packets (slice_cols 32), or by
+// 16-column eighths (slice_cols 16, G = 128, no pieces), on the native stream schedule
+// (w4a16_gemv_arc_quarter.hip): whole units per workgroup plus pieces of the units left over.
+// arc_quarter_lds: its dynamic LDS bytes; arc_quarter_magic: GemvLaunch::ng_magic for K/G;
 // arc_quarter_magic_exact: whether that reciprocal is exact over every unit index of the launch.
 hipError_t launch_w4a16_gemv_arc_quarter(const GemvLaunch& launch, hipStream_t stream);
-size_t arc_quarter_lds(int group_size, int k);
+size_t arc_quarter_lds(int group_size, int k, int cols = kSliceCols);
 uint32_t arc_quarter_magic(int num_groups);
 bool arc_quarter_magic_exact(int num_groups, long long slices);
 // Matrix-core kernel on the stream schedule (w4a16_gemm_mfma_stream.hip): native slabs, 1-16 rows

@@ -23,8 +23,9 @@ int gemv_partials_m_tile_for_batch(int batch) {
 
 hipError_t launch_w4a16_gemv(const GemvLaunch& l, hipStream_t stream) {
   if (l.stream && l.format == PacketFormat::kArc) {
-    return l.slice_cols == kSliceCols ? launch_w4a16_gemv_arc_quarter(l, stream)
-                                      : launch_w4a16_gemv_arc_stream(l, stream);
+    return l.slice_cols == kSliceCols || l.slice_cols == kSliceCols / 2
+               ? launch_w4a16_gemv_arc_quarter(l, stream)
+               : launch_w4a16_gemv_arc_stream(l, stream);
   }
   if (l.fuse != GemvFuse::kNone) {
     return l.stream ? launch_w4a16_gemv_stream(l, stream) : launch_w4a16_gemv_fused(l, stream);

@@ -29,6 +29,12 @@
 //    added, the wave's 32 totals go to an LDS ring slot, and every four slices (and after the
 //    last) a barrier lets the workgroup add the waves' totals in wave order and write them.
 //
+// kCols = 16 (G = 128, no pieces, short K): the unit is a packet's 16-column eighth (64-byte runs
+// at the 512-byte stride), so that shapes with at most half as many quarters as CUs use every CU
+// (7B and 8B o: 256 eighths). Lane l then reads word row l / 4, columns 16 e + 4 (l % 4) .. + 3;
+// the 16 row groups alternate alphas and betas (the partner by DPP row_ror:4), and the fold adds
+// lanes l ^ 4 .. l ^ 32.
+//
 // The slice of a unit comes from its linear (slice, group) index by a multiply-high with a
 // reciprocal of K / G (GemvParams::ng_magic, exact over the launch's indices: see
 // arc_quarter_magic_exact), no division in the loop.
@@ -42,15 +48,27 @@ namespace {
 
 constexpr int kQuarterWaves = 8;
 
-template <int G>
-struct QuarterUnit {
-  static constexpr int kRows = G / 64;  // word rows of the lane
-  uint4 w[kRows];                       // word row R (l / 8) + k, columns 4 (l % 8) .. + 3
-  uint2 ab;  // the lane's four columns' alphas (l / 8 even) or betas (odd); lane l ^ 8 the other
+// Unit geometry for kCols = 32 (a packet quarter) or 16 (an eighth, G = 128): kCols / 4 lanes
+// cover a word row's kCols columns (16 bytes each), so a wave covers 64 / (kCols / 4) row groups
+// of R word rows.
+template <int G, int kCols>
+struct QuarterGeom {
+  static constexpr int kLanesPerRow = kCols / 4;
+  static constexpr int kRowGroups = 64 / kLanesPerRow;
+  static constexpr int kRows = (G / 8) / kRowGroups;  // word rows of the lane
+  static_assert(kRows >= 1, "one word row per lane at least");
 };
 
-// LDS: xs [(NG + 1) * G/8] re-paired words (group-major), sums [(NG + 1) * 8] {seed, S} per
-// (group, row group), scale [NG + 1] bf16 staging scales per group.
+template <int G, int kCols>
+struct QuarterUnit {
+  static constexpr int kRows = QuarterGeom<G, kCols>::kRows;
+  uint4 w[kRows];  // word rows R rg + k, columns 4 (l % (kCols / 4)) .. + 3 of the unit
+  uint2 ab;  // the lane's four columns' alphas (row group even) or betas (odd); a lane of the
+             // other parity and the same columns holds the other
+};
+
+// LDS: xs [(NG + 1) * G/8] re-paired words (group-major), sums [(NG + 1) * row groups] {seed, S}
+// per (group, row group), scale [NG + 1] bf16 staging scales per group.
 template <int G>
 struct QuarterLds {
   uint4* xs;
@@ -58,28 +76,33 @@ struct QuarterLds {
   float* scale;
 };
 
-template <int G>
+template <int G, int kCols>
 __host__ __device__ constexpr size_t quarter_lds_bytes(int ng) {
-  return static_cast<size_t>(ng + 1) * ((G / 8) * 16 + 8 * 8 + 4);
+  return static_cast<size_t>(ng + 1) *
+         ((G / 8) * 16 + QuarterGeom<G, kCols>::kRowGroups * 8 + 4);
 }
 
-template <int G, Act A, int kStageSlots, bool kPieces>
+template <int G, Act A, int kStageSlots, bool kPieces, int kCols>
 __global__ void __launch_bounds__(64 * (kQuarterWaves + (kPieces ? 1 : 0)), 1)
     w4a16_gemv_arc_quarter_kernel(GemvParams p) {
   constexpr int kW = kQuarterWaves;
-  constexpr int D = G == 128 ? 2 : 4;  // units in flight per wave (4 KB of codes)
-  constexpr int R = QuarterUnit<G>::kRows;
+  constexpr int D = G == 128 ? 2 : 4;  // units in flight per wave (4 KB of codes at kCols = 32)
+  using Geom = QuarterGeom<G, kCols>;
+  constexpr int R = Geom::kRows;
+  constexpr int kLpr = Geom::kLanesPerRow;
+  constexpr int kRg = Geom::kRowGroups;
+  constexpr int kUnitsPerTile = kTileCols / kCols;
   constexpr int WR = G / 8;
   constexpr int Q = kW * D;  // groups per block
   constexpr int kRing = 4;
   extern __shared__ uint4 quarter_lds[];
   // Wave totals: slots 0 and 1 for the pieces, then two rounds of kRing whole slices.
-  __shared__ float red[2 + 2 * kRing][kW][kSliceCols];
+  __shared__ float red[2 + 2 * kRing][kW][kCols];
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int rg8 = lane >> 3;  // the lane's row group
-  const int c8 = lane & 7;    // the lane's columns 4 c8 .. 4 c8 + 3 of the slice
+  const int rg8 = lane / kLpr;  // the lane's row group
+  const int c8 = lane % kLpr;   // the lane's columns 4 c8 .. 4 c8 + 3 of the unit
   const uint32_t mask_lo = vgpr_constant(0x000f000fu);
   const uint32_t mask_hi = vgpr_constant(0x00f000f0u);
   const size_t stride = static_cast<size_t>(format_packet_stride(G, PacketFormat::kArc));
@@ -88,8 +111,8 @@ __global__ void __launch_bounds__(64 * (kQuarterWaves + (kPieces ? 1 : 0)), 1)
   b = p.xcd_remap != 0 ? (b & 7) * p.xcd_remap + (b >> 3) : b;
   const int ng = p.NG;
   const int nbs = ng / Q;  // blocks per slice
-  const int slices = p.N / kSliceCols;
-  constexpr int kOut = kSliceCols;
+  const int slices = p.N / kCols;  // units
+  constexpr int kOut = kCols;
 
   if constexpr (kPieces) {
     if (wave == kW) {
@@ -145,7 +168,7 @@ __global__ void __launch_bounds__(64 * (kQuarterWaves + (kPieces ? 1 : 0)), 1)
   QuarterLds<G> sm;
   sm.xs = quarter_lds;
   sm.sums = reinterpret_cast<float2*>(sm.xs + static_cast<size_t>(ng + 1) * WR);
-  sm.scale = reinterpret_cast<float*>(sm.sums + static_cast<size_t>(ng + 1) * 8);
+  sm.scale = reinterpret_cast<float*>(sm.sums + static_cast<size_t>(ng + 1) * kRg);
 
   // The wave's units, in order: the head piece's, the tail piece's, then the whole slices' (as
   // in the native stream kernel, linear index slice * NG + group). Past its last unit a wave
@@ -161,7 +184,7 @@ __global__ void __launch_bounds__(64 * (kQuarterWaves + (kPieces ? 1 : 0)), 1)
   const int lane_off = R * rg8 * kWordRowBytes + c8 * 16;
   const int scale_off = kTileCols * G / 2 + (rg8 & 1) * (kTileCols * 2) + c8 * 8;
   const bool has_alpha = (rg8 & 1) == 0;
-  auto load_unit = [&](QuarterUnit<G>& u, int i) __attribute__((always_inline)) {
+  auto load_unit = [&](QuarterUnit<G, kCols>& u, int i) __attribute__((always_inline)) {
     const int c = min(i, j_last);
     int off = off_w;
     if constexpr (kPieces) {
@@ -176,18 +199,18 @@ __global__ void __launch_bounds__(64 * (kQuarterWaves + (kPieces ? 1 : 0)), 1)
     const uint32_t lin = static_cast<uint32_t>(c * kW + off);
     const uint32_t s = __umulhi(lin, magic);
     const uint32_t g = lin - s * static_cast<uint32_t>(ng);
-    const uint32_t pkt = (s >> 2) * static_cast<uint32_t>(ng) + g;
+    const uint32_t pkt = (s / kUnitsPerTile) * static_cast<uint32_t>(ng) + g;
     const uint8_t* pk = p.packets + static_cast<size_t>(pkt) * stride;
-    const uint8_t* codes = pk + (s & 3) * (kSliceCols * 4) + lane_off;
+    const uint8_t* codes = pk + (s % kUnitsPerTile) * (kCols * 4) + lane_off;
 #pragma unroll
     for (int k = 0; k < R; ++k) {
       u.w[k] = stream_load16(codes + k * kWordRowBytes);
     }
     // one 8-byte load per lane for the scales: alphas on even row groups, betas on odd ones
-    u.ab = stream_load8(pk + scale_off + (s & 3) * (kSliceCols * 2));
+    u.ab = stream_load8(pk + scale_off + (s % kUnitsPerTile) * (kCols * 2));
   };
 
-  QuarterUnit<G> buf[D];
+  QuarterUnit<G, kCols> buf[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
     load_unit(buf[d], d);
@@ -222,7 +245,7 @@ __global__ void __launch_bounds__(64 * (kQuarterWaves + (kPieces ? 1 : 0)), 1)
     }
     sm.xs[static_cast<size_t>(g) * WR + w] = xp;
     // every lane of a row group holds the same values and writes them (no branch)
-    sm.sums[static_cast<size_t>(g) * 8 + w / R] =
+    sm.sums[static_cast<size_t>(g) * kRg + w / R] =
         make_float2(fmaf(-1024.0f, se, -64.0f * so), se + so);
     sm.scale[g] = undo;
 #pragma unroll
@@ -250,7 +273,7 @@ __global__ void __launch_bounds__(64 * (kQuarterWaves + (kPieces ? 1 : 0)), 1)
     uint32_t e0[R][4], o0[R][4], e1[R][4], o1[R][4];
     float a[4], bt[4];
   };
-  auto unpack = [&](const QuarterUnit<G>& u, Unpacked& up) __attribute__((always_inline)) {
+  auto unpack = [&](const QuarterUnit<G, kCols>& u, Unpacked& up) __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < R; ++k) {
       const uint32_t words[4] = {u.w[k].x, u.w[k].y, u.w[k].z, u.w[k].w};
@@ -264,9 +287,10 @@ __global__ void __launch_bounds__(64 * (kQuarterWaves + (kPieces ? 1 : 0)), 1)
         up.o1[k][j] = (w8 & mask_hi) | kBiasHigh;  // k3, k7
       }
     }
-    // lane l ^ 8 (the other row-group parity, same columns) holds the other half: DPP row_ror:8
-    const uint32_t ox = __builtin_amdgcn_mov_dpp(u.ab.x, 0x128, 0xf, 0xf, true);
-    const uint32_t oy = __builtin_amdgcn_mov_dpp(u.ab.y, 0x128, 0xf, 0xf, true);
+    // the lane kLpr further in its 16-lane row (the other row-group parity, same columns) holds
+    // the other half: DPP row_ror:kLpr
+    const uint32_t ox = __builtin_amdgcn_mov_dpp(u.ab.x, 0x120 + kLpr, 0xf, 0xf, true);
+    const uint32_t oy = __builtin_amdgcn_mov_dpp(u.ab.y, 0x120 + kLpr, 0xf, 0xf, true);
     const uint32_t ax = has_alpha ? u.ab.x : ox;
     const uint32_t ay = has_alpha ? u.ab.y : oy;
     const uint32_t bx = has_alpha ? ox : u.ab.x;
@@ -280,7 +304,7 @@ __global__ void __launch_bounds__(64 * (kQuarterWaves + (kPieces ? 1 : 0)), 1)
     }
   };
   auto compute = [&](const Unpacked& up, int g) __attribute__((always_inline)) {
-    const float2 sp = sm.sums[static_cast<size_t>(g) * 8 + rg8];
+    const float2 sp = sm.sums[static_cast<size_t>(g) * kRg + rg8];
     float acc[4][2];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -331,15 +355,16 @@ __global__ void __launch_bounds__(64 * (kQuarterWaves + (kPieces ? 1 : 0)), 1)
     j += D;
   };
   auto block = [&](int gl0) { block_r(gl0, std::true_type{}); };
-  // The eight row groups of each column added, then the wave's 32 totals into LDS slot `slot`.
+  // The row groups of each column added, then the wave's kCols totals into LDS slot `slot`.
   auto fold = [&](int slot) {
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
-      y[jj] += __shfl_xor(y[jj], 8);
-      y[jj] += __shfl_xor(y[jj], 16);
-      y[jj] += __shfl_xor(y[jj], 32);
+#pragma unroll
+      for (int o = kLpr; o < 64; o *= 2) {
+        y[jj] += __shfl_xor(y[jj], o);
+      }
     }
-    if (lane < 8) {
+    if (lane < kLpr) {
       *reinterpret_cast<float4*>(&red[slot][wave][4 * c8]) = make_float4(y[0], y[1], y[2], y[3]);
     }
 #pragma unroll
@@ -402,16 +427,16 @@ __global__ void __launch_bounds__(64 * (kQuarterWaves + (kPieces ? 1 : 0)), 1)
     if (in_round == kRing - 1 || r == rg.whole - 1) {
       lds_barrier();
       const int r0 = r - in_round;
-      for (int o = tid; o < (in_round + 1) * kSliceCols; o += 64 * kW) {
-        const int rr = r0 + o / kSliceCols;
-        const int c = o % kSliceCols;
+      for (int o = tid; o < (in_round + 1) * kCols; o += 64 * kW) {
+        const int rr = r0 + o / kCols;
+        const int c = o % kCols;
         const int slot = 2 + rr % (2 * kRing);
         float v = red[slot][0][c];
 #pragma unroll
         for (int w = 1; w < kW; ++w) {
           v += red[slot][w][c];
         }
-        p.out[static_cast<size_t>(rg.whole_slice0 + rr) * kSliceCols + c] = float_to_act_bits<A>(v);
+        p.out[static_cast<size_t>(rg.whole_slice0 + rr) * kCols + c] = float_to_act_bits<A>(v);
       }
     }
   }
@@ -419,7 +444,7 @@ __global__ void __launch_bounds__(64 * (kQuarterWaves + (kPieces ? 1 : 0)), 1)
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
 }
 
-template <int G, Act A, int kStageSlots>
+template <int G, Act A, int kStageSlots, int kCols>
 hipError_t launch_arc_quarter_t(const GemvLaunch& l, hipStream_t stream) {
   int grid = 0;
   GemvParams p = native_params<G, 1>(l, &grid);
@@ -429,35 +454,44 @@ hipError_t launch_arc_quarter_t(const GemvLaunch& l, hipStream_t stream) {
   p.grid = grid;
   p.xcd_remap = grid % 8 == 0 ? grid / 8 : 0;
   p.ng_magic = l.ng_magic;
-  const size_t lds = quarter_lds_bytes<G>(l.K / G);
-  if (l.stream_pieces) {
-    hipLaunchKernelGGL((w4a16_gemv_arc_quarter_kernel<G, A, kStageSlots, true>), dim3(grid),
-                       dim3(64 * (kQuarterWaves + 1)), lds, stream, p);
-  } else {
-    hipLaunchKernelGGL((w4a16_gemv_arc_quarter_kernel<G, A, kStageSlots, false>), dim3(grid),
-                       dim3(64 * kQuarterWaves), lds, stream, p);
+  const size_t lds = quarter_lds_bytes<G, kCols>(l.K / G);
+  if constexpr (kCols == kSliceCols) {
+    if (l.stream_pieces) {
+      hipLaunchKernelGGL((w4a16_gemv_arc_quarter_kernel<G, A, kStageSlots, true, kCols>),
+                         dim3(grid), dim3(64 * (kQuarterWaves + 1)), lds, stream, p);
+      return hipGetLastError();
+    }
   }
+  hipLaunchKernelGGL((w4a16_gemv_arc_quarter_kernel<G, A, kStageSlots, false, kCols>), dim3(grid),
+                     dim3(64 * kQuarterWaves), lds, stream, p);
   return hipGetLastError();
 }
 
-template <int G, Act A>
+template <int G, Act A, int kCols>
 hipError_t arc_quarter_slots(const GemvLaunch& l, hipStream_t stream) {
   // passes of a wave: (K/G / 8 groups) / (64 / (G / 8) groups per pass)
   constexpr int kGroupsPerPass = 64 / (G / 8);
   const int passes = (l.K / G / kQuarterWaves + kGroupsPerPass - 1) / kGroupsPerPass;
   if (passes <= 2) {
-    return launch_arc_quarter_t<G, A, 2>(l, stream);
+    return launch_arc_quarter_t<G, A, 2, kCols>(l, stream);
   }
-  if (passes <= 8) {
-    return launch_arc_quarter_t<G, A, 8>(l, stream);
+  // eighths: short K only (K/G <= 64 at G = 128)
+  if constexpr (kCols == kSliceCols) {
+    if (passes <= 8) {
+      return launch_arc_quarter_t<G, A, 8, kCols>(l, stream);
+    }
   }
   return hipErrorInvalidValue;
 }
 
 }  // namespace
 
-size_t arc_quarter_lds(int group_size, int k) {
-  return group_size == 64 ? quarter_lds_bytes<64>(k / 64) : quarter_lds_bytes<128>(k / 128);
+size_t arc_quarter_lds(int group_size, int k, int cols) {
+  if (group_size == 64) {
+    return quarter_lds_bytes<64, kSliceCols>(k / 64);
+  }
+  return cols == kSliceCols / 2 ? quarter_lds_bytes<128, kSliceCols / 2>(k / 128)
+                                : quarter_lds_bytes<128, kSliceCols>(k / 128);
 }
 
 bool arc_quarter_magic_exact(int num_groups, long long slices) {
@@ -475,7 +509,9 @@ uint32_t arc_quarter_magic(int num_groups) {
 hipError_t launch_w4a16_gemv_arc_quarter(const GemvLaunch& l, hipStream_t stream) {
   if (l.mode != GemvMode::kStreamK || l.M != 1 || l.m_tile != 1 || l.format != PacketFormat::kArc ||
       l.fuse != GemvFuse::kNone || l.K > kStreamMaxK || l.stream_grid <= 0 ||
-      l.stream_whole < 0 || (l.group_size != 64 && l.group_size != 128)) {
+      l.stream_whole < 0 || (l.group_size != 64 && l.group_size != 128) ||
+      (l.slice_cols != kSliceCols &&
+       (l.slice_cols != kSliceCols / 2 || l.group_size != 128 || l.stream_pieces))) {
     return hipErrorInvalidValue;
   }
   const int ng = l.K / l.group_size;
@@ -484,7 +520,7 @@ hipError_t launch_w4a16_gemv_arc_quarter(const GemvLaunch& l, hipStream_t stream
     return hipErrorInvalidValue;
   }
   const long long nbs = ng / quantum;
-  const long long slices = l.N / kSliceCols;
+  const long long slices = l.N / l.slice_cols;  // units
   const long long left = slices - static_cast<long long>(l.stream_grid) * l.stream_whole;
   if (l.stream_pieces) {
     // left-over slices fewer than the workgroups, at least one left-over block per workgroup
@@ -500,11 +536,15 @@ hipError_t launch_w4a16_gemv_arc_quarter(const GemvLaunch& l, hipStream_t stream
     return hipErrorInvalidValue;
   }
   if (l.group_size == 64) {
-    return l.act == Act::kF16 ? arc_quarter_slots<64, Act::kF16>(l, stream)
-                              : arc_quarter_slots<64, Act::kBF16>(l, stream);
+    return l.act == Act::kF16 ? arc_quarter_slots<64, Act::kF16, kSliceCols>(l, stream)
+                              : arc_quarter_slots<64, Act::kBF16, kSliceCols>(l, stream);
   }
-  return l.act == Act::kF16 ? arc_quarter_slots<128, Act::kF16>(l, stream)
-                            : arc_quarter_slots<128, Act::kBF16>(l, stream);
+  if (l.slice_cols == kSliceCols / 2) {
+    return l.act == Act::kF16 ? arc_quarter_slots<128, Act::kF16, kSliceCols / 2>(l, stream)
+                              : arc_quarter_slots<128, Act::kBF16, kSliceCols / 2>(l, stream);
+  }
+  return l.act == Act::kF16 ? arc_quarter_slots<128, Act::kF16, kSliceCols>(l, stream)
+                            : arc_quarter_slots<128, Act::kBF16, kSliceCols>(l, stream);
 }
 
 }  // namespace fk

@@ -448,13 +448,20 @@ bool arc_quarter_enabled() {
   return enabled;
 }
 
+// FK_W4A16_ARC_EIGHTHS=0 keeps the quarter schedule over reference packets off 16-column units.
+bool arc_eighths_enabled() {
+  static const bool enabled = env_enabled("FK_W4A16_ARC_EIGHTHS");
+  return enabled;
+}
+
 // One row over the reference packets by 32-column quarters of the packets, for the shapes with
 // fewer 128-column tiles than CUs (the whole-tile stream schedule, arc_stream_plan, takes the
 // others: 70B gate_up 39.7 us on it against 41.0 by quarters). The slices are dealt like the
 // native stream kernel's: whole slices per CU when they divide, pieces of the slices left over
 // when there are more slices than CUs and K is long (K/G >= 64), a divisor grid of at least 7/8
-// of the CUs, or one slice per workgroup when there are fewer slices than CUs and the per-tile
-// runs would not split K either. Blocks are 8 waves x D groups (D = 2 at G = 128, 4 at G = 64).
+// of the CUs, one 16-column eighth per workgroup when there are at most half as many slices as
+// CUs and K is short (G = 128, K/G <= 32), or one slice per workgroup when there are fewer slices
+// than CUs and the per-tile runs would not split K either. Blocks are 8 waves x D groups (D = 2 at G = 128, 4 at G = 64).
 // Measured on MI355X (bench.py --packets arc, alternating runs against the per-tile runs): 70B
 // qkv 11.4 -> 10.0 us, o 8.4 -> 7.7, down 22.4 -> 21.8; 7B o 5.06 -> 4.24. False (plan
 // unchanged) when it does not apply.
@@ -475,12 +482,17 @@ bool arc_quarter_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_siz
     return false;
   }
   constexpr int kMinPieceGroups = 64;
+  // 16-column eighths, one per workgroup, for short K only (measured on MI355X, bench.py
+  // --packets arc, alternating runs: 7B o 4.20-4.23 -> 4.03-4.06 us, 8B o 4.34-4.37 -> 4.07-4.08;
+  // 8B down, K/G = 112, 9.07-9.19 -> 9.01-9.56; 7B qkv as three eighths per CU 6.9 -> 9.8).
+  constexpr int kMaxEighthGroups = 32;
   const long long nbs = num_groups / per_block;
   const long long cus = cu_count;
   const long long left = slices % cus;
   long long grid = 0;
   int whole = 0;
   bool pieces = false;
+  bool eighths = false;
   if (slices >= cus && left == 0) {
     grid = cus;
     whole = static_cast<int>(slices / cus);
@@ -492,14 +504,23 @@ bool arc_quarter_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_siz
   } else if (const long long dgrid = divisor_grid(slices, cus); dgrid > 0) {
     grid = dgrid;
     whole = static_cast<int>(slices / dgrid);
+  } else if (group_size == 128 && 2 * slices <= cus && num_groups <= kMaxEighthGroups &&
+             arc_eighths_enabled() && fk::arc_quarter_magic_exact(num_groups, 2 * slices)) {
+    grid = 2 * slices;
+    whole = 1;
+    eighths = true;
   } else if (slices < cus && plan.groups_per_workgroup == num_groups) {
     grid = slices;
     whole = 1;
   } else {
     return false;
   }
+  if (eighths && fk::arc_quarter_lds(group_size, k, fk::kSliceCols / 2) +
+                         fk::kStreamStaticLdsBytes > lds_limit) {
+    return false;
+  }
   plan.schedule = kScheduleStream;
-  plan.slice_cols = fk::kSliceCols;
+  plan.slice_cols = eighths ? fk::kSliceCols / 2 : fk::kSliceCols;
   plan.workgroups = static_cast<int>(grid);
   plan.stream_depth = depth;
   plan.stream_whole = whole;
@@ -893,7 +914,8 @@ void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::u
     l.units_per_workgroup = 2 * plan.groups_per_workgroup;
   } else if (plan.schedule == kScheduleStream && format == fk::PacketFormat::kArc) {
     if (batch != 1 || plan.m_tile != 1 ||
-        (plan.slice_cols != fk::kTileCols && plan.slice_cols != fk::kSliceCols) ||
+        (plan.slice_cols != fk::kTileCols && plan.slice_cols != fk::kSliceCols &&
+         plan.slice_cols != fk::kSliceCols / 2) ||
         fuse != fk::GemvFuse::kNone) {
       throw std::logic_error("stream schedule on a reference-packet plan it does not take");
     }

@@ -256,7 +256,8 @@ def test_native_plan_policy_without_gpu(lib: ctypes.CDLL, shape, want) -> None:
     elif n // 128 >= 256:
         assert (arc.schedule, arc.slice_cols) == (2, 128)
     elif arc.schedule == 2:
-        assert arc.slice_cols == 32
+        # quarters, or eighths when at most half as many quarters as CUs and K/G <= 32
+        assert arc.slice_cols == (16 if g == 128 and n // 32 <= 128 and k // g <= 32 else 32)
     # a fix-up needs a workspace exactly when slices are shared (runs that do not cover whole
     # slices, or stream pieces)
     assert (p.workspace_bytes > 0) == (p.max_tile_contributors > 1)
@@ -383,25 +384,28 @@ def test_reference_packet_stream_plan_without_gpu(lib: ctypes.CDLL, n, k, g, gri
 @pytest.mark.parametrize(
     "n,k,g,want",
     [
-        # (workgroups, groups per workgroup, fix-up workspace) on 256 CUs
-        ((28672), 8192, 128, (256, 3 * 64 + 32, True)),  # 896 slices: 3 whole + pieces of 128
-        (10240, 8192, 128, (256, 64 + 16, True)),          # 70B qkv: a slice and a block
-        (8192, 8192, 128, (256, 64, False)),               # 70B o
-        (8192, 28672, 128, (256, 224, False)),             # 70B down
-        (4096, 4096, 128, (128, 32, False)),               # 7B o: one slice each, K not split
-        (14336, 4096, 128, (224, 64, False)),              # divisor grid (7/8 of the CUs)
-        (10240, 8192, 64, (256, 128 + 32, True)),          # G = 64: blocks of 32 groups
+        # (unit columns, workgroups, groups per workgroup, fix-up workspace) on 256 CUs
+        ((28672), 8192, 128, (32, 256, 3 * 64 + 32, True)),  # 896 slices: 3 whole + pieces
+        (10240, 8192, 128, (32, 256, 64 + 16, True)),          # 70B qkv: a slice and a block
+        (8192, 8192, 128, (32, 256, 64, False)),               # 70B o
+        (8192, 28672, 128, (32, 256, 224, False)),             # 70B down
+        (4096, 8192, 128, (32, 128, 64, False)),               # one slice each, K not split
+        (4096, 4096, 128, (16, 256, 32, False)),               # 7B o: one 16-column eighth each
+        (2048, 4096, 128, (16, 128, 32, False)),               # 128 eighths
+        (14336, 4096, 128, (32, 224, 64, False)),              # divisor grid (7/8 of the CUs)
+        (10240, 8192, 64, (32, 256, 128 + 32, True)),          # G = 64: blocks of 32 groups
     ],
 )
 def test_reference_packet_quarter_plan_without_gpu(lib: ctypes.CDLL, n, k, g, want) -> None:
     """One row over reference packets with fewer whole 128-column tiles than CUs takes the
-    quarter schedule (32-column quarters of the packets on the native stream split); shapes with
-    a whole tile per CU keep the whole-tile stream schedule."""
+    quarter schedule (32-column quarters of the packets on the native stream split, or 16-column
+    eighths for short K with at most half as many quarters as CUs); shapes with a whole tile per
+    CU keep the whole-tile stream schedule."""
     rc, p = _plan(lib, 1, n, k, g)
     assert rc == 0
-    assert (p.schedule, p.slice_cols, p.m_tile) == (2, 32, 1)
-    assert (p.workgroups, p.groups_per_workgroup, p.workspace_bytes > 0) == want
-    if want[2]:
+    assert (p.schedule, p.m_tile) == (2, 1)
+    assert (p.slice_cols, p.workgroups, p.groups_per_workgroup, p.workspace_bytes > 0) == want
+    if want[3]:
         assert p.workspace_bytes == 65536 + p.workgroups * 2 * 32 * 4
     rc, p = _plan(lib, 1, 57344, 8192, 128)
     assert rc == 0 and (p.schedule, p.slice_cols) == (2, 128)

@@ -388,21 +388,25 @@ def test_reference_packets_stream_schedule(n: int, k: int, g: int, act: str) -> 
 @pytest.mark.parametrize(
     "n,k,g,act,want",
     [
-        # n, k, G, activation, (workgroups, groups per workgroup, fix-up workspace) on 256 CUs
-        (8192, 8192, 128, "bf16", (256, 64, False)),    # 70B o: one 32-column slice per CU
-        (10240, 8192, 128, "bf16", (256, 80, True)),    # 70B qkv: a slice and a piece per CU
-        (8192, 28672, 128, "bf16", (256, 224, False)),  # 70B down: seven staging passes
-        (4096, 4096, 128, "f16", (128, 32, False)),     # 7B o: fewer slices than CUs, one each
-        (14336, 4096, 128, "f16", (224, 64, False)),    # divisor grid: 448 slices on 224 CUs
-        (16384, 4096, 64, "f16", (256, 128, False)),    # G = 64: blocks of 32 groups
-        (10240, 8192, 64, "bf16", (256, 160, True)),    # G = 64 with pieces
+        # n, k, G, activation, (unit columns, workgroups, groups per workgroup, fix-up
+        # workspace) on 256 CUs
+        (8192, 8192, 128, "bf16", (32, 256, 64, False)),    # 70B o: one 32-column slice per CU
+        (10240, 8192, 128, "bf16", (32, 256, 80, True)),    # 70B qkv: a slice and a piece per CU
+        (8192, 28672, 128, "bf16", (32, 256, 224, False)),  # 70B down: seven staging passes
+        (14336, 4096, 128, "f16", (32, 224, 64, False)),    # divisor grid: 448 slices on 224 CUs
+        (16384, 4096, 64, "f16", (32, 256, 128, False)),    # G = 64: blocks of 32 groups
+        (10240, 8192, 64, "bf16", (32, 256, 160, True)),    # G = 64 with pieces
+        # 16-column eighths of the packets (G = 128)
+        (4096, 4096, 128, "f16", (16, 256, 32, False)),     # 7B o: one eighth per CU
+        (2048, 4096, 128, "bf16", (16, 128, 32, False)),    # 128 eighths, one each
+        (4096, 4096, 128, "bf16", (16, 256, 32, False)),    # 8B o
     ],
 )
 def test_reference_packets_quarter_schedule(n: int, k: int, g: int, act: str, want) -> None:
     """The reference signature (arc_w4a16_forward, arc_w4a16.cu:687-707) over the reference
-    packets by 32-column quarters of the packets (w4a16_gemv_arc_quarter.hip), asymmetric packets
-    (any fp16 beta): sampled rows against the oracle (every row for 7B o), identical bits over
-    three calls."""
+    packets by 32-column quarters or 16-column eighths of the packets (w4a16_gemv_arc_quarter.hip),
+    asymmetric packets (any fp16 beta): sampled rows against the oracle (every row for 7B o),
+    identical bits over three calls."""
     if torch.cuda.get_device_properties(0).multi_processor_count != 256:
         pytest.skip("the shapes are chosen for 256 CUs")
     from fast_kernels.ops import arc_w4a16_forward
@@ -412,8 +416,9 @@ def test_reference_packets_quarter_schedule(n: int, k: int, g: int, act: str, wa
     packets = pack_arc_w4a16_packets(q, a, b, group_size=g)
     plan = arc_w4a16_plan(batch=1, n=n, k=k, group_size=g, activation_dtype=x.dtype,
                           packet_format=0)
-    assert plan["schedule"] == 2 and plan["slice_cols"] == 32, plan
-    got = (plan["workgroups"], plan["groups_per_workgroup"], plan["workspace_bytes"] > 0)
+    assert plan["schedule"] == 2, plan
+    got = (plan["slice_cols"], plan["workgroups"], plan["groups_per_workgroup"],
+           plan["workspace_bytes"] > 0)
     assert got == want, plan
     outs = []
     for _ in range(3):

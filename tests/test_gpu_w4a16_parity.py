@@ -156,7 +156,7 @@ def test_forward_baseline_shapes_match_oracle(shape: tuple[int, int, int, int]) 
     "shape,act,asym,want",
     [
         # (batch, n, k, G), activation, asymmetric, (slice_cols, groups per workgroup) on 256 CUs
-        ((1, 1024, 2048, 128), "f16", False, (32, 16)),    # 8 tiles -> 32 narrow slices
+        ((1, 1024, 2048, 128), "f16", False, (16, 16)),    # 8 tiles -> 64 16-column eighths
         ((1, 10240, 4096, 128), "f16", True, (64, 32)),    # 80 tiles -> 160 64-column slices
         ((1, 4096, 14336, 128), "bf16", False, (32, 56)),  # narrow slices + K split (fix-up)
         ((2, 4096, 4096, 64), "f16", True, (128, 8)),      # two rows: whole tiles, 8 runs per tile
@@ -167,8 +167,8 @@ def test_forward_baseline_shapes_match_oracle(shape: tuple[int, int, int, int]) 
     ],
 )
 def test_forward_column_slices_match_oracle(shape, act, asym, want) -> None:
-    """The automatic plan's 64- and 32-column slices, alone and with K split across workgroups,
-    and its K splits for several rows."""
+    """The automatic plan's 64-, 32- and 16-column slices, alone and with K split across
+    workgroups, and its K splits for several rows."""
     batch, n, k, g = shape
     plan = arc_w4a16_plan(batch=batch, n=n, k=k, group_size=g,
                           activation_dtype=torch.float16 if act == "f16" else torch.bfloat16)
