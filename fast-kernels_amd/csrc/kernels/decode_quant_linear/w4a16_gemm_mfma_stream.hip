@@ -1,5 +1,5 @@
-// W4A16 small-batch GEMM (2-16 activation rows) over native slabs on the gfx950 matrix cores, on
-// the persistent stream schedule.
+// W4A16 small-batch GEMM (2-16 activation rows) over native slabs or the reference packets on the
+// gfx950 matrix cores, on the persistent stream schedule.
 //
 // The work split is the one-row stream kernel's (w4a16_stream_common.h): one workgroup per CU
 // streams its whole 32-column slices as one contiguous range, plus pieces of the slices left
@@ -25,6 +25,11 @@
 //    the others; one wave (rotating with the slice, or the control wave for pieces) adds the
 //    eight partials in wave order and writes the slice, and a second barrier frees the one LDS
 //    slot (the activations of 16 rows leave no room for a second).
+//  * Over the reference packets (kArc) the slices are the packets' 32-column quarters (slice
+//    4 tile + q, so the output columns and the work split are the same): lane l = 16 t + n reads,
+//    for window j, the 8 bytes of columns 32 q + 2 n and + 1 in word row 4 j + t (four 128-byte
+//    runs per load) and those columns' alphas and betas; the two chains are the two columns, A
+//    the staged k-chunk 4 j + t, and the epilogue y += alpha D + beta S with the packet's betas.
 #include "w4a16_gemv_native.h"
 #include "w4a16_stream_common.h"
 
@@ -90,6 +95,30 @@ __device__ __forceinline__ uint32_t slab_word(const NativeLoad<G>& ld, int i, in
   }
 }
 
+// One 32-column quarter q of a reference packet (kArc) for the matrix cores: lane l = 16 t + n
+// holds, for window j, the words of columns 32 q + 2 n and 32 q + 2 n + 1 in word row 4 j + t
+// (8 bytes), and those two columns' alphas and betas.
+template <int G>
+struct ArcMfmaLoad {
+  static constexpr int kWindows = G / 32;
+  uint2 w[kWindows];
+  uint32_t alpha;
+  uint32_t beta;
+};
+
+template <int G>
+__device__ __forceinline__ void arc_mfma_load(ArcMfmaLoad<G>& ld, const uint8_t* packet, int q,
+                                              int t, int n) {
+  const uint8_t* codes = packet + q * (kSliceCols * 4) + 8 * n;
+#pragma unroll
+  for (int j = 0; j < ArcMfmaLoad<G>::kWindows; ++j) {
+    ld.w[j] = stream_load8(codes + (4 * j + t) * kWordRowBytes);
+  }
+  const uint8_t* scales = packet + kTileCols * G / 2 + q * (kSliceCols * 2) + 4 * n;
+  ld.alpha = stream_load4(scales);
+  ld.beta = stream_load4(scales + kTileCols * 2);
+}
+
 // Most staging loads per lane (a wave's groups x MT rows x G/8 word rows / 64 lanes): MT. The
 // host keeps launches within it.
 constexpr int max_stage_per_lane(int mt) { return mt; }
@@ -120,6 +149,8 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   const int rows = p.M;  // rows < MT are real, the rest zeros
   const int n_out = rows * kSliceCols;
   const StreamRange rg = stream_range(b, grid, p.stream_whole, slices, nbs, kPieces);
+  constexpr bool kArcPk = F == PacketFormat::kArc;
+  using Load = std::conditional_t<kArcPk, ArcMfmaLoad<G>, NativeLoad<G>>;
 
   MfmaStreamLds<G, MT> sm;
   sm.xs = mfma_stream_lds;
@@ -194,6 +225,30 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     }
     return p.packets + static_cast<size_t>(static_cast<uint32_t>(c * kW + off)) * stride;
   };
+  // kArc: the slab index slice * NG + group gives the slice by a multiply-high with a reciprocal
+  // of NG (exact over the launch's indices, checked by the host), then packet (slice / 4) * NG +
+  // group and quarter slice % 4.
+  auto load_slab = [&](Load& ld, int i) __attribute__((always_inline)) {
+    if constexpr (kArcPk) {
+      const int c = min(i, j_last);
+      int off = off_w;
+      if constexpr (kPieces) {
+        int in_t = c < n_h + n_t ? 1 : 0;
+        int in_h = c < n_h ? 1 : 0;
+        in_t = __builtin_amdgcn_readfirstlane(in_t);
+        in_h = __builtin_amdgcn_readfirstlane(in_h);
+        off += in_t * (off_t - off_w) + in_h * (off_h - off_t);
+      }
+      const uint32_t lin = static_cast<uint32_t>(c * kW + off);
+      const uint32_t sl = __umulhi(lin, p.ng_magic);
+      const uint32_t g = lin - sl * static_cast<uint32_t>(ng);
+      const uint8_t* pk =
+          p.packets + static_cast<size_t>((sl >> 2) * static_cast<uint32_t>(ng) + g) * stride;
+      arc_mfma_load<G>(ld, pk, static_cast<int>(sl & 3), t, n);
+    } else {
+      native_load<G, F>(ld, slab(i), lane);
+    }
+  };
 
   // Staging: the wave's (group, row, word row) units, 64 a pass, groups g = wave + kW gi; a
   // group's MT * WR units are P consecutive lanes' worth (row and word row fastest), so a group's
@@ -226,10 +281,10 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     raw[i] = *reinterpret_cast<const uint4*>(p.x + (m * p.K + g * G + wr * 8));
   }
   __builtin_amdgcn_sched_barrier(0);
-  NativeLoad<G> buf[D];
+  Load buf[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
-    native_load<G, F>(buf[d], slab(d), lane);
+    load_slab(buf[d], d);
     __builtin_amdgcn_sched_barrier(0);
   }
   // Convert and store: rows past the batch stage zeros (a mask, not a branch); a pass past the
@@ -291,8 +346,10 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   auto load_op = [&](int gl, Op& o) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < U; ++j) {
-      const uint4 xv = sm.xs[(static_cast<size_t>(gl) * WR + U * t + j) * MT +
-                             xs_slot<MT>(U * t + j, min(n, MT - 1))];
+      // the k-chunk of window j for lane quarter t: U t + j (native slabs), 4 j + t (kArc)
+      const int wr_j = kArcPk ? 4 * j + t : U * t + j;
+      const uint4 xv = sm.xs[(static_cast<size_t>(gl) * WR + wr_j) * MT +
+                             xs_slot<MT>(wr_j, min(n, MT - 1))];
       o.a[j] = __builtin_bit_cast(half8_t, n < MT ? xv : make_uint4(0u, 0u, 0u, 0u));
     }
 #pragma unroll
@@ -307,13 +364,17 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     }
   };
   // Slab of one group: 2 U MFMAs and the epilogue.
-  auto compute = [&](const NativeLoad<G>& ld, const Op& o) __attribute__((always_inline)) {
+  // kArc: the two chains are the lane's columns 2 n and 2 n + 1, with the packet's betas.
+  constexpr bool kBeta = F != PacketFormat::kNativeSym;
+  auto compute = [&](const Load& ld, const Op& o) __attribute__((always_inline)) {
     const auto& a = o.a;
     const float4_t seed = o.seed;
     const auto& s = o.s;
     const auto& sc = o.sc;
     uint32_t beta_pair = 0;
-    if constexpr (F == PacketFormat::kNativeAsym) {
+    if constexpr (kArcPk) {
+      beta_pair = ld.beta;
+    } else if constexpr (F == PacketFormat::kNativeAsym) {
       beta_pair = __builtin_bit_cast(
           uint32_t, __builtin_bit_cast(half2_t, ld.alpha) * __builtin_bit_cast(half2_t, ld.zp));
     }
@@ -323,8 +384,14 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
       dd[i] = seed;
 #pragma unroll
       for (int j = 0; j < U; ++j) {
-        dd[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            a[j], unpack_word8(slab_word<G>(ld, i, j), mask_lo, mask_hi), dd[i], 0, 0, 0);
+        uint32_t word;
+        if constexpr (kArcPk) {
+          word = i == 0 ? ld.w[j].x : ld.w[j].y;
+        } else {
+          word = slab_word<G>(ld, i, j);
+        }
+        dd[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j], unpack_word8(word, mask_lo, mask_hi),
+                                                       dd[i], 0, 0, 0);
       }
     }
 #pragma unroll
@@ -335,13 +402,13 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
       for (int r = 0; r < 4; ++r) {
         if constexpr (A == Act::kBF16) {
           float tt = alpha * dd[i][r];
-          if constexpr (F == PacketFormat::kNativeAsym) {
+          if constexpr (kBeta) {
             tt = fmaf(beta, s[r], tt);
           }
           y[i][r] = fmaf(tt, sc[r], y[i][r]);
         } else {
           y[i][r] = fmaf(alpha, dd[i][r], y[i][r]);
-          if constexpr (F == PacketFormat::kNativeAsym) {
+          if constexpr (kBeta) {
             y[i][r] = fmaf(beta, s[r], y[i][r]);
           }
         }
@@ -360,7 +427,7 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     }
     compute(buf[d], cur);
     if constexpr (decltype(refill)::value) {
-      native_load<G, F>(buf[d], slab(j + d + D), lane);
+      load_slab(buf[d], j + d + D);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -374,7 +441,7 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
         load_op(gl0 + kW * d, op);
         compute(buf[d], op);
         if constexpr (decltype(refill)::value) {
-          native_load<G, F>(buf[d], slab(j + d + D), lane);
+          load_slab(buf[d], j + d + D);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -398,7 +465,7 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         if (r0 + r < MT) {
-          sm.red[(wave * MT + r0 + r) * kSliceCols + 16 * i + n] = y[i][r];
+          sm.red[(wave * MT + r0 + r) * kSliceCols + (kArcPk ? 2 * n + i : 16 * i + n)] = y[i][r];
         }
         y[i][r] = 0.0f;
       }
@@ -457,14 +524,19 @@ hipError_t launch_mfma_stream_t(const GemvLaunch& l, hipStream_t stream) {
   grid = l.stream_grid;
   p.grid = grid;
   p.xcd_remap = grid % 8 == 0 ? grid / 8 : 0;
+  p.ng_magic = l.ng_magic;
   const size_t lds = mfma_stream_lds_bytes<G, MT>(l.K / G, kStreamWaves);
   if (l.stream_pieces) {
-    hipLaunchKernelGGL((w4a16_gemm_mfma_stream_kernel<G, A, F, kStreamWaves, D, MT, true>),
-                       dim3(grid), dim3(64 * (kStreamWaves + 1)), lds, stream, p);
-  } else {
-    hipLaunchKernelGGL((w4a16_gemm_mfma_stream_kernel<G, A, F, kStreamWaves, D, MT, false>),
-                       dim3(grid), dim3(64 * kStreamWaves), lds, stream, p);
+    // (over the reference packets the pieces' registers spill: whole slices only)
+    if constexpr (F != PacketFormat::kArc) {
+      hipLaunchKernelGGL((w4a16_gemm_mfma_stream_kernel<G, A, F, kStreamWaves, D, MT, true>),
+                         dim3(grid), dim3(64 * (kStreamWaves + 1)), lds, stream, p);
+      return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
   }
+  hipLaunchKernelGGL((w4a16_gemm_mfma_stream_kernel<G, A, F, kStreamWaves, D, MT, false>),
+                     dim3(grid), dim3(64 * kStreamWaves), lds, stream, p);
   return hipGetLastError();
 }
 
@@ -516,6 +588,10 @@ hipError_t launch_w4a16_gemm_mfma_stream(const GemvLaunch& l, hipStream_t stream
     return hipErrorInvalidValue;
   }
   const long long slices = l.N / kSliceCols;
+  if (l.format == PacketFormat::kArc &&
+      (l.ng_magic != arc_quarter_magic(ng) || !arc_quarter_magic_exact(ng, slices))) {
+    return hipErrorInvalidValue;
+  }
   if (l.stream_pieces) {
     const long long left = slices - static_cast<long long>(l.stream_grid) * l.stream_whole;
     if (l.counters == nullptr || l.partials == nullptr || slices > kStreamMaxSlices ||
@@ -531,6 +607,7 @@ hipError_t launch_w4a16_gemm_mfma_stream(const GemvLaunch& l, hipStream_t stream
   switch (l.format) {
     case PacketFormat::kNativeSym: return mfma_stream_dispatch<PacketFormat::kNativeSym>(l, stream);
     case PacketFormat::kNativeAsym: return mfma_stream_dispatch<PacketFormat::kNativeAsym>(l, stream);
+    case PacketFormat::kArc: return mfma_stream_dispatch<PacketFormat::kArc>(l, stream);
     default: return hipErrorInvalidValue;
   }
 }

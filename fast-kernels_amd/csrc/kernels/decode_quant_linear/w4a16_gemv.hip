@@ -22,6 +22,9 @@ int gemv_partials_m_tile_for_batch(int batch) {
 }
 
 hipError_t launch_w4a16_gemv(const GemvLaunch& l, hipStream_t stream) {
+  if (l.stream && l.m_tile == kMfmaRows) {
+    return launch_w4a16_gemm_mfma_stream(l, stream);
+  }
   if (l.stream && l.format == PacketFormat::kArc) {
     return l.slice_cols == kSliceCols || l.slice_cols == kSliceCols / 2
                ? launch_w4a16_gemv_arc_quarter(l, stream)

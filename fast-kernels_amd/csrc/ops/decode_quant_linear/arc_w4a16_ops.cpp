@@ -218,6 +218,8 @@ bool arc_stream_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_size
                      int split_k_slices, int cu_count, bool cu_count_given);
 bool arc_quarter_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_size,
                       int split_k_slices, int cu_count, bool cu_count_given);
+bool arc_mfma_stream_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_size,
+                          int split_k_slices, int cu_count, bool cu_count_given);
 
 }  // namespace
 
@@ -226,7 +228,8 @@ ArcW4A16Plan plan_arc_w4a16_for_cu_count(int batch, int n, int k, int group_size
   validate_dimensions(batch, n, k, group_size);
   ArcW4A16Plan plan = plan_arc_impl(batch, n, k, group_size, activation_dtype, split_k_slices,
                                     cu_count, fk::gemv_m_tile_for_batch(batch));
-  if (!arc_stream_plan(plan, batch, n, k, group_size, split_k_slices, cu_count, true)) {
+  if (!arc_mfma_stream_plan(plan, batch, n, k, group_size, split_k_slices, cu_count, true) &&
+      !arc_stream_plan(plan, batch, n, k, group_size, split_k_slices, cu_count, true)) {
     arc_quarter_plan(plan, batch, n, k, group_size, split_k_slices, cu_count, true);
   }
   return plan;
@@ -448,6 +451,13 @@ bool arc_quarter_enabled() {
   return enabled;
 }
 
+// FK_W4A16_ARC_MFMA_STREAM=0 keeps 2-16-row launches over the reference packets off the
+// matrix-core stream kernel.
+bool arc_mfma_stream_enabled() {
+  static const bool enabled = env_enabled("FK_W4A16_ARC_MFMA_STREAM");
+  return enabled;
+}
+
 // FK_W4A16_ARC_EIGHTHS=0 keeps the quarter schedule over reference packets off 16-column units.
 bool arc_eighths_enabled() {
   static const bool enabled = env_enabled("FK_W4A16_ARC_EIGHTHS");
@@ -593,6 +603,81 @@ bool fused_stream_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_si
   return true;
 }
 
+// The matrix cores on the stream schedule (w4a16_gemm_mfma_stream.hip) for 2-16 rows: the rows
+// staged whole in LDS, one workgroup per CU streaming whole 32-column slices of native slabs, or
+// (arc) 32-column quarters of the reference packets. False (plan unchanged) when the shape does
+// not fit. Measured on MI355X (benchmark configuration 3, 14336 x 4096, G = 64, asymmetric, fp16:
+// 448 slices, two per workgroup on a divisor grid of 224 CUs; alternating runs on one GPU against
+// the plans without it): 2 rows 9.8 -> 8.6 us, 4 rows 10.9 -> 8.6, 8 rows 12.5 -> 10.0, 16 rows
+// 13.0 -> 11.4. With pieces of the slices left over (256 CUs, a block of 32 groups the unit, so
+// ranges of 1 or 2 blocks) the same shape took 11.0 us at 4 rows and 12.6 at 8, and two and
+// sixteen rows were slower than without the stream schedule: pieces only for 3-8 rows.
+bool mfma_stream_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_size, bool arc,
+                      int cu_count, bool cu_count_given) {
+  const std::size_t lds_limit = cu_count_given ? kGfx950LdsBytes : device_lds_per_block();
+  const int depth = fk::stream_depth_for_kb(group_size, fk::kStreamKB);
+  const int num_groups = k / group_size;
+  const int nbs = num_groups / (fk::kStreamWaves * depth);
+  const long long slices = n / fk::kSliceCols;
+  const long long cus = cu_count;
+  if (num_groups % (fk::kStreamWaves * depth) != 0 || !fk::mfma_stream_fits(group_size, k, batch) ||
+      fk::mfma_stream_lds(group_size, k, batch) > lds_limit || slices > fk::kStreamMaxSlices ||
+      (arc && !fk::arc_quarter_magic_exact(num_groups, slices))) {
+    return false;
+  }
+  const long long left = slices % cus;
+  const long long dgrid = divisor_grid(slices, cus);
+  long long grid = 0;
+  int whole = 0;
+  bool pieces = false;
+  if (slices >= cus && left == 0) {
+    grid = cus;
+    whole = static_cast<int>(slices / cus);
+  } else if (dgrid > 0) {
+    grid = dgrid;
+    whole = static_cast<int>(slices / dgrid);
+  } else if (slices > cus && left * nbs >= cus && batch >= kMfmaPiecesMinBatch &&
+             batch <= kMfmaPiecesMaxBatch && !arc) {
+    // (pieces over the reference packets spill registers: no pieces there)
+    grid = cus;
+    whole = static_cast<int>(slices / cus);
+    pieces = true;
+  } else if (slices < cus && batch >= kMfmaPiecesMinBatch && batch <= kMfmaPiecesMaxBatch) {
+    grid = slices;
+    whole = 1;
+  } else {
+    return false;
+  }
+  plan.m_tile = fk::kMfmaRows;
+  plan.schedule = kScheduleStream;
+  plan.slice_cols = fk::kSliceCols;
+  plan.workgroups = static_cast<int>(grid);
+  plan.stream_depth = depth;
+  plan.stream_whole = whole;
+  plan.stream_pieces = pieces ? 1 : 0;
+  plan.stream_half = 0;
+  const long long left_blocks = (slices - grid * whole) * nbs;
+  const long long piece_blocks = pieces ? (left_blocks + grid - 1) / grid : 0;
+  plan.groups_per_workgroup =
+      static_cast<int>(whole * num_groups + piece_blocks * fk::kStreamWaves * depth);
+  plan.max_tile_contributors =
+      pieces ? static_cast<int>((nbs * grid + left_blocks - 1) / left_blocks + 1) : 1;
+  plan.workspace_bytes =
+      pieces ? kCounterRegionBytes +
+                   fk::stream_partial_floats(static_cast<int>(grid), fk::kMfmaRows) * sizeof(float)
+             : 0;
+  return true;
+}
+
+// The reference-signature plan's matrix-core stream schedule over the reference packets (the
+// automatic kernel choice).
+bool arc_mfma_stream_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_size,
+                          int split_k_slices, int cu_count, bool cu_count_given) {
+  return split_k_slices == 0 && batch >= kMfmaStreamMinBatch && batch <= kMfmaStreamMaxBatch &&
+         mfma_stream_enabled() && arc_mfma_stream_enabled() &&
+         mfma_stream_plan(plan, batch, n, k, group_size, true, cu_count, cu_count_given);
+}
+
 // plan_w4a16_for_format for a kernel choice (kKernelDot2 is what the fused kernels need).
 ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int activation_dtype,
                                   int split_k_slices, int cu_count, int packet_format,
@@ -605,68 +690,12 @@ ArcW4A16Plan plan_for_format_impl(int batch, int n, int k, int group_size, int a
   }
   ArcW4A16Plan plan = plan_arc_impl(batch, n, k, group_size, activation_dtype, split_k_slices,
                                     cu_count, m_tile_for_kernel(batch, kernel));
-  if (format != fk::PacketFormat::kArc && plain && split_k_slices == 0 &&
-      batch >= kMfmaStreamMinBatch && batch <= kMfmaStreamMaxBatch && kernel != kKernelDot2 &&
-      mfma_stream_enabled()) {
-    // The matrix cores on the stream schedule (w4a16_gemm_mfma_stream.hip): the rows staged whole
-    // in LDS, one workgroup per CU streaming whole slices. Measured on MI355X (benchmark
-    // configuration 3, 14336 x 4096, G = 64, asymmetric, fp16: 448 slices, two per workgroup on a
-    // divisor grid of 224 CUs; alternating runs on one GPU against the plans without it): 2 rows
-    // 9.8 -> 8.6 us, 4 rows 10.9 -> 8.6, 8 rows 12.5 -> 10.0, 16 rows 13.0 -> 11.4. With pieces of
-    // the slices left over (256 CUs, a block of 32 groups the unit, so ranges of 1 or 2 blocks) the
-    // same shape took 11.0 us at 4 rows and 12.6 at 8, and two and sixteen rows were slower than
-    // without the stream schedule: pieces only for 3-8 rows.
-    const std::size_t lds_limit = cu_count_given ? kGfx950LdsBytes : device_lds_per_block();
-    const int depth = fk::stream_depth_for_kb(group_size, fk::kStreamKB);
-    const int num_groups = k / group_size;
-    const int nbs = num_groups / (fk::kStreamWaves * depth);
-    const long long slices = n / fk::kSliceCols;
-    const long long cus = cu_count;
-    if (num_groups % (fk::kStreamWaves * depth) == 0 && fk::mfma_stream_fits(group_size, k, batch) &&
-        fk::mfma_stream_lds(group_size, k, batch) <= lds_limit && slices <= fk::kStreamMaxSlices) {
-      const long long left = slices % cus;
-      const long long dgrid = divisor_grid(slices, cus);
-      long long grid = 0;
-      int whole = 0;
-      bool pieces = false;
-      if (slices >= cus && left == 0) {
-        grid = cus;
-        whole = static_cast<int>(slices / cus);
-      } else if (dgrid > 0) {
-        grid = dgrid;
-        whole = static_cast<int>(slices / dgrid);
-      } else if (slices > cus && left * nbs >= cus && batch >= kMfmaPiecesMinBatch &&
-                 batch <= kMfmaPiecesMaxBatch) {
-        grid = cus;
-        whole = static_cast<int>(slices / cus);
-        pieces = true;
-      } else if (slices < cus && batch >= kMfmaPiecesMinBatch && batch <= kMfmaPiecesMaxBatch) {
-        grid = slices;
-        whole = 1;
-      }
-      if (grid > 0) {
-        plan.m_tile = fk::kMfmaRows;
-        plan.schedule = kScheduleStream;
-        plan.slice_cols = fk::kSliceCols;
-        plan.workgroups = static_cast<int>(grid);
-        plan.stream_depth = depth;
-        plan.stream_whole = whole;
-        plan.stream_pieces = pieces ? 1 : 0;
-        plan.stream_half = 0;
-        const long long left_blocks = (slices - grid * whole) * nbs;
-        const long long piece_blocks = pieces ? (left_blocks + grid - 1) / grid : 0;
-        plan.groups_per_workgroup = static_cast<int>(
-            whole * num_groups + piece_blocks * fk::kStreamWaves * depth);
-        plan.max_tile_contributors =
-            pieces ? static_cast<int>((nbs * grid + left_blocks - 1) / left_blocks + 1) : 1;
-        plan.workspace_bytes =
-            pieces ? kCounterRegionBytes + fk::stream_partial_floats(static_cast<int>(grid),
-                                                                     fk::kMfmaRows) *
-                                               sizeof(float)
-                   : 0;
-        return plan;
-      }
-    }
+  if (plain && split_k_slices == 0 && batch >= kMfmaStreamMinBatch &&
+      batch <= kMfmaStreamMaxBatch && kernel != kKernelDot2 && mfma_stream_enabled() &&
+      (format != fk::PacketFormat::kArc || arc_mfma_stream_enabled()) &&
+      mfma_stream_plan(plan, batch, n, k, group_size, format == fk::PacketFormat::kArc, cu_count,
+                       cu_count_given)) {
+    return plan;
   }
   if (format == fk::PacketFormat::kArc && plain && kernel != kKernelMfma &&
       !arc_stream_plan(plan, batch, n, k, group_size, split_k_slices, cu_count, cu_count_given)) {
@@ -912,6 +941,21 @@ void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::u
     l.slice_cols = fk::kSliceCols;
     l.slice_pair = true;
     l.units_per_workgroup = 2 * plan.groups_per_workgroup;
+  } else if (plan.schedule == kScheduleStream && format == fk::PacketFormat::kArc &&
+             plan.m_tile == fk::kMfmaRows) {
+    // 2-16 rows over the packets' quarters on the matrix-core stream kernel
+    if (batch > fk::kMfmaRows || plan.slice_cols != fk::kSliceCols || plan.stream_half != 0 ||
+        fuse != fk::GemvFuse::kNone) {
+      throw std::logic_error("matrix-core stream schedule on a reference-packet plan it does not take");
+    }
+    l.stream = true;
+    l.slice_cols = fk::kSliceCols;
+    l.ng_magic = fk::arc_quarter_magic(k / group_size);
+    l.stream_waves = fk::kStreamWaves;
+    l.stream_depth = plan.stream_depth;
+    l.stream_grid = plan.workgroups;
+    l.stream_whole = plan.stream_whole;
+    l.stream_pieces = plan.stream_pieces != 0;
   } else if (plan.schedule == kScheduleStream && format == fk::PacketFormat::kArc) {
     if (batch != 1 || plan.m_tile != 1 ||
         (plan.slice_cols != fk::kTileCols && plan.slice_cols != fk::kSliceCols &&

@@ -94,11 +94,16 @@ def test_plan_policy_without_gpu(lib: ctypes.CDLL, shape, want_runs_per_tile, wa
 
 
 def test_plan_batch_tiles_and_forced_split(lib: ctypes.CDLL) -> None:
-    rc, p = _plan(lib, 16, 14336, 4096, 64)
-    assert rc == 0 and p.m_tile == 16  # matrix-core kernel from 8 rows
-    rc, p = _plan(lib, 7, 14336, 4096, 64)
+    # 2-16 rows over the reference packets: the matrix-core stream kernel by packet quarters
+    for batch in (2, 3, 7, 16):
+        rc, p = _plan(lib, batch, 14336, 4096, 64)
+        assert rc == 0 and (p.m_tile, p.schedule, p.slice_cols, p.workgroups) == (16, 2, 32, 224)
+    # with a forced K split the per-tile kernels: matrix cores from 8 rows, dot2 m-tiles below
+    rc, p = _plan(lib, 16, 14336, 4096, 64, split=1)
+    assert rc == 0 and p.m_tile == 16 and p.schedule == 0
+    rc, p = _plan(lib, 7, 14336, 4096, 64, split=1)
     assert rc == 0 and p.m_tile == 8
-    rc, p = _plan(lib, 3, 14336, 4096, 64, act=1)
+    rc, p = _plan(lib, 3, 14336, 4096, 64, act=1, split=1)
     assert rc == 0 and p.m_tile == 4
     # S = 7 slices of a 64-group tile: runs of ceil(64/7) = 10 groups straddle tile boundaries
     rc, p = _plan(lib, 1, 1024, 8192, 128, split=7)
@@ -249,10 +254,12 @@ def test_native_plan_policy_without_gpu(lib: ctypes.CDLL, shape, want) -> None:
     rc, ref = _plan(lib, batch, n, k, g)
     assert rc == 0 and (arc.slice_cols, arc.workgroups) == (ref.slice_cols, ref.workgroups)
     # reference packets, from either planning entry point: per-tile runs, the whole-tile stream
-    # schedule with a whole tile per CU, or (one row, fewer tiles) the quarter schedule
-    assert arc.schedule == ref.schedule
+    # schedule with a whole tile per CU, (one row, fewer tiles) the quarter schedule, or (2-16
+    # rows) the matrix-core stream kernel by packet quarters where the native plan takes it
+    assert arc.schedule == ref.schedule and arc.m_tile == ref.m_tile
     if batch != 1:
-        assert arc.schedule == 0
+        assert arc.schedule == 0 or (arc.m_tile, arc.slice_cols, arc.workgroups) == (
+            16, 32, p.workgroups)
     elif n // 128 >= 256:
         assert (arc.schedule, arc.slice_cols) == (2, 128)
     elif arc.schedule == 2:

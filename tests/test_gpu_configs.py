@@ -348,6 +348,47 @@ def test_mfma_stream_variants(m: int, n: int, k: int, g: int, act: str, asym: bo
 
 
 @pytest.mark.parametrize(
+    "m,n,k,g,act,want",
+    [
+        # m, n, k, G, activation, (workgroups, whole slices each) on 256 CUs
+        (2, 14336, 4096, 64, "f16", (224, 2)),    # configuration 3: 448 quarters on 224 CUs
+        (5, 14336, 4096, 64, "bf16", (224, 2)),   # eight-row staging, bf16
+        (16, 14336, 4096, 64, "f16", (224, 2)),   # sixteen rows
+        (3, 4096, 4096, 128, "bf16", (128, 1)),   # G = 128: fewer quarters than CUs, one each
+        (13, 8192, 4096, 128, "f16", (256, 1)),   # G = 128, sixteen-row staging, an odd batch
+        (8, 16384, 4096, 64, "bf16", (256, 2)),   # two quarters per CU on every CU
+    ],
+)
+def test_reference_packets_mfma_stream(m: int, n: int, k: int, g: int, act: str, want) -> None:
+    """The reference signature (arc_w4a16_forward, arc_w4a16.cu:687-707) at 2-16 rows over the
+    reference packets on the matrix-core stream kernel (w4a16_gemm_mfma_stream.hip, packet
+    quarters as slices, any fp16 beta): both group sizes and dtypes; sampled rows of every output
+    row against the oracle, and identical bits over three calls."""
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the shapes are chosen for 256 CUs")
+    from fast_kernels.ops import arc_w4a16_forward
+
+    case = make_case(m, n, k, g, act=act, asymmetric=True, seed=5 * n + k + g + m)
+    x, q, a, b = _upload(case)
+    packets = pack_arc_w4a16_packets(q, a, b, group_size=g)
+    plan = arc_w4a16_plan(batch=m, n=n, k=k, group_size=g, activation_dtype=x.dtype,
+                          packet_format=0)
+    assert (plan["schedule"], plan["m_tile"], plan["slice_cols"]) == (2, 16, 32), plan
+    assert (plan["workgroups"], plan["groups_per_workgroup"] // (k // g)) == want, plan
+    outs = []
+    for _ in range(3):
+        y = arc_w4a16_forward(x, packets, n=n, k=k, group_size=g)
+        torch.cuda.synchronize()
+        outs.append(_bits(y))
+    rows = _rows(n)
+    _assert_gemv_close(outs[0][:, rows], _oracle_rows(case, rows, act), case,
+                       f"reference packets, matrix-core stream, M={m} {n}x{k} G{g} {act} "
+                       f"plan={plan}")
+    np.testing.assert_array_equal(outs[1], outs[0])
+    np.testing.assert_array_equal(outs[2], outs[0])
+
+
+@pytest.mark.parametrize(
     "n,k,g,act",
     [
         (32768, 4096, 128, "f16"),   # 256 tiles: one whole tile per CU, no pieces
