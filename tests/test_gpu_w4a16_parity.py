@@ -163,12 +163,13 @@ def test_forward_baseline_shapes_match_oracle(shape: tuple[int, int, int, int]) 
         ((2, 1024, 8192, 64), "bf16", True, (128, 8)),     # two rows, 16 runs per tile
         ((3, 1024, 37 * 64, 64), "f16", True, (128, 10)),  # odd group count, runs of 10
         ((2, 2048, 130 * 64, 64), "bf16", False, (128, 9)),  # 130 groups, runs of 9 across chunks
-        ((5, 1024, 4096, 128), "bf16", False, (128, 8)),   # five rows on an 8-row m-tile
+        ((5, 1024, 4096, 128), "bf16", False, (32, 32)),   # five rows: matrix-core stream kernel,
+                                                           # one packet quarter per workgroup
     ],
 )
 def test_forward_column_slices_match_oracle(shape, act, asym, want) -> None:
     """The automatic plan's 64-, 32- and 16-column slices, alone and with K split across
-    workgroups, and its K splits for several rows."""
+    workgroups, its K splits for several rows, and the matrix-core stream kernel at five."""
     batch, n, k, g = shape
     plan = arc_w4a16_plan(batch=batch, n=n, k=k, group_size=g,
                           activation_dtype=torch.float16 if act == "f16" else torch.bfloat16)

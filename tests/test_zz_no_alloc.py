@@ -76,7 +76,7 @@ def _both(lib, shape):
 # (batch, n, k, G, activation, packet format) -- each plan splits slices (a fix-up workspace)
 LARGE = (1, 4096, 14336, 64, "bf16", 1)    # 128 slices, two runs of 112 groups each
 SMALL = (1, 1024, 8192, 64, "f16", 2)      # 32 slices, K split in four, asymmetric slabs
-BATCHED = (8, 8192, 4096, 64, "f16", 0)    # matrix cores over reference packets, 4.5 MB scratch
+BATCHED = (8, 8192, 8192, 64, "f16", 0)    # matrix-core tiles over reference packets, 4.6 MB scratch
 TAIL = (1, 10240, 8192, 128, "bf16", 1)    # stream schedule: a quarter of a left-over slice per CU
 ARC_TAIL = (1, 10240, 8192, 128, "bf16", 0)  # reference packets by 32-column quarters, pieces
 
