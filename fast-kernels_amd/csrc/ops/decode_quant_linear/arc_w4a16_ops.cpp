@@ -642,7 +642,9 @@ bool mfma_stream_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_siz
     grid = cus;
     whole = static_cast<int>(slices / cus);
     pieces = true;
-  } else if (slices < cus && batch >= kMfmaPiecesMinBatch && batch <= kMfmaPiecesMaxBatch) {
+  } else if (slices < cus) {
+    // fewer slices than CUs: one each (4096 x 4096, two rows over reference packets: 7.6 -> 5.25
+    // us at G = 64, 6.9 -> 4.9 at G = 128, against the per-tile kernels)
     grid = slices;
     whole = 1;
   } else {

@@ -68,6 +68,15 @@ SHAPES: list[tuple[str, str, int, int, int, int, str, str]] = [
     ("2", "70B o arc", 1, 8192, 8192, 128, "bf16", "arc"),
     ("2", "70B gate_up arc", 1, 57344, 8192, 128, "bf16", "arc"),
     ("2", "70B down arc", 1, 8192, 28672, 128, "bf16", "arc"),
+    ("3", "M=2 arc", 2, 14336, 4096, 64, "f16", "arc"),
+    ("3", "M=4 arc", 4, 14336, 4096, 64, "f16", "arc"),
+    ("3", "M=8 arc", 8, 14336, 4096, 64, "f16", "arc"),
+    ("3", "M=16 arc", 16, 14336, 4096, 64, "f16", "arc"),
+    # fewer slices than CUs at 2-16 rows (the reference suite's qkv shape)
+    ("-", "4096^2 M=2", 2, 4096, 4096, 64, "f16", "native_asym"),
+    ("-", "4096^2 M=16", 16, 4096, 4096, 64, "f16", "native_asym"),
+    ("-", "4096^2 M=2 arc", 2, 4096, 4096, 64, "f16", "arc"),
+    ("-", "4096^2 M=16 arc", 16, 4096, 4096, 64, "f16", "arc"),
 ]
 
 # Environments (one child process each): name -> variables.
@@ -83,6 +92,8 @@ ENVS: dict[str, dict[str, str]] = {
     "no_mfma_stream": {"FK_W4A16_MFMA_STREAM": "0"},
     "no_arc_quarter": {"FK_W4A16_ARC_QUARTER": "0"},
     "no_arc_stream": {"FK_W4A16_ARC_STREAM": "0"},
+    "no_arc_eighths": {"FK_W4A16_ARC_EIGHTHS": "0"},
+    "no_arc_mfma_stream": {"FK_W4A16_ARC_MFMA_STREAM": "0"},
 }
 SPLITS = (1, 2, 3, 4, 6, 8, 16)
 KERNELS = {"auto": 0, "dot2": 1, "mfma": 2}

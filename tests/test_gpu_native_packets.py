@@ -187,7 +187,8 @@ def test_forward_native_matches_reference_packets(asym, group_size, batch, act) 
         ((2, 2048, 130 * 64, 64), "bf16", False, 32),  # three 64-group chunks, the last of 2 groups
         ((2, 4096, 4096, 64), "f16", True, 32),      # two rows
         ((8, 4096, 4096, 64), "bf16", True, 32),     # eight rows: matrix cores, stream schedule
-        ((16, 4096, 4096, 64), "bf16", True, 128),   # matrix-core tile over four slabs per group
+        ((16, 4096, 4096, 64), "bf16", True, 32),    # sixteen rows: matrix-core stream, 128 slices
+        ((16, 4096, 8192, 64), "bf16", True, 128),   # long K: matrix-core tile over four slabs
         ((5, 4096, 8192, 64), "f16", False, 32),     # staging past the registers: dot2 runs
     ],
 )

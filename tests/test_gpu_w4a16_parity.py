@@ -159,7 +159,7 @@ def test_forward_baseline_shapes_match_oracle(shape: tuple[int, int, int, int]) 
         ((1, 1024, 2048, 128), "f16", False, (16, 16)),    # 8 tiles -> 64 16-column eighths
         ((1, 10240, 4096, 128), "f16", True, (64, 32)),    # 80 tiles -> 160 64-column slices
         ((1, 4096, 14336, 128), "bf16", False, (32, 56)),  # narrow slices + K split (fix-up)
-        ((2, 4096, 4096, 64), "f16", True, (128, 8)),      # two rows: whole tiles, 8 runs per tile
+        ((2, 4096, 4096, 64), "f16", True, (32, 64)),      # two rows: matrix-core stream kernel
         ((2, 1024, 8192, 64), "bf16", True, (128, 8)),     # two rows, 16 runs per tile
         ((3, 1024, 37 * 64, 64), "f16", True, (128, 10)),  # odd group count, runs of 10
         ((2, 2048, 130 * 64, 64), "bf16", False, (128, 9)),  # 130 groups, runs of 9 across chunks
