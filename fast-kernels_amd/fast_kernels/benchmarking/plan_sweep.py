@@ -77,6 +77,14 @@ SHAPES: list[tuple[str, str, int, int, int, int, str, str]] = [
     ("-", "4096^2 M=16", 16, 4096, 4096, 64, "f16", "native_asym"),
     ("-", "4096^2 M=2 arc", 2, 4096, 4096, 64, "f16", "arc"),
     ("-", "4096^2 M=16 arc", 16, 4096, 4096, 64, "f16", "arc"),
+    # long K at 2-8 rows (the reference suite's MLP down shape)
+    ("-", "4096x14336 M=2 arc", 2, 4096, 14336, 64, "f16", "arc"),
+    ("-", "4096x14336 M=4 arc", 4, 4096, 14336, 64, "f16", "arc"),
+    ("-", "4096x14336 M=8 arc", 8, 4096, 14336, 64, "f16", "arc"),
+    ("-", "4096x14336 M=4", 4, 4096, 14336, 64, "f16", "native_asym"),
+    ("-", "70B qkv M=4 arc", 4, 10240, 8192, 128, "bf16", "arc"),
+    ("-", "70B down M=4 arc", 4, 8192, 28672, 128, "bf16", "arc"),
+    ("-", "70B down M=8", 8, 8192, 28672, 128, "bf16", "native_sym"),
 ]
 
 # Environments (one child process each): name -> variables.
