@@ -161,7 +161,7 @@ def test_forward_baseline_shapes_match_oracle(shape: tuple[int, int, int, int]) 
         ((1, 4096, 14336, 128), "bf16", False, (32, 56)),  # narrow slices + K split (fix-up)
         ((2, 4096, 4096, 64), "f16", True, (32, 64)),      # two rows: matrix-core stream kernel
         ((2, 1024, 8192, 64), "bf16", True, (128, 8)),     # two rows, 16 runs per tile
-        ((3, 1024, 37 * 64, 64), "f16", True, (128, 10)),  # odd group count, runs of 10
+        ((3, 1024, 37 * 64, 64), "f16", True, (128, 19)),  # odd group count, runs of 19 and 18
         ((2, 2048, 130 * 64, 64), "bf16", False, (128, 9)),  # 130 groups, runs of 9 across chunks
         ((5, 1024, 4096, 128), "bf16", False, (32, 32)),   # five rows: matrix-core stream kernel,
                                                            # one packet quarter per workgroup
