@@ -141,7 +141,12 @@ class _Shape:
         rotations = max(2, math.ceil(2 * INFINITY_CACHE_BYTES / weight_bytes) + 1)
         stream = torch.cuda.current_stream().cuda_stream
         self.packets = []
-        for _ in range(rotations):
+        native_fmt = self.fmt != FORMATS["arc"]
+        rows, row_bytes = (((n // 32) * ng, packet_stride_bytes(g, fmt)) if native_fmt
+                           else ((n // 128) * ng, stride))
+        # every copy in one allocation, as bench.py places them
+        pool = torch.empty((rotations, rows, row_bytes), device=dev, dtype=torch.uint8)
+        for r in range(rotations):
             q = torch.randint(0, 256, (n, k // 2), device=dev, dtype=torch.uint8, generator=gen)
             alpha = (0.001 + 0.019 * torch.rand((n, ng), device=dev, generator=gen)).to(torch.float16)
             if self.fmt == FORMATS["native_asym"]:
@@ -149,13 +154,13 @@ class _Shape:
                 beta = -(alpha * zp)
             else:
                 beta = -(alpha * 8)
-            pk = torch.empty(((n // 128) * ng, stride), device=dev, dtype=torch.uint8)
+            pk = (torch.empty(((n // 128) * ng, stride), device=dev, dtype=torch.uint8)
+                  if native_fmt else pool[r])
             native.pack_arc_w4a16_packets(q.data_ptr(), alpha.data_ptr(), beta.data_ptr(),
                                           pk.data_ptr(), n, k, g, stride, stream)
-            if self.fmt != FORMATS["arc"]:
+            if native_fmt:
                 arc = pk
-                pk = torch.empty(((n // 32) * ng, packet_stride_bytes(g, fmt)), device=dev,
-                                 dtype=torch.uint8)
+                pk = pool[r]
                 native.convert_arc_to_native_packets(arc.data_ptr(), pk.data_ptr(), n, k, g,
                                                      self.fmt, stream)
                 del arc
