@@ -123,9 +123,10 @@ __device__ __forceinline__ void arc_mfma_load(ArcMfmaLoad<G>& ld, const uint8_t*
 // host keeps launches within it.
 constexpr int max_stage_per_lane(int mt) { return mt; }
 
-template <int G, Act A, PacketFormat F, int kW, int D, int MT, bool kPieces>
+template <int G, Act A, PacketFormat F, int kW, int D, int MT, bool kPieces, bool kParts = false>
 __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     w4a16_gemm_mfma_stream_kernel(GemvParams p) {
+  static_assert(!(kPieces && kParts), "pieces or K parts, not both");
   extern __shared__ uint4 mfma_stream_lds[];
   constexpr int WR = G / 8;
   constexpr int U = native_unit_words(G);
@@ -144,7 +145,18 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   int b = static_cast<int>(blockIdx.x);
   b = p.xcd_remap != 0 ? (b & 7) * p.xcd_remap + (b >> 3) : b;
   const int ng = p.NG;
-  const int nbs = ng / Q;
+  // kParts: workgroup b streams K part `part` (groups g0 .. g0 + ngs - 1 of every slice) of its
+  // slices; the slice groups of one part are grid / parts consecutive workgroups.
+  const int parts = kParts ? p.stream_parts : 1;
+  const int ngs = ng / parts;  // groups staged, and streamed per slice
+  int part = 0;
+  if constexpr (kParts) {
+    const int per_part = grid / parts;
+    part = b / per_part;
+    b -= part * per_part;
+  }
+  const int g0 = part * ngs;
+  const int nbs = ngs / Q;
   const int slices = p.N / kSliceCols;
   const int rows = p.M;  // rows < MT are real, the rest zeros
   const int n_out = rows * kSliceCols;
@@ -154,9 +166,9 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
 
   MfmaStreamLds<G, MT> sm;
   sm.xs = mfma_stream_lds;
-  sm.sums = reinterpret_cast<float2*>(sm.xs + static_cast<size_t>(ng) * WR * MT);
-  sm.scale = reinterpret_cast<float*>(sm.sums + static_cast<size_t>(ng) * MT);
-  sm.red = sm.scale + static_cast<size_t>(ng) * MT;
+  sm.sums = reinterpret_cast<float2*>(sm.xs + static_cast<size_t>(ngs) * WR * MT);
+  sm.scale = reinterpret_cast<float*>(sm.sums + static_cast<size_t>(ngs) * MT);
+  sm.red = sm.scale + static_cast<size_t>(ngs) * MT;
 
   // Adds the waves' partial tiles of output o in wave order.
   auto total = [&](int o) __attribute__((always_inline)) {
@@ -228,8 +240,24 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   // kArc: the slab index slice * NG + group gives the slice by a multiply-high with a reciprocal
   // of NG (exact over the launch's indices, checked by the host), then packet (slice / 4) * NG +
   // group and quarter slice % 4.
+  // kParts: the wave's slab i is group g0 + wave + kW gi of slice whole_slice0 + r (spw slabs of
+  // the wave per slice), uniform 32-bit arithmetic.
+  const int spw = ngs / kW;
   auto load_slab = [&](Load& ld, int i) __attribute__((always_inline)) {
-    if constexpr (kArcPk) {
+    if constexpr (kParts) {
+      const int c = __builtin_amdgcn_readfirstlane(min(i, j_last));
+      const int r = static_cast<int>(static_cast<uint32_t>(c) / static_cast<uint32_t>(spw));
+      const int gi = c - r * spw;
+      const uint32_t sl = static_cast<uint32_t>(rg.whole_slice0 + r);
+      const uint32_t g = static_cast<uint32_t>(g0 + wave + kW * gi);
+      if constexpr (kArcPk) {
+        const uint8_t* pk =
+            p.packets + static_cast<size_t>((sl >> 2) * static_cast<uint32_t>(ng) + g) * stride;
+        arc_mfma_load<G>(ld, pk, static_cast<int>(sl & 3), t, n);
+      } else {
+        native_load<G, F>(ld, p.packets + static_cast<size_t>(sl * ng + g) * stride, lane);
+      }
+    } else if constexpr (kArcPk) {
       const int c = min(i, j_last);
       int off = off_w;
       if constexpr (kPieces) {
@@ -263,7 +291,7 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
   const int gsub = lane / L;
   const int m_l = (lane % L) / WR;
   const int wr = lane % WR;
-  const int g_last = ng / kW - 1;  // the wave's last group index
+  const int g_last = ngs / kW - 1;  // the wave's last group index
   // Group index and row of this lane's unit in pass i (i a compile-time constant). Passes past
   // the wave's last group stage that group again (the same values; the host bounds the passes).
   auto pass_group = [&](int i) __attribute__((always_inline)) {
@@ -278,7 +306,7 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
     // spills raw[] to scratch)
     const int g = wave + kW * pass_group(i);
     const int m = min(pass_row(i), rows - 1);  // rows past the batch: read a real row, stage 0
-    raw[i] = *reinterpret_cast<const uint4*>(p.x + (m * p.K + g * G + wr * 8));
+    raw[i] = *reinterpret_cast<const uint4*>(p.x + (m * p.K + (g0 + g) * G + wr * 8));
   }
   __builtin_amdgcn_sched_barrier(0);
   Load buf[D];
@@ -504,14 +532,35 @@ __global__ void __launch_bounds__(64 * (kW + (kPieces ? 1 : 0)), 1)
       for (int i = 0; i < kPer; ++i) {
         const int o = lane + 64 * i;
         if (o < n_out) {
-          p.out[static_cast<size_t>(o / kSliceCols) * p.N + slice * kSliceCols + o % kSliceCols] =
-              float_to_act_bits<A>(total(o));
+          const size_t at =
+              static_cast<size_t>(o / kSliceCols) * p.N + slice * kSliceCols + o % kSliceCols;
+          if constexpr (kParts) {
+            p.partials[static_cast<size_t>(part) * p.M * p.N + at] = total(o);
+          } else {
+            p.out[at] = float_to_act_bits<A>(total(o));
+          }
         }
       }
     }
     lds_barrier();  // the slot is free again
   }
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+}
+
+// The K parts' partial sums added in part order and rounded once: out[i] = act(sum_p parts[p][i]).
+template <Act A>
+__global__ void __launch_bounds__(256) add_parts_kernel(const float* __restrict__ parts,
+                                                        uint16_t* __restrict__ out, int total,
+                                                        int n_parts) {
+  const int i = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+  if (i >= total) {
+    return;
+  }
+  float v = 0.0f;
+  for (int q = 0; q < n_parts; ++q) {
+    v += parts[static_cast<size_t>(q) * total + i];
+  }
+  out[i] = float_to_act_bits<A>(v);
 }
 
 template <int G, Act A, PacketFormat F, int MT>
@@ -525,7 +574,21 @@ hipError_t launch_mfma_stream_t(const GemvLaunch& l, hipStream_t stream) {
   p.grid = grid;
   p.xcd_remap = grid % 8 == 0 ? grid / 8 : 0;
   p.ng_magic = l.ng_magic;
-  const size_t lds = mfma_stream_lds_bytes<G, MT>(l.K / G, kStreamWaves);
+  p.stream_parts = l.stream_parts;
+  const size_t lds = mfma_stream_lds_bytes<G, MT>(l.K / G / l.stream_parts, kStreamWaves);
+  if (l.stream_parts > 1) {
+    hipLaunchKernelGGL((w4a16_gemm_mfma_stream_kernel<G, A, F, kStreamWaves, D, MT, false, true>),
+                       dim3(grid), dim3(64 * kStreamWaves), lds, stream, p);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) {
+      return err;
+    }
+    const int total = l.M * l.N;
+    hipLaunchKernelGGL(add_parts_kernel<A>, dim3((total + 255) / 256), dim3(256), 0, stream,
+                       static_cast<const float*>(l.partials), static_cast<uint16_t*>(l.out), total,
+                       l.stream_parts);
+    return hipGetLastError();
+  }
   if (l.stream_pieces) {
     // (over the reference packets the pieces' registers spill: whole slices only)
     if constexpr (F != PacketFormat::kArc) {
@@ -578,7 +641,8 @@ bool mfma_stream_fits(int group_size, int k, int batch) {
 hipError_t launch_w4a16_gemm_mfma_stream(const GemvLaunch& l, hipStream_t stream) {
   if (l.mode != GemvMode::kStreamK || !l.stream || l.m_tile != kMfmaRows || l.M < 1 ||
       l.M > kMfmaRows || l.fuse != GemvFuse::kNone || l.slice_cols != kSliceCols ||
-      l.stream_half || l.stream_grid <= 0 || !mfma_stream_fits(l.group_size, l.K, l.M)) {
+      l.stream_half || l.stream_grid <= 0 || l.stream_parts < 1 ||
+      (l.stream_parts == 1 && !mfma_stream_fits(l.group_size, l.K, l.M))) {
     return hipErrorInvalidValue;
   }
   const int ng = l.K / l.group_size;
@@ -588,6 +652,27 @@ hipError_t launch_w4a16_gemm_mfma_stream(const GemvLaunch& l, hipStream_t stream
     return hipErrorInvalidValue;
   }
   const long long slices = l.N / kSliceCols;
+  if (l.stream_parts > 1) {
+    // K parts: whole blocks per part, the part's rows fit the staging, every part has the same
+    // slice groups, and the partials [parts, M, N] in the workspace
+    const int ngs = ng / l.stream_parts;
+    if (l.stream_pieces || ng % l.stream_parts != 0 || ngs % quantum != 0 ||
+        !mfma_stream_fits(l.group_size, ngs * l.group_size, l.M) ||
+        l.stream_grid % l.stream_parts != 0 || l.stream_whole <= 0 ||
+        static_cast<long long>(l.stream_grid / l.stream_parts) * l.stream_whole != slices ||
+        l.partials == nullptr || static_cast<long long>(l.M) * l.N >= (1LL << 31)) {
+      return hipErrorInvalidValue;
+    }
+    switch (l.format) {
+      case PacketFormat::kNativeSym: return mfma_stream_dispatch<PacketFormat::kNativeSym>(l, stream);
+      case PacketFormat::kNativeAsym: return mfma_stream_dispatch<PacketFormat::kNativeAsym>(l, stream);
+      case PacketFormat::kArc: return mfma_stream_dispatch<PacketFormat::kArc>(l, stream);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  if (l.stream_parts != 1) {
+    return hipErrorInvalidValue;
+  }
   if (l.format == PacketFormat::kArc &&
       (l.ng_magic != arc_quarter_magic(ng) || !arc_quarter_magic_exact(ng, slices))) {
     return hipErrorInvalidValue;

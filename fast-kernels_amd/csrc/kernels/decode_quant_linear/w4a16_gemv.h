@@ -63,6 +63,11 @@ struct GemvLaunch {
   // floor(2^32 / (K/G)) + 1, the reciprocal that turns a unit's linear (unit, group) index into
   // its unit.
   uint32_t ng_magic = 0;
+  // Matrix-core stream kernel (m_tile == kMfmaRows), no pieces: K split into stream_parts equal
+  // parts. Workgroup b takes part b / (stream_grid / stream_parts) of stream_whole slices, stages
+  // only that part's activations and writes fp32 partial sums ([parts, M, N] in `partials`),
+  // which a second launch adds in part order.
+  int stream_parts = 1;
 };
 
 // Longest K the stream schedule stages (its LDS holds the whole activation row).

@@ -115,6 +115,7 @@ struct GemvParams {
   int pair;                         // native slabs: each run streams two adjacent whole slices
   int stream_whole;                 // stream schedule: whole slices per workgroup
   uint32_t ng_magic;                // quarter schedule over reference packets: floor(2^32/NG) + 1
+  int stream_parts;                 // matrix-core stream kernel: K in this many parts (1: whole)
 };
 
 template <int G, int MT, int CW>

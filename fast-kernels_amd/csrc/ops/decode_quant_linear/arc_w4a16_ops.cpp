@@ -616,6 +616,60 @@ bool fused_stream_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_si
 // 13.0 -> 11.4. With pieces of the slices left over (256 CUs, a block of 32 groups the unit, so
 // ranges of 1 or 2 blocks) the same shape took 11.0 us at 4 rows and 12.6 at 8, and two and
 // sixteen rows were slower than without the stream schedule: pieces only for 3-8 rows.
+// K too long to stage whole rows: K in the fewest equal parts whose rows fit the staging, each
+// workgroup streaming whole slices over one part (the slices in groups of `whole`, every part with
+// the same groups), over a grid of 7/8 of the CUs or more; the parts' fp32 sums go to the
+// workspace and a second launch adds them in part order. Within kMaxPartsBytes of partials, from
+// kMfmaPartsMinBatch rows. Measured on MI355X (plan sweep, against the best per-tile plan): 4096 x
+// 14336 G64 at 4 rows 14.8 -> 12.9 us (reference packets) and 13.7 -> 12.6 (native), 70B qkv at
+// 4 rows 18.0 -> 14.7, 70B down at 4 rows 31.1 -> 29.0 and at 8 rows 31.9 -> 29.2; at 8 rows of
+// 4096 x 14336 even (14.2); at 2 rows slower (11.5 -> 12.5 us: the second launch and the parts'
+// slice ends cost more than two rows gain).
+constexpr int kMfmaPartsMinBatch = 3;
+bool mfma_stream_parts_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_size,
+                            int cu_count, std::size_t lds_limit) {
+  constexpr long long kMaxPartsBytes = 6LL << 20;
+  const int depth = fk::stream_depth_for_kb(group_size, fk::kStreamKB);
+  const int num_groups = k / group_size;
+  const int quantum = fk::kStreamWaves * depth;
+  const long long slices = n / fk::kSliceCols;
+  const long long cus = cu_count;
+  for (int parts = 2; parts <= num_groups / quantum; ++parts) {
+    const int ngs = num_groups / parts;
+    if (num_groups % parts != 0 || ngs % quantum != 0 ||
+        !fk::mfma_stream_fits(group_size, ngs * group_size, batch) ||
+        fk::mfma_stream_lds(group_size, ngs * group_size, batch) > lds_limit ||
+        static_cast<long long>(parts) * batch * n * 4 > kMaxPartsBytes) {
+      continue;
+    }
+    // slice groups per part: the most that keep parts x groups within the CUs and at 7/8 or more
+    long long groups = 0;
+    for (long long gs = cus / parts; gs >= 1 && 8 * parts * gs >= 7 * cus; --gs) {
+      if (slices % gs == 0) {
+        groups = gs;
+        break;
+      }
+    }
+    if (groups == 0) {
+      continue;
+    }
+    plan.m_tile = fk::kMfmaRows;
+    plan.schedule = kScheduleStream;
+    plan.slice_cols = fk::kSliceCols;
+    plan.workgroups = static_cast<int>(parts * groups);
+    plan.stream_depth = depth;
+    plan.stream_whole = static_cast<int>(slices / groups);
+    plan.stream_pieces = 0;
+    plan.stream_half = 0;
+    plan.groups_per_workgroup = plan.stream_whole * ngs;
+    plan.max_tile_contributors = parts;
+    plan.workspace_bytes =
+        kCounterRegionBytes + static_cast<std::size_t>(parts) * batch * n * sizeof(float);
+    return true;
+  }
+  return false;
+}
+
 bool mfma_stream_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_size, bool arc,
                       int cu_count, bool cu_count_given) {
   const std::size_t lds_limit = cu_count_given ? kGfx950LdsBytes : device_lds_per_block();
@@ -624,9 +678,15 @@ bool mfma_stream_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_siz
   const int nbs = num_groups / (fk::kStreamWaves * depth);
   const long long slices = n / fk::kSliceCols;
   const long long cus = cu_count;
-  if (num_groups % (fk::kStreamWaves * depth) != 0 || !fk::mfma_stream_fits(group_size, k, batch) ||
-      fk::mfma_stream_lds(group_size, k, batch) > lds_limit || slices > fk::kStreamMaxSlices ||
-      (arc && !fk::arc_quarter_magic_exact(num_groups, slices))) {
+  if (num_groups % (fk::kStreamWaves * depth) != 0 || slices > fk::kStreamMaxSlices) {
+    return false;
+  }
+  if (!fk::mfma_stream_fits(group_size, k, batch) ||
+      fk::mfma_stream_lds(group_size, k, batch) > lds_limit) {
+    return batch >= kMfmaPartsMinBatch &&
+           mfma_stream_parts_plan(plan, batch, n, k, group_size, cu_count, lds_limit);
+  }
+  if (arc && !fk::arc_quarter_magic_exact(num_groups, slices)) {
     return false;
   }
   const long long left = slices % cus;
@@ -964,6 +1024,7 @@ void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::u
     l.stream_grid = plan.workgroups;
     l.stream_whole = plan.stream_whole;
     l.stream_pieces = plan.stream_pieces != 0;
+    l.stream_parts = plan.stream_pieces != 0 ? 1 : plan.max_tile_contributors;
   } else if (plan.schedule == kScheduleStream && format == fk::PacketFormat::kArc) {
     if (batch != 1 || plan.m_tile != 1 ||
         (plan.slice_cols != fk::kTileCols && plan.slice_cols != fk::kSliceCols &&
@@ -993,6 +1054,9 @@ void run_gemv(std::uintptr_t activations_ptr, std::uintptr_t packets_ptr, std::u
     l.stream_whole = plan.stream_whole;
     l.stream_pieces = plan.stream_pieces != 0;
     l.stream_half = plan.stream_half != 0;
+    if (plan.m_tile == fk::kMfmaRows && plan.stream_pieces == 0) {
+      l.stream_parts = plan.max_tile_contributors;
+    }
   }
   l.format = format;
   l.fuse = fuse;

@@ -389,6 +389,55 @@ def test_reference_packets_mfma_stream(m: int, n: int, k: int, g: int, act: str,
 
 
 @pytest.mark.parametrize(
+    "m,n,k,g,act,packets,parts",
+    [
+        (3, 4096, 14336, 64, "f16", "arc", 7),            # the MLP down shape: 7 parts of 32 groups
+        (4, 4096, 14336, 64, "bf16", "native_asym", 7),
+        (16, 4096, 14336, 64, "f16", "arc", 7),
+        (5, 10240, 8192, 128, "f16", "arc", 4),           # 70B qkv: 4 parts of 16 groups, 5 slices
+        (3, 8192, 8192, 128, "bf16", "arc", 2),           # 70B o: 2 parts, two slices per workgroup
+        (8, 8192, 28672, 128, "bf16", "native_sym", 7),   # 70B down, 8 rows
+    ],
+)
+def test_mfma_stream_k_parts(m: int, n: int, k: int, g: int, act: str, packets: str,
+                             parts: int) -> None:
+    """The matrix-core stream kernel with K in parts (rows too long to stage whole): each
+    workgroup stages one part of K and streams whole slices over it, the parts' fp32 sums added in
+    part order by a second launch. Both formats and dtypes, 2-16 rows; sampled rows against the
+    oracle and identical bits over three calls."""
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the shapes are chosen for 256 CUs")
+    from fast_kernels.ops import arc_w4a16_forward
+
+    asym = packets != "native_sym"
+    case = make_case(m, n, k, g, act=act, asymmetric=asym, seed=7 * n + k + g + m)
+    x, q, a, b = _upload(case)
+    arc = pack_arc_w4a16_packets(q, a, b, group_size=g)
+    code = {"arc": 0, "native_sym": 1, "native_asym": 2}[packets]
+    weights = arc if code == 0 else convert_arc_to_native_packets(arc, n=n, k=k, group_size=g,
+                                                                  packet_format=packets)
+    plan = arc_w4a16_plan(batch=m, n=n, k=k, group_size=g, activation_dtype=x.dtype,
+                          packet_format=code)
+    assert (plan["schedule"], plan["m_tile"], plan["max_tile_contributors"]) == (2, 16, parts), plan
+
+    def run():
+        if code == 0:
+            y = arc_w4a16_forward(x, weights, n=n, k=k, group_size=g)
+        else:
+            y = arc_w4a16_forward_native(x, weights, n=n, k=k, group_size=g, packet_format=packets)
+        torch.cuda.synchronize()
+        return _bits(y)
+
+    outs = [run() for _ in range(3)]
+    rows = _rows(n)
+    _assert_gemv_close(outs[0][:, rows], _oracle_rows(case, rows, act), case,
+                       f"matrix-core stream, {parts} K parts, M={m} {n}x{k} G{g} {act} {packets} "
+                       f"plan={plan}")
+    np.testing.assert_array_equal(outs[1], outs[0])
+    np.testing.assert_array_equal(outs[2], outs[0])
+
+
+@pytest.mark.parametrize(
     "n,k,g,act",
     [
         (32768, 4096, 128, "f16"),   # 256 tiles: one whole tile per CU, no pieces

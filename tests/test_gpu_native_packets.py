@@ -188,7 +188,8 @@ def test_forward_native_matches_reference_packets(asym, group_size, batch, act) 
         ((2, 4096, 4096, 64), "f16", True, 32),      # two rows
         ((8, 4096, 4096, 64), "bf16", True, 32),     # eight rows: matrix cores, stream schedule
         ((16, 4096, 4096, 64), "bf16", True, 32),    # sixteen rows: matrix-core stream, 128 slices
-        ((16, 4096, 8192, 64), "bf16", True, 128),   # long K: matrix-core tile over four slabs
+        ((16, 4096, 8192, 64), "bf16", True, 32),    # long K: matrix-core stream, K in 2 parts
+        ((16, 4096, 32768, 128), "f16", False, 32),   # K in 8 parts of 32 groups
         ((5, 4096, 8192, 64), "f16", False, 32),     # staging past the registers: dot2 runs
     ],
 )
