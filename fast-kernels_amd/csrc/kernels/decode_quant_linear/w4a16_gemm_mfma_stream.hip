@@ -30,6 +30,10 @@
 //    for window j, the 8 bytes of columns 32 q + 2 n and + 1 in word row 4 j + t (four 128-byte
 //    runs per load) and those columns' alphas and betas; the two chains are the two columns, A
 //    the staged k-chunk 4 j + t, and the epilogue y += alpha D + beta S with the packet's betas.
+//  * kParts (rows too long to stage whole): K in stream_parts equal parts; workgroup b takes part
+//    b / (grid / parts) of its whole slices, stages only that part's activations, and writes its
+//    fp32 partial tiles to partials [parts, M, N]; add_parts_kernel then adds the parts in part
+//    order and rounds once (no counters, no hand-off).
 #include "w4a16_gemv_native.h"
 #include "w4a16_stream_common.h"
 
