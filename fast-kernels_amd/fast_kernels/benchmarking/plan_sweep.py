@@ -85,6 +85,14 @@ SHAPES: list[tuple[str, str, int, int, int, int, str, str]] = [
     ("-", "70B qkv M=4 arc", 4, 10240, 8192, 128, "bf16", "arc"),
     ("-", "70B down M=4 arc", 4, 8192, 28672, 128, "bf16", "arc"),
     ("-", "70B down M=8", 8, 8192, 28672, 128, "bf16", "native_sym"),
+    # one row at G = 64 (the reference suite's shapes)
+    ("-", "14336x4096 G64 arc", 1, 14336, 4096, 64, "f16", "arc"),
+    ("-", "14336x4096 G64", 1, 14336, 4096, 64, "f16", "native_asym"),
+    ("-", "4096x14336 G64 arc", 1, 4096, 14336, 64, "f16", "arc"),
+    ("-", "4096^2 G64 arc", 1, 4096, 4096, 64, "f16", "arc"),
+    # a divisor grid or pieces (896 slices, K/G = 64)
+    ("-", "28672x8192 arc", 1, 28672, 8192, 128, "bf16", "arc"),
+    ("-", "28672x8192", 1, 28672, 8192, 128, "bf16", "native_sym"),
 ]
 
 # Environments (one child process each): name -> variables.
