@@ -511,7 +511,11 @@ bool arc_quarter_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_siz
     grid = cus;
     whole = static_cast<int>(slices / cus);
   } else if (const long long dgrid = divisor_grid(slices, cus); dgrid > 0) {
-    // ahead of pieces, as on native slabs (14336 x 4096 G64: 10.4 us with pieces)
+    // ahead of pieces, as on native slabs; at G = 64 the per-tile runs are faster still
+    // (14336 x 4096 G64: pieces 10.4 us, quarters on 224 CUs 7.6, 64-column runs on 224 7.2)
+    if (group_size != 128) {
+      return false;
+    }
     grid = dgrid;
     whole = static_cast<int>(slices / dgrid);
   } else if (slices > cus && left * nbs >= cus && num_groups >= kMinPieceGroups &&

@@ -94,6 +94,14 @@ SHAPES: list[tuple[str, str, int, int, int, int, str, str]] = [
     ("-", "28672x8192 arc", 1, 28672, 8192, 128, "bf16", "arc"),
     ("-", "28672x8192", 1, 28672, 8192, 128, "bf16", "native_sym"),
 ]
+# the reference's own suite (benchmarks/suites/decode_linear_w4a16.toml): its shapes over the
+# reference packets at 1-8 rows, both group sizes, fp16
+SHAPES += [
+    ("suite", f"ref {n}x{k} G{g} M={m}", m, n, k, g, "f16", "arc")
+    for g in (64, 128)
+    for n, k in ((4096, 4096), (14336, 4096), (4096, 14336))
+    for m in (1, 2, 4, 8)
+]
 
 # Environments (one child process each): name -> variables.
 ENVS: dict[str, dict[str, str]] = {
