@@ -511,9 +511,11 @@ bool arc_quarter_plan(ArcW4A16Plan& plan, int batch, int n, int k, int group_siz
     grid = cus;
     whole = static_cast<int>(slices / cus);
   } else if (const long long dgrid = divisor_grid(slices, cus); dgrid > 0) {
-    // ahead of pieces, as on native slabs; at G = 64 the per-tile runs are faster still
-    // (14336 x 4096 G64: pieces 10.4 us, quarters on 224 CUs 7.6, 64-column runs on 224 7.2)
-    if (group_size != 128) {
+    // ahead of pieces, as on native slabs; the per-tile runs are faster still at G = 64
+    // (14336 x 4096 G64: pieces 10.4 us, quarters on 224 CUs 7.6, 64-column runs on 224 7.2) and
+    // where the whole tiles alone fill 7/8 of the CUs (28672 x 4096, 224 tiles: 11.96 against
+    // 11.68 us; 28672 x 8192: 21.6 against 21.3)
+    if (group_size != 128 || 8 * (slices / 4) >= 7 * cus) {
       return false;
     }
     grid = dgrid;

@@ -68,6 +68,10 @@ SHAPES: list[tuple[str, str, int, int, int, int, str, str]] = [
     ("2", "70B o arc", 1, 8192, 8192, 128, "bf16", "arc"),
     ("2", "70B gate_up arc", 1, 57344, 8192, 128, "bf16", "arc"),
     ("2", "70B down arc", 1, 8192, 28672, 128, "bf16", "arc"),
+    ("4", "8B qkv arc", 1, 6144, 4096, 128, "bf16", "arc"),
+    ("4", "8B o arc", 1, 4096, 4096, 128, "bf16", "arc"),
+    ("4", "8B gate_up arc", 1, 28672, 4096, 128, "bf16", "arc"),
+    ("4", "8B down arc", 1, 4096, 14336, 128, "bf16", "arc"),
     ("3", "M=2 arc", 2, 14336, 4096, 64, "f16", "arc"),
     ("3", "M=4 arc", 4, 14336, 4096, 64, "f16", "arc"),
     ("3", "M=8 arc", 8, 14336, 4096, 64, "f16", "arc"),

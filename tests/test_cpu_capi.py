@@ -392,7 +392,7 @@ def test_reference_packet_stream_plan_without_gpu(lib: ctypes.CDLL, n, k, g, gri
     "n,k,g,want",
     [
         # (unit columns, workgroups, groups per workgroup, fix-up workspace) on 256 CUs
-        ((28672), 8192, 128, (32, 224, 4 * 64, False)),      # 896 slices: 4 each on 224 CUs
+        ((14336), 8192, 128, (32, 224, 2 * 64, False)),      # 448 slices: 2 each on 224 CUs
         ((12288), 8192, 128, (32, 256, 64 + 32, True)),       # 384 slices: 1 whole + pieces
         (10240, 8192, 128, (32, 256, 64 + 16, True)),          # 70B qkv: a slice and a block
         (8192, 8192, 128, (32, 256, 64, False)),               # 70B o
