@@ -417,3 +417,38 @@ def test_reference_packet_quarter_plan_without_gpu(lib: ctypes.CDLL, n, k, g, wa
         assert p.workspace_bytes == 65536 + p.workgroups * 2 * 32 * 4
     rc, p = _plan(lib, 1, 57344, 8192, 128)
     assert rc == 0 and (p.schedule, p.slice_cols) == (2, 128)
+
+
+def test_matrix_core_stream_k_parts_plans_are_consistent(lib: ctypes.CDLL) -> None:
+    """Every matrix-core stream plan with K in parts (2-16 rows, rows too long to stage whole):
+    the parts divide K/G into whole blocks (8 waves x 2 or 4 groups), every part has the same
+    slice groups (workgroups = parts x groups, groups x whole slices = N / 32), the grid keeps to
+    7/8 of the CUs or more, and the workspace holds the counters region and [parts, M, N] fp32
+    partials within 6 MB; the same plan for both formats at one shape."""
+    seen = 0
+    for g in (64, 128):
+        quantum = 8 * (4 if g == 64 else 2)
+        for batch in (3, 4, 8, 13, 16):
+            for n in (2048, 4096, 8192, 10240, 14336, 28672):
+                for k in (8192, 11008 // 128 * 128, 14336, 28672):
+                    if k % g:
+                        continue
+                    for cu in (224, 256, 304):
+                        for fmt in (0, 2):
+                            p = Plan()
+                            assert lib.fk_w4a16_plan_for_format(batch, n, k, g, 0, 0, cu, fmt,
+                                                                ctypes.byref(p)) == 0
+                            if not (p.m_tile == 16 and p.schedule == 2 and
+                                    p.max_tile_contributors > 1):
+                                continue
+                            seen += 1
+                            parts, ng, slices = p.max_tile_contributors, k // g, n // 32
+                            assert ng % parts == 0 and (ng // parts) % quantum == 0, (batch, n, k, g)
+                            assert p.workgroups % parts == 0
+                            groups = p.workgroups // parts
+                            whole = p.groups_per_workgroup // (ng // parts)
+                            assert groups * whole == slices, (batch, n, k, g, cu, p.workgroups)
+                            assert 8 * p.workgroups >= 7 * cu and p.workgroups <= cu
+                            assert p.workspace_bytes == 65536 + parts * batch * n * 4
+                            assert parts * batch * n * 4 <= 6 << 20
+    assert seen > 50
