@@ -105,9 +105,10 @@ typedef struct fk_arc_w4a16_plan {
   int m_tile;                /* activation rows per 128-column tile */
   int workgroups;            /* grid size */
   int groups_per_workgroup;  /* run of (tile, group) units each workgroup streams */
-  int max_tile_contributors; /* workgroups that can share one slice (1 = none shared) */
+  int max_tile_contributors; /* workgroups that can share one slice (1 = none shared); on the
+                                matrix-core stream schedule (m_tile 16, no pieces) the K parts */
   size_t workspace_bytes;    /* workspace fk_arc_w4a16_forward_ex needs */
-  int slice_cols;            /* columns of a tile per workgroup slice: 128, 64, 32 or 16 */
+  int slice_cols;            /* columns per workgroup unit: 128, 64, 32 or 16 */
   int schedule;              /* FK_SCHEDULE_*: how the workgroups walk their units */
 } fk_arc_w4a16_plan;
 
@@ -118,7 +119,11 @@ typedef struct fk_arc_w4a16_plan {
  * whole slices as one contiguous range across slice boundaries, plus, when the slices do not
  * divide over the CUs, one piece of a left-over slice (groups_per_workgroup is then not a
  * multiple of K/G; the pieces are finished through the workspace). With at most half as many
- * 32-column slices as CUs (G = 128) a workgroup streams half a slice (slice_cols 16). */
+ * 32-column slices as CUs (G = 128) a workgroup streams half a slice (slice_cols 16). The same
+ * schedule serves one row over reference packets (whole 128-column tiles, 32-column packet
+ * quarters or 16-column eighths) and 2-16 rows on the matrix cores (m_tile 16, native slabs or
+ * packet quarters; K in max_tile_contributors parts when rows are too long to stage whole, the
+ * parts' fp32 sums then added by a second launch). */
 #define FK_SCHEDULE_RUNS 0
 #define FK_SCHEDULE_PAIRS 1
 #define FK_SCHEDULE_STREAM 2
