@@ -12,7 +12,8 @@ that were summed (fp32 accumulation of products of exact fp16 values stays near 
 Activations are N(0, 1) scaled by powers of two from 2^-40 to 2^40 (within each dtype's range),
 and "mixed": |x| = 2^u, u uniform over 30 binades, random signs, so that one group holds values
 2^30 apart. Every packet format (reference packets, native symmetric and asymmetric slabs) and
-both kernels (the dot2 loop at 1 and 4 rows, the matrix cores at 16) are run.
+both kernels (the dot2 loop at 1 and 4 rows, the matrix cores at 16) are run, and the stream
+schedules of larger shapes (packet eighths, the matrix cores over packet quarters, K in parts).
 """
 
 from __future__ import annotations
@@ -127,4 +128,45 @@ def test_error_relative_to_term_magnitudes(act, scale, group_size, fmt, kernel, 
         f"{act} x~{scale} G={group_size} fmt={fmt} kernel={kernel} M={batch}: "
         f"err {err[worst]:.4g} > bound {bound[worst]:.4g} at {worst} (ref {ref[worst]:.4g}, "
         f"sum|Wx| {mag[worst]:.4g}); max err/sum|Wx| = {rel:.3g}"
+    )
+
+
+# The stream schedules added for the reference packets and for long K, under the same bar:
+# (batch, n, k, group size, packet format, (m_tile, slice_cols, K parts) of the automatic plan).
+STREAM_CASES = [
+    (1, 4096, 4096, 128, 0, (1, 16, 1)),   # one row by 16-column packet eighths
+    (8, 4096, 4096, 64, 0, (16, 32, 1)),   # matrix cores over packet quarters, whole rows staged
+    (4, 2048, 16384, 64, 0, (16, 32, 4)),  # the same with K in four parts
+    (4, 2048, 16384, 64, 2, (16, 32, 4)),  # K in parts over native asymmetric slabs
+]
+
+
+@pytest.mark.parametrize("batch,n,k,group_size,fmt,want", STREAM_CASES)
+@pytest.mark.parametrize("act,scale", [("f16", "2^-20"), ("f16", "mixed"), ("bf16", "2^-40"),
+                                       ("bf16", "2^40"), ("bf16", "mixed")])
+def test_stream_schedules_error_relative_to_term_magnitudes(act, scale, batch, n, k, group_size,
+                                                            fmt, want) -> None:
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the plans are chosen for 256 CUs")
+    case = make_case(batch, n, k, group_size, act=act, asymmetric=(fmt != 1),
+                     seed=2000 + 7 * group_size + fmt + batch)
+    case.x[:] = _scaled_x(case, scale)
+    plan = arc_w4a16_plan(batch=batch, n=n, k=k, group_size=group_size,
+                          activation_dtype=torch.float16 if act == "f16" else torch.bfloat16,
+                          packet_format=fmt)
+    assert plan["schedule"] == 2, plan
+    assert (plan["m_tile"], plan["slice_cols"], plan["max_tile_contributors"]) == want, plan
+    y_bits = _run(case, fmt, 0)
+    ref_bits, _ = oracle.gemv(case.x, case.q_u8, case.alpha, case.beta, group_size, act)
+    to_f32 = f16_bits_to_f32 if act == "f16" else bf16_bits_to_f32
+    y = to_f32(y_bits).astype(np.float64)
+    ref = to_f32(ref_bits).astype(np.float64)
+    mag = np.abs(case.x_f32().astype(np.float64)) @ np.abs(_weights_f64(case)).T
+    assert np.all(np.isfinite(y))
+    err = np.abs(y - ref)
+    bound = _ulp(ref, act) + 1e-3 * mag
+    worst = np.unravel_index(int(np.argmax(err - bound)), err.shape)
+    assert np.all(err <= bound), (
+        f"{act} x~{scale} {n}x{k} G={group_size} fmt={fmt} M={batch} plan={plan}: "
+        f"err {err[worst]:.4g} > bound {bound[worst]:.4g} at {worst} (ref {ref[worst]:.4g})"
     )
