@@ -437,6 +437,52 @@ def test_mfma_stream_k_parts(m: int, n: int, k: int, g: int, act: str, packets: 
     np.testing.assert_array_equal(outs[2], outs[0])
 
 
+def test_small_batch_stream_schedules_graph_replays_match_eager() -> None:
+    """The 2-16-row matrix-core stream launches over the reference packets (whole rows staged,
+    and K in parts: a GEMV launch and the parts' addition) captured in one HIP graph, replayed
+    four times with eager work in between: every replay bit-identical to the eager run."""
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the shapes are chosen for 256 CUs")
+    from fast_kernels.ops import arc_w4a16_forward
+
+    dev = torch.device(DEV)
+    shapes = [(4, 14336, 4096, 64), (8, 4096, 14336, 64), (3, 8192, 28672, 128)]
+    weights, xs, outs = {}, {}, {}
+    for i, (m, n, k, g) in enumerate(shapes):
+        case = make_case(m, n, k, g, act="f16", asymmetric=True, seed=300 + i)
+        x, q, a, b = _upload(case)
+        weights[i] = pack_arc_w4a16_packets(q, a, b, group_size=g)
+        xs[i] = x
+        outs[i] = torch.empty((m, n), device=dev, dtype=torch.float16)
+        plan = arc_w4a16_plan(batch=m, n=n, k=k, group_size=g, activation_dtype=x.dtype,
+                              packet_format=0)
+        assert (plan["schedule"], plan["m_tile"]) == (2, 16), plan
+        assert (plan["max_tile_contributors"] > 1) == (i > 0), plan
+
+    def run() -> None:
+        for i, (m, n, k, g) in enumerate(shapes):
+            arc_w4a16_forward(xs[i], weights[i], n=n, k=k, group_size=g, output=outs[i])
+
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        run()  # the workspace exists before the capture
+    torch.cuda.synchronize()
+    eager = {i: _bits(o) for i, o in outs.items()}
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        run()
+    for replay in range(4):
+        for o in outs.values():
+            o.fill_(float("nan"))
+        scratch = torch.randn(1 << 20, device=dev).sum()  # eager work between the replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        del scratch
+        for i, o in outs.items():
+            np.testing.assert_array_equal(_bits(o), eager[i], err_msg=f"replay {replay} {shapes[i]}")
+
+
 @pytest.mark.parametrize(
     "n,k,g,act",
     [
